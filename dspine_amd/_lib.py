@@ -1,0 +1,135 @@
+"""ctypes binding of libdspine_verify.so (the C ABI declared in include/dspine_verify.h).
+
+The library is built in-tree by ``dspine_amd/csrc/build.py`` (``__graft_entry__.build()``).
+There is no fallback: every product entry point raises when the library is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdspine_verify.so")
+
+DSV_OK, DSV_ERR_INVALID, DSV_ERR_UNSUPPORTED, DSV_ERR_LAUNCH, DSV_ERR_WORKSPACE = range(5)
+DSV_F32, DSV_BF16, DSV_F16 = 0, 1, 2
+DSV_BACKEND_PYTORCH, DSV_BACKEND_FLASHINFER = 0, 1
+LIST_K = 64
+
+# Every symbol include/dspine_verify.h declares (checked by tests/test_lib_symbols.py).
+EXPORTS = (
+    "dsv_last_error", "dsv_device_count", "dsv_verify_workspace_bytes", "dsv_verify",
+    "dsv_greedy_verify", "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_uniforms",
+)
+
+_c = ctypes
+vp, i32, i64 = _c.c_void_p, _c.c_int32, _c.c_int64
+
+
+class VerifyArgs(ctypes.Structure):
+    """Mirror of ``dsv_verify_args``."""
+
+    _fields_ = [
+        ("logits", vp), ("logits_dtype", i32), ("stages", i32),
+        ("rows", i64), ("vocab", i64), ("row_stride", i64),
+        ("bs", i32), ("T", i32),
+        ("verify_lens", vp), ("row_offsets", vp), ("row_offsets_i64", i32),
+        ("backend", i32),
+        ("temperatures", vp), ("top_ks", vp), ("top_ps", vp), ("min_ps", vp),
+        ("filter", i32), ("need_min_p", i32), ("any_greedy", i32), ("max_top_k", i32),
+        ("hist_ids", vp), ("hist_len", i32), ("pad1", i32), ("presence", vp), ("repetition", vp),
+        ("candidates", vp), ("q_ids", vp), ("q_ids_i64", i32), ("K", i32), ("q_values", vp),
+        ("uniforms", vp), ("uniform_final", vp), ("prefix_lens", vp),
+        ("page_table", vp), ("page_stride", i64), ("page_cols", i64),
+        ("accept", vp), ("commit", vp), ("bonus", vp), ("output", vp), ("new_seq", vp),
+        ("kv_slots", vp),
+        ("workspace", vp), ("workspace_bytes", i64),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load():
+    """Load (once) the HIP library; raise when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.dsv_last_error.restype = ctypes.c_char_p
+        lib.dsv_device_count.restype = i32
+        lib.dsv_verify_workspace_bytes.restype = i64
+        lib.dsv_verify_workspace_bytes.argtypes = [i64, i32, i32, i64]
+        lib.dsv_greedy_workspace_bytes.restype = i64
+        lib.dsv_greedy_workspace_bytes.argtypes = [i64]
+        lib.dsv_verify.restype = i32
+        lib.dsv_verify.argtypes = [ctypes.POINTER(VerifyArgs), vp]
+        lib.dsv_greedy_verify.restype = i32
+        lib.dsv_greedy_verify.argtypes = [vp, i32, i64, i64, i64, i32, i32, vp, vp, i32, vp,
+                                          vp, vp, vp, vp, vp, vp, vp, i64, vp]
+        lib.dsv_topk.restype = i32
+        lib.dsv_topk.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, i32, vp]
+        lib.dsv_uniforms.restype = i32
+        lib.dsv_uniforms.argtypes = [vp, vp, i32, i64, i32, i32, vp, vp]
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a library status onto the reference's exception types (ValueError for contract
+    violations before launch, RuntimeError for launch failures)."""
+    if rc == DSV_OK:
+        return
+    msg = load().dsv_last_error().decode(errors="replace")
+    if rc in (DSV_ERR_INVALID, DSV_ERR_WORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    if rc == DSV_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return DSV_BF16
+    if t.dtype == torch.float32:
+        return DSV_F32
+    raise ValueError(f"unsupported logits dtype {t.dtype} (expected float32 or bfloat16)")
+
+
+def require_cuda(*tensors) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("the HIP verification path requires device (cuda) tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on one device")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev

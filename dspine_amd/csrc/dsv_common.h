@@ -1,0 +1,173 @@
+// Shared device/host helpers of the gfx950 verification kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dspine_verify.h"
+
+namespace dsv {
+
+void set_error(const char* fmt, ...);
+
+#define DSV_FAIL(code, ...)        \
+  do {                             \
+    ::dsv::set_error(__VA_ARGS__); \
+    return (code);                 \
+  } while (0)
+
+#define DSV_CHECK_LAUNCH(what)                                                             \
+  do {                                                                                     \
+    hipError_t e_ = hipGetLastError();                                                     \
+    if (e_ != hipSuccess)                                                                  \
+      DSV_FAIL(DSV_ERR_LAUNCH, "%s: HIP launch failed: %s", (what), hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr int WAVE = 64;
+constexpr uint32_t NEG_INF_BF16_KEY = 0x007Fu;  // key16 of bf16 -inf (0xFF80)
+
+// ---------------------------------------------------------------------------------------
+// Order-preserving keys.  -0.0 is folded onto +0.0 so that equal values share one key, as
+// torch's comparisons (sort, argmax) treat them as equal.  Larger value -> larger key.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_f32(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+// 16-bit key of a bf16 value given as raw bits.
+__device__ __forceinline__ uint32_t bf16_key(uint32_t b) {
+  b &= 0xffffu;
+  if (b == 0x8000u) b = 0u;
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+__device__ __forceinline__ float bf16_key_to_f32(uint32_t k) {
+  uint32_t b = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+  return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even float -> bf16 bits (what torch's copy into a bf16 tensor does).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// e^x for the running softmax sums: 2^(x*log2e) with the product error folded back in,
+// about 1 ulp over the range that matters (|x| < 104).
+__device__ __forceinline__ float exp_fast(float x) {
+  const float L = 1.44269502162933349609375f;  // fp32(log2 e)
+  const float Llo = 1.925963033500011e-08f;    // log2 e - L
+  float t = x * L;
+  float err = fmaf(x, L, -t);
+  err = fmaf(x, Llo, err);
+  float r = __builtin_amdgcn_exp2f(t);
+  return fmaf(r, err * 0.693147180559945309f, r);
+}
+
+// ---------------------------------------------------------------------------------------
+// Wave / block reductions (wave64).
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t w = __shfl_xor(v, o, WAVE);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o, WAVE);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o, WAVE);
+    v = w < v ? w : v;
+  }
+  return v;
+}
+// Inclusive prefix sum over lanes 0..63.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    T w = __shfl_up(v, o, WAVE);
+    if (lane >= o) v += w;
+  }
+  return v;
+}
+
+// Block-wide sum.  `scratch` holds >= nwaves entries; result broadcast to every thread.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* scratch) {
+  const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
+  const int nw = blockDim.x / WAVE;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  T s = T(0);
+  for (int i = 0; i < nw; ++i) s += scratch[i];  // fixed order: deterministic
+  return s;
+}
+
+// Block-wide exclusive prefix over thread order (deterministic); also returns the total.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
+  const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
+  const int nw = blockDim.x / WAVE;
+  T incl = wave_incl_scan(v);
+  __syncthreads();
+  if (lane == WAVE - 1) scratch[wid] = incl;
+  __syncthreads();
+  T before = T(0), tot = T(0);
+  for (int i = 0; i < nw; ++i) {
+    if (i < wid) before += scratch[i];
+    tot += scratch[i];
+  }
+  if (total) *total = tot;
+  return before + incl - v;
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch) {
+  const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
+  const int nw = blockDim.x / WAVE;
+  v = wave_max_u64(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  uint64_t m = 0;
+  for (int i = 0; i < nw; ++i) m = scratch[i] > m ? scratch[i] : m;
+  return m;
+}
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* scratch) {
+  const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
+  const int nw = blockDim.x / WAVE;
+  v = wave_min_u64(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  uint64_t m = ~0ull;
+  for (int i = 0; i < nw; ++i) m = scratch[i] < m ? scratch[i] : m;
+  return m;
+}
+
+}  // namespace dsv

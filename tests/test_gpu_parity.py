@@ -1,0 +1,294 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle on identical inputs.
+
+Integer outputs must match bit-exactly.  A request may differ only when the oracle itself
+reports a decision margin below MARGIN (an accept test u*q vs p or a bonus CDF boundary within
+rounding of the reference's own float32 softmax); such requests are counted and must be rare.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from dspine_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+MARGIN = 1e-4  # relative: well above the ~1e-5 error of CPU torch's float32 softmax
+
+
+def _oracle():
+    import oracle.verify_oracle as O
+
+    return O
+
+
+def compare_outputs(gpu, ref, requests, tag):
+    """gpu/ref: dicts of numpy arrays (accept, bonus, output, new_seq, [kv_slots]); returns the
+    list of near-margin requests that differ (asserts every other request is identical)."""
+    near = []
+    for b in requests:
+        same = (int(gpu["accept"][b]) == int(ref["accept"][b])
+                and int(gpu["bonus"][b]) == int(ref["bonus"][b])
+                and np.array_equal(gpu["output"][b], ref["output"][b])
+                and int(gpu["new_seq"][b]) == int(ref["new_seq"][b]))
+        if same and ref.get("kv_slots") is not None and gpu.get("kv_slots") is not None:
+            same = np.array_equal(gpu["kv_slots"][b], ref["kv_slots"][b])
+        if not same:
+            m = float(ref["margins"][b])
+            assert m < MARGIN, (tag, b, {k: gpu[k][b] for k in ("accept", "bonus")},
+                                {k: ref[k][b] for k in ("accept", "bonus")}, m)
+            near.append(b)
+    return near
+
+
+def run_gpu_verify(batch, device, backend="pytorch"):
+    from dspine_amd.verify import History, verify_step
+
+    d = W.to_device(batch, device)
+    hist = None
+    if "hist_ids" in d:
+        hist = History(d["hist_ids"], d["presence"], d["repetition"])
+    outs, kv = verify_step(
+        logits=d["logits"], sampling_info=d["info"], candidates=d["candidates"], q_ids=d["q_ids"],
+        q_values=d["q_values"], uniforms=d["uniforms"], uniform_final=d["uniform_final"],
+        prefix_lens=d["prefix_lens"], verify_lens=d.get("verify_lens"),
+        row_offsets=d.get("row_offsets"), history=hist, page_table=d.get("page_table"),
+        sampling_backend=backend)
+    torch.cuda.synchronize()
+    names = ("accept", "commit", "bonus", "output", "new_seq")
+    res = {n: t.cpu().numpy() for n, t in zip(names, outs)}
+    res["kv_slots"] = kv.cpu().numpy() if kv is not None else None
+    return res
+
+
+def run_oracle(batch, requests, backend="pytorch"):
+    O = _oracle()
+    bs, T = batch["candidates"].shape
+    lens = batch.get("verify_lens")
+    lens = np.full(bs, T) if lens is None else lens.numpy()
+    return O.verify_step(
+        batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
+        q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(), verify_lens=lens,
+        uniforms=batch["uniforms"].numpy(), uniform_final=batch["uniform_final"].numpy(),
+        prefix_lens=batch["prefix_lens"].numpy(), hist_ids=batch.get("hist_ids"),
+        presence=batch.get("presence"), repetition=batch.get("repetition"),
+        page_table=batch.get("page_table"),
+        row_offsets=None if batch.get("row_offsets") is None else batch["row_offsets"].numpy(),
+        sampling_backend=backend, requests=requests)
+
+
+# ------------------------------------------------------------------------------------------
+# uniforms
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("stream", [0, 1, 2, 3])
+def test_uniforms_bitwise(device, stream):
+    from dspine_amd.sampling.random import seeded_uniforms
+
+    O = _oracle()
+    seeds = torch.tensor([0, -1, -(2**63), 2**63 - 1, 2**40 + 7, 12345])
+    positions = torch.tensor([0, 19, 214, 8192, 131071, 7], dtype=torch.int32)
+    got = seeded_uniforms(seeds.to(device), positions.to(device), 15, stream).cpu().numpy()
+    ref = O.seeded_uniforms(seeds.numpy(), positions.numpy(), 15, stream)
+    assert np.array_equal(got, ref)
+    got64 = seeded_uniforms(seeds.to(device), positions.long().to(device), 15, stream).cpu().numpy()
+    assert np.array_equal(got64, ref)
+
+
+# ------------------------------------------------------------------------------------------
+# top-k
+# ------------------------------------------------------------------------------------------
+def _topk_check(x_cpu, k, device):
+    from dspine_amd.kernels.dspine import topk, topk_ids
+
+    O = _oracle()
+    vals, ids = topk(x_cpu.to(device), k)
+    rv, ri = O.topk(x_cpu.float(), k)
+    assert torch.equal(ids.cpu(), ri), "ids differ from the stable (value desc, id asc) order"
+    assert torch.equal(vals.cpu(), rv)
+    srt = topk_ids(x_cpu.to(device), k).cpu()
+    assert torch.equal(srt, ri.sort(-1).values)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("k", [16, 128])
+def test_topk_small_ties(device, dtype, k):
+    # tests/test_topk_compat.py:70-84: 257-wide rows of i % 7 with a -inf tail
+    scores = torch.arange(257).remainder(7).to(dtype).repeat(2, 1)
+    scores[1, 254:] = -torch.inf
+    _topk_check(scores, k, device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("k", [1, 20, 64])
+def test_topk_serving_rows(device, dtype, k):
+    x = W.topk_rows(rows=96, seed=11, dtype=dtype)["logits"]
+    _topk_check(x, k, device)
+
+
+@pytest.mark.parametrize("k", [1, 20, 64, 1000])
+def test_topk_degenerate_rows(device, k):
+    V = 70001
+    rows = torch.zeros(4, V)
+    rows[1] = torch.arange(V).float()          # ascending: every block raises the threshold
+    rows[2] = -torch.arange(V).float()         # descending
+    rows[3, :] = -torch.inf
+    rows[3, 5::1000] = 1.0                     # only 71 finite values
+    for dtype in (torch.float32, torch.bfloat16):
+        _topk_check(rows.to(dtype), k, device)
+
+
+# ------------------------------------------------------------------------------------------
+# greedy verify (config: 1 x 17 x 151936 fp32)
+# ------------------------------------------------------------------------------------------
+def test_greedy_round(device):
+    from dspine_amd.verification.caps import accept_greedy
+
+    O = _oracle()
+    batch = W.greedy_round()
+    top1 = O.argmax_rows(batch["logits"])
+    ref = O.greedy_accept(top1, batch["candidates"].numpy(), [17], batch["prefix_lens"].numpy())
+    outs = accept_greedy(candidates=batch["candidates"].to(device),
+                         next_token_logits=batch["logits"].to(device),
+                         prefix_lens=batch["prefix_lens"].to(device), cap=17)
+    got = [t.cpu().numpy() for t in outs]
+    assert int(got[0][0]) == batch["mismatch"] == int(ref[0][0])
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, r)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_ties_and_caps(device, dtype):
+    from dspine_amd.verification.caps import accept_greedy
+
+    O = _oracle()
+    g = torch.Generator().manual_seed(5)
+    bs, T, V = 9, 16, 997
+    logits = torch.randint(-3, 3, (bs * T, V), generator=g).to(dtype)  # heavy ties
+    logits[: 3 * T] = 0  # all-tie rows: first id wins
+    top1 = O.argmax_rows(logits)
+    cand = torch.zeros(bs, T, dtype=torch.int64)
+    cand[:, 1:] = torch.as_tensor(top1).view(bs, T)[:, : T - 1]
+    cand[4, 6] = (cand[4, 6] + 1) % V
+    lens = (torch.arange(bs, dtype=torch.int32) % T) + 1
+    prefix = torch.arange(bs, dtype=torch.int32) + 100
+    for cap, vl in ((T, None), (7, None), (None, lens)):
+        ref = O.greedy_accept(top1, cand.numpy(), (lens.numpy() if vl is not None else [cap] * bs),
+                              prefix.numpy())
+        outs = accept_greedy(candidates=cand.to(device), next_token_logits=logits.to(device),
+                             prefix_lens=prefix.to(device), cap=cap,
+                             verify_lens=None if vl is None else vl.to(device))
+        for got, r in zip(outs, ref):
+            assert np.array_equal(got.cpu().numpy(), r), (cap, vl)
+
+
+# ------------------------------------------------------------------------------------------
+# fused sampled verify
+# ------------------------------------------------------------------------------------------
+def _small_batch(seed, bs=24, T=8, V=997, K=8, dtype=torch.float32, mixed=True, penalties=False,
+                 ragged=False):
+    g = torch.Generator().manual_seed(seed)
+    rows_per = torch.full((bs,), T, dtype=torch.int64)
+    if ragged:
+        rows_per = torch.randint(1, T + 1, (bs,), generator=g)
+    offsets = torch.cat((torch.zeros(1, dtype=torch.int64), rows_per.cumsum(0)))[:-1]
+    nrows = int(rows_per.sum()) if ragged else bs * T
+    logits = (torch.randn(nrows, V, generator=g) * 2.0).to(dtype)
+    if mixed:
+        temps = torch.tensor([0.0, 0.6, 1.0, 1.3])[torch.randint(0, 4, (bs,), generator=g)]
+        ks = torch.tensor([0, 1, 5, 20, 64, 100])[torch.randint(0, 6, (bs,), generator=g)]
+        ps = torch.tensor([1.0, 0.95, 0.8, 0.5])[torch.randint(0, 4, (bs,), generator=g)]
+    else:
+        temps = torch.full((bs,), 0.8)
+        ks = torch.full((bs,), 20)
+        ps = torch.full((bs,), 0.9)
+    info = W.sampling_info(temps, ks, ps)
+    q_ids = torch.stack([torch.randperm(V, generator=g)[:K] for _ in range(bs * (T - 1))]).view(bs, T - 1, K)
+    # make the most likely target token a q lane often, so acceptances happen
+    base = logits.float()
+    for b in range(bs):
+        r0 = int(offsets[b]) if ragged else b * T
+        for s in range(T - 1):
+            r = r0 + min(s, int(rows_per[b]) - 1)
+            q_ids[b, s, 0] = int(base[r].argmax())
+    q_ids, _ = q_ids.sort(-1)
+    q = torch.softmax(torch.randn(bs, T - 1, K, generator=g) * 2, -1)
+    lanes = torch.multinomial(q.view(-1, K), 1, generator=g).view(bs, T - 1)
+    drafts = q_ids.gather(2, lanes[..., None]).squeeze(-1)
+    cand = torch.cat((torch.zeros(bs, 1, dtype=torch.int64), drafts), 1)
+    u = W.philox_uniforms(seed, bs, T)
+    batch = dict(logits=logits, info=info, candidates=cand, q_ids=q_ids, q_values=q.float(),
+                 uniforms=u[:, : T - 1].contiguous(), uniform_final=u[:, T - 1].contiguous(),
+                 prefix_lens=torch.randint(0, 50, (bs,), generator=g, dtype=torch.int64).to(torch.int32),
+                 page_table=torch.randperm(bs * 80, generator=g).view(bs, 80).to(torch.int32))
+    if ragged:
+        batch["verify_lens"] = rows_per.to(torch.int32)
+        batch["row_offsets"] = offsets
+    else:
+        batch["verify_lens"] = torch.randint(1, T + 1, (bs,), generator=g, dtype=torch.int64).to(torch.int32)
+    if penalties:
+        batch["hist_ids"] = torch.randint(-1, V, (bs, 40), generator=g, dtype=torch.int64).to(torch.int32)
+        batch["presence"] = torch.rand(bs, generator=g)
+        batch["repetition"] = 1.0 + torch.rand(bs, generator=g)
+    return batch
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("penalties", [False, True])
+def test_verify_small_mixed(device, seed, dtype, penalties):
+    if dtype == torch.float32:
+        # float32 nucleus rows (top-k > 64 with top-p) are rejected up front; keep top-k small
+        batch = _small_batch(seed, dtype=dtype, mixed=False, penalties=penalties)
+    else:
+        batch = _small_batch(seed, dtype=dtype, penalties=penalties)
+    bs = batch["candidates"].shape[0]
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    near = compare_outputs(gpu, ref, range(bs), f"small seed={seed}")
+    assert len(near) <= 1
+
+
+@pytest.mark.parametrize("seed", [3, 4])
+def test_verify_small_ragged(device, seed):
+    batch = _small_batch(seed, dtype=torch.bfloat16, ragged=True, penalties=True)
+    bs = batch["candidates"].shape[0]
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    assert len(compare_outputs(gpu, ref, range(bs), f"ragged seed={seed}")) <= 1
+
+
+def test_verify_unfiltered(device):
+    batch = _small_batch(7, dtype=torch.bfloat16, mixed=False)
+    batch["info"] = W.sampling_info([0.7] * 24, [0] * 24, [1.0] * 24)
+    bs = 24
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    assert len(compare_outputs(gpu, ref, range(bs), "unfiltered")) <= 1
+
+
+SERVING_SUBSET = [0, 1, 2, 3, 5, 8, 13, 21, 34, 55, 63]
+
+
+def test_verify_serving_round_subset(device):
+    batch = W.serving_round()
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, SERVING_SUBSET)
+    near = compare_outputs(gpu, ref, SERVING_SUBSET, "serving")
+    assert len(near) <= 1
+
+
+@pytest.mark.parametrize("sigma", [0.5, 1.5])
+def test_verify_rejection_round_subset(device, sigma):
+    batch = W.rejection_round(sigma_draft=sigma)
+    subset = [0, 3, 7, 12, 19, 31]
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, subset)
+    assert len(compare_outputs(gpu, ref, subset, f"rejection sigma={sigma}")) <= 1
+
+
+def test_verify_ragged_round_subset(device):
+    batch = W.ragged_round()
+    subset = [0, 1, 9, 17, 31]
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, subset)
+    assert len(compare_outputs(gpu, ref, subset, "ragged")) <= 1
