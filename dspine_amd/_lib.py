@@ -22,7 +22,8 @@ LIST_K = 64
 # Every symbol include/dspine_verify.h declares (checked by tests/test_lib_symbols.py).
 EXPORTS = (
     "dsv_last_error", "dsv_device_count", "dsv_verify_workspace_bytes", "dsv_verify",
-    "dsv_greedy_verify", "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_uniforms",
+    "dsv_greedy_verify", "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_topk_workspace_bytes",
+    "dsv_uniforms",
 )
 
 _c = ctypes
@@ -76,14 +77,16 @@ def load():
         lib.dsv_verify_workspace_bytes.restype = i64
         lib.dsv_verify_workspace_bytes.argtypes = [i64, i32, i32, i64]
         lib.dsv_greedy_workspace_bytes.restype = i64
-        lib.dsv_greedy_workspace_bytes.argtypes = [i64]
+        lib.dsv_greedy_workspace_bytes.argtypes = [i64, i64]
+        lib.dsv_topk_workspace_bytes.restype = i64
+        lib.dsv_topk_workspace_bytes.argtypes = [i64, i64, i32]
         lib.dsv_verify.restype = i32
         lib.dsv_verify.argtypes = [ctypes.POINTER(VerifyArgs), vp]
         lib.dsv_greedy_verify.restype = i32
         lib.dsv_greedy_verify.argtypes = [vp, i32, i64, i64, i64, i32, i32, vp, vp, i32, vp,
                                           vp, vp, vp, vp, vp, vp, vp, i64, vp]
         lib.dsv_topk.restype = i32
-        lib.dsv_topk.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, i32, vp]
+        lib.dsv_topk.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, i32, vp, i64, vp]
         lib.dsv_uniforms.restype = i32
         lib.dsv_uniforms.argtypes = [vp, vp, i32, i64, i32, i32, vp, vp]
         _lib = lib

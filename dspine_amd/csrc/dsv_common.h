@@ -115,11 +115,13 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
-// Block-wide sum.  `scratch` holds >= nwaves entries; result broadcast to every thread.
-template <typename T>
+// Block-wide reductions over NW waves (the block size / 64, a compile-time constant so that
+// the final loop over the per-wave partials is fully unrolled).
+// Block-wide sum.  `scratch` holds NW entries; result broadcast to every thread.
+template <int NW, typename T>
 __device__ __forceinline__ T block_sum(T v, T* scratch) {
   const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
-  const int nw = blockDim.x / WAVE;
+  constexpr int nw = NW;
   v = wave_sum(v);
   __syncthreads();
   if (lane == 0) scratch[wid] = v;
@@ -130,10 +132,10 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
 }
 
 // Block-wide exclusive prefix over thread order (deterministic); also returns the total.
-template <typename T>
+template <int NW, typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
   const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
-  const int nw = blockDim.x / WAVE;
+  constexpr int nw = NW;
   T incl = wave_incl_scan(v);
   __syncthreads();
   if (lane == WAVE - 1) scratch[wid] = incl;
@@ -147,9 +149,10 @@ __device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
   return before + incl - v;
 }
 
+template <int NW>
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch) {
   const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
-  const int nw = blockDim.x / WAVE;
+  constexpr int nw = NW;
   v = wave_max_u64(v);
   __syncthreads();
   if (lane == 0) scratch[wid] = v;
@@ -158,9 +161,10 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
   for (int i = 0; i < nw; ++i) m = scratch[i] > m ? scratch[i] : m;
   return m;
 }
+template <int NW>
 __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* scratch) {
   const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
-  const int nw = blockDim.x / WAVE;
+  constexpr int nw = NW;
   v = wave_min_u64(v);
   __syncthreads();
   if (lane == 0) scratch[wid] = v;

@@ -4,7 +4,7 @@ The reference's two-stage Triton top-k returns the k largest ids of each row asc
 with the value multiset of ``torch.topk`` and boundary ties to lower ids inside the chosen
 chunks.  Here a single streaming HIP kernel selects the exact top-k under the
 ``(value desc, id asc)`` order of ``layers/fp8/coarse.py:19-34`` / ``sampling/tp_head.py:9-14``,
-so ties at the k-th place always go to the lowest ids.  k is any value in [1, 1024].
+so ties at the k-th place always go to the lowest ids.  k is any value in [1, 256].
 """
 
 from __future__ import annotations
@@ -12,13 +12,23 @@ from __future__ import annotations
 import torch
 
 from dspine_amd import _lib
+from dspine_amd.verify import Workspace
+
+TOPK_MAX = 256
+_ws: dict = {}
+
+
+def _workspace(logits: torch.Tensor, k: int) -> torch.Tensor:
+    lib = _lib.load()
+    nbytes = int(lib.dsv_topk_workspace_bytes(logits.shape[0], logits.shape[1], k))
+    return _ws.setdefault(logits.device, Workspace()).get(nbytes, logits.device)
 
 
 def _check(logits: torch.Tensor, k: int):
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("topk expects a row-contiguous [N, V] tensor")
-    if not isinstance(k, int) or not 1 <= k <= min(1024, logits.shape[1]):
-        raise ValueError(f"topk needs an integer k in [1, min(1024, V)], got {k}")
+    if not isinstance(k, int) or not 1 <= k <= min(TOPK_MAX, logits.shape[1]):
+        raise ValueError(f"topk needs an integer k in [1, min({TOPK_MAX}, V)], got {k}")
     _lib.require_cuda(logits)
 
 
@@ -35,9 +45,10 @@ def topk(logits: torch.Tensor, k: int, values: torch.Tensor | None = None,
             or ids.dtype != torch.int64 or not values.is_contiguous() or not ids.is_contiguous():
         raise ValueError("topk outputs must be contiguous float32/int64 [N, k]")
     lib = _lib.load()
+    ws = _workspace(logits, k)
     _lib.check(lib.dsv_topk(logits.data_ptr(), _lib.dtype_code(logits), n, logits.shape[1],
                             logits.stride(0), k, values.data_ptr(), ids.data_ptr(), 0,
-                            _lib.stream_of(logits.device)), "dsv_topk")
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(logits.device)), "dsv_topk")
     return values, ids
 
 
@@ -53,7 +64,8 @@ def topk_ids(logits: torch.Tensor, k: int, out: torch.Tensor = None) -> torch.Te
     if n == 0:
         return out
     lib = _lib.load()
+    ws = _workspace(logits, k)
     _lib.check(lib.dsv_topk(logits.data_ptr(), _lib.dtype_code(logits), n, logits.shape[1],
                             logits.stride(0), k, None, out.data_ptr(), 1,
-                            _lib.stream_of(logits.device)), "dsv_topk")
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(logits.device)), "dsv_topk")
     return out

@@ -50,7 +50,7 @@ def accept_greedy(*, candidates: torch.Tensor, next_token_logits: torch.Tensor,
     if top1 is not None and (top1.shape != (bs, T) or top1.dtype != torch.int64):
         raise ValueError("top1 must be int64 [bs, T]")
     lib = _lib.load()
-    ws = _ws.setdefault(dev, Workspace()).get(int(lib.dsv_greedy_workspace_bytes(bs * T)), dev)
+    ws = _ws.setdefault(dev, Workspace()).get(int(lib.dsv_greedy_workspace_bytes(bs * T, logits.shape[1])), dev)
     _lib.check(lib.dsv_greedy_verify(
         logits.data_ptr(), _lib.dtype_code(logits), bs * T, logits.shape[1], logits.stride(0), bs, T,
         candidates.data_ptr(), _lib.ptr(verify_lens), int(cap or 0), prefix_lens.data_ptr(),

@@ -118,21 +118,23 @@ int64_t dsv_verify_workspace_bytes(int64_t rows, int32_t bs, int32_t T, int64_t 
 int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream);
 
 /* Greedy verify (argmax acceptance): top1 = first argmax of each row, a = first mismatch   */
-/* below verify_lens[b]-1, bonus = top1[a]; output keeps proposals after a.  Rows are        */
-/* b*T + s (the full-width envelope).  top1_out [rows] (int64) is optional.                  */
+/* below verify_lens[b]-1 (or cap-1), bonus = top1[a]; output keeps proposals after a.      */
+/* Rows are b*T + s (the full-width envelope).  top1_out [rows] (int64) is optional.        */
 int dsv_greedy_verify(const void* logits, int32_t logits_dtype, int64_t rows, int64_t vocab,
                       int64_t row_stride, int32_t bs, int32_t T, const int64_t* candidates,
                       const int32_t* verify_lens, int32_t cap, const int32_t* prefix_lens,
                       int32_t* accept, int32_t* commit, int64_t* bonus, int64_t* output,
                       int32_t* new_seq, int64_t* top1_out, void* workspace,
                       int64_t workspace_bytes, dsv_stream_t stream);
-int64_t dsv_greedy_workspace_bytes(int64_t rows);
+int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab);
 
-/* Top-k per row in (value desc, id asc) order.  values_out [rows, k] float32 (may be NULL), */
-/* ids_out [rows, k] int64; sort_by_id != 0 re-sorts each row's ids ascending (topk_ids).   */
+/* Top-k per row in (value desc, id asc) order, k in [1, 256].  values_out [rows, k] float32 */
+/* (may be NULL), ids_out [rows, k] int64; sort_by_id != 0 re-sorts each row's ids ascending */
+/* (topk_ids).  workspace: dsv_topk_workspace_bytes(rows, vocab, k) bytes of device memory.  */
 int dsv_topk(const void* logits, int32_t logits_dtype, int64_t rows, int64_t vocab,
              int64_t row_stride, int32_t k, float* values_out, int64_t* ids_out,
-             int32_t sort_by_id, dsv_stream_t stream);
+             int32_t sort_by_id, void* workspace, int64_t workspace_bytes, dsv_stream_t stream);
+int64_t dsv_topk_workspace_bytes(int64_t rows, int64_t vocab, int32_t k);
 
 /* Seeded uniforms [n, width] of draw stream `stream` (0..3), murmur3 keyed by              */
 /* (seed, position, column).                                                                */

@@ -125,7 +125,7 @@ def test_topk_serving_rows(device, dtype, k):
     _topk_check(x, k, device)
 
 
-@pytest.mark.parametrize("k", [1, 20, 64, 1000])
+@pytest.mark.parametrize("k", [1, 20, 64, 256])
 def test_topk_degenerate_rows(device, k):
     V = 70001
     rows = torch.zeros(4, V)

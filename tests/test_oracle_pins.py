@@ -1,0 +1,385 @@
+"""Pin the CPU oracle before trusting it: published vectors, the reference tests' known answers,
+independent float64 references with explicit sorts/loops, and brute force on tiny inputs.
+Each check is chosen so that a plausible slip (dropped term, wrong sign, swapped index, wrong
+tie rule) fails it."""
+
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.verify_oracle as O
+
+# ---------------------------------------------------------------------------------------
+# S5 uniforms
+# ---------------------------------------------------------------------------------------
+MURMUR_VECTORS = [  # MurmurHash3_x86_32 published test vectors (SMHasher / reference ports)
+    (b"", 0, 0x00000000), (b"", 1, 0x514E28B7), (b"", 0xFFFFFFFF, 0x81F16F39),
+    (b"\0\0\0\0", 0, 0x2362F9DE), (b"aaaa", 0x9747B28C, 0x5A97808A), (b"aaa", 0x9747B28C, 0x283E0130),
+    (b"Hello, world!", 0x9747B28C, 0x24884CBA), (b"abc", 0, 0xB3DD93FA), (b"abcd", 0, 0x43ED676A),
+    (b"The quick brown fox jumps over the lazy dog", 0x9747B28C, 0x2FA826CD),
+    (b"Hello, world!", 1234, 0xFAF6CDB3), (b"The quick brown fox jumps over the lazy dog", 0, 0x2E4FF723),
+]
+
+
+@pytest.mark.parametrize("data,seed,expected", MURMUR_VECTORS)
+def test_murmur3_published_vectors(data, seed, expected):
+    assert O.murmur3_x86_32(data, seed) == expected
+
+
+def test_uniforms_are_murmur_of_the_16_byte_message():
+    seeds = [0, -1, -(2 ** 63), 2 ** 63 - 1, 2 ** 40 + 7]
+    positions = [0, 19, 214, 8192, 131071]
+    for stream in range(4):
+        u = O.seeded_uniforms(seeds, positions, 15, stream)
+        for r, (s, p) in enumerate(zip(seeds, positions)):
+            s &= (1 << 64) - 1
+            for c in (0, 1, 7, 14):
+                msg = b"".join(int(w).to_bytes(4, "little") for w in
+                               (s & 0xFFFFFFFF, s >> 32, p & 0xFFFFFFFF, c + (stream << 16)))
+                h = O.murmur3_x86_32(msg, 0)
+                assert u[r, c] == np.float32((h >> 8) * 2.0 ** -24)
+
+
+def test_uniform_layout_invariants():
+    # tests/test_random.py:25-53: reordering / compaction / other requests do not change draws;
+    # streams, positions and both seed halves matter; values in [0, 1)
+    seeds = np.array([0, -1, -(2 ** 63), 2 ** 63 - 1, 2 ** 40 + 7])
+    pos = np.array([0, 19, 214, 8192, 131071])
+    ref = O.seeded_uniforms(seeds, pos, 15, O.ACCEPT)
+    order = [4, 1, 3]
+    assert np.array_equal(ref[order], O.seeded_uniforms(seeds[order], pos[order], 15, O.ACCEPT))
+    assert ((ref >= 0) & (ref < 1)).all()
+    v = [O.seeded_uniforms([7], [99], 15, s) for s in range(4)]
+    assert all(not np.array_equal(v[i], v[j]) for i in range(4) for j in range(i))
+    assert not np.array_equal(v[0], O.seeded_uniforms([7 + 2 ** 32], [99], 15, 0))
+    assert not np.array_equal(v[0], O.seeded_uniforms([7], [100], 15, 0))
+
+
+# ---------------------------------------------------------------------------------------
+# S1 target distribution
+# ---------------------------------------------------------------------------------------
+def _info(bs, temperature, top_k=None, top_p=None, min_p=None):
+    # tests/ref_utils.py:150-162 stand-in: a filter left None is off
+    from types import SimpleNamespace
+    return SimpleNamespace(
+        temperatures=torch.full((bs, 1), float(temperature)),
+        top_ks=torch.full((bs,), top_k or O.TOP_K_ALL, dtype=torch.int32),
+        top_ps=torch.full((bs,), top_p or 1.0), min_ps=torch.full((bs,), min_p or 0.0),
+        need_top_k_sampling=top_k is not None, need_top_p_sampling=top_p is not None,
+        need_min_p_sampling=min_p is not None, is_all_greedy=False)
+
+
+def test_target_probs_hand_computed():
+    # tests/test_sampling.py:38-59 with unfiltered p = [.4, .3, .2, .1]
+    logits = torch.log(torch.tensor([[4.0, 3.0, 2.0, 1.0]]))
+    got = O.build_target_probs(logits, _info(1, 1.0, top_k=2, top_p=0.5), 1, 1, "flashinfer")[0, 0]
+    torch.testing.assert_close(got.double(), torch.tensor([4 / 7, 3 / 7, 0, 0]).double(), rtol=0, atol=1e-6)
+    got = O.build_target_probs(logits, _info(1, 1.0, top_k=3, top_p=0.8, min_p=0.6), 1, 1, "flashinfer")[0, 0]
+    torch.testing.assert_close(got.double(), torch.tensor([4 / 7, 3 / 7, 0, 0]).double(), rtol=0, atol=1e-6)
+    got = O.build_target_probs(logits, _info(1, 1.0, top_p=0.75), 1, 1, "pytorch")[0, 0]
+    torch.testing.assert_close(got.double(), torch.tensor([4 / 9, 3 / 9, 2 / 9, 0]).double(), rtol=0, atol=1e-6)
+    # pytorch backend, top_k=2 and top_p=.5 jointly: support {0, 1}
+    got = O.build_target_probs(logits, _info(1, 1.0, top_k=2, top_p=0.5), 1, 1, "pytorch")[0, 0]
+    torch.testing.assert_close(got.double(), torch.tensor([4 / 7, 3 / 7, 0, 0]).double(), rtol=0, atol=1e-6)
+
+
+def _independent_row(logits_row, temperature, top_k, top_p, min_p):
+    """float64, explicit Python sort by (-p, id) and explicit mass-ahead loop: the definition of
+    the joint top-k / top-p / min-p support (tests/ref_utils.py:79-108)."""
+    x = [float(v) for v in logits_row]
+    m = max(v / temperature for v in x)
+    e = [math.exp(v / temperature - m) for v in x]
+    z = sum(e)
+    p = [v / z for v in e]
+    order = sorted(range(len(p)), key=lambda i: (-p[i], i))
+    keep = [False] * len(p)
+    ahead = 0.0
+    for rank, i in enumerate(order):
+        keep[i] = rank < top_k and ahead <= top_p and p[i] >= min_p * p[order[0]]
+        ahead += p[i]
+    w = [p[i] if keep[i] else 0.0 for i in range(len(p))]
+    s = sum(w)
+    return torch.tensor([v / s for v in w], dtype=torch.float64)
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p,min_p", [
+    (0.8, None, None, 0.2), (0.6, 20, 0.95, None), (1.0, 7, None, None), (1.2, None, 0.6, None),
+    (0.9, 30, 0.9, 0.05)])
+def test_target_probs_match_independent_reference(temperature, top_k, top_p, min_p):
+    bs, T, V = 3, 4, 200
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(bs * T, V, generator=g) * 3
+    info = _info(bs, temperature, top_k, top_p, min_p)
+    got = O.build_target_probs(logits, info, T, bs, "pytorch").view(bs * T, V)
+    for r in range(bs * T):
+        ref = _independent_row(logits[r], temperature, top_k or O.TOP_K_ALL, top_p or 1.0, min_p or 0.0)
+        assert torch.equal(got[r] > 0, ref > 0), r
+        torch.testing.assert_close(got[r].double(), ref, rtol=1e-5, atol=1e-7)
+
+
+def test_ties_rank_lower_ids_first():
+    # equal probabilities straddling top_k keep the lower ids (stable sort)
+    logits = torch.tensor([[1.0, 3.0, 2.0, 3.0, 3.0, 0.0]])
+    got = O.build_target_probs(logits, _info(1, 1.0, top_k=2), 1, 1, "pytorch")[0, 0]
+    assert (got > 0).tolist() == [False, True, False, True, False, False]
+
+
+def test_mixed_greedy_rows_are_one_hot_at_first_argmax():
+    # tests/test_dynamic_sampling.py:306-331: all-equal greedy rows pick id 0
+    info = _info(3, 0.7, top_k=10, top_p=0.8)
+    info.is_any_greedy = True
+    info.top_ks[[0, 2]] = 1
+    logits = torch.randn(3 * 2, 11)
+    logits[0:2] = 0
+    logits[4:6] = 0
+    p = O.build_target_probs(logits, info, 2, 3, "pytorch")
+    onehot = torch.zeros(2, 11)
+    onehot[:, 0] = 1
+    assert torch.equal(p[0], onehot) and torch.equal(p[2], onehot)
+    assert bool((p[1] > 0).sum(-1).ge(1).all())
+
+
+def test_unfiltered_rows_are_not_renormalised():
+    # runtime/worker.py:477-478: no filter flag -> the softmax itself
+    logits = torch.randn(2, 50)
+    p = O.build_target_probs(logits, _info(2, 0.7), 1, 2, "pytorch")
+    assert torch.equal(p.view(2, 50), torch.softmax(logits / 0.7, -1))
+
+
+# ---------------------------------------------------------------------------------------
+# S9 adjustments
+# ---------------------------------------------------------------------------------------
+def test_adjustments_known_answer():
+    # tests/test_compact_integration.py:37-46
+    from types import SimpleNamespace
+    owner = torch.tensor([0, 1, 1])
+    info = SimpleNamespace(acc_scaling_penalties=torch.tensor([[2.0, 2.0], [.5, .5]]),
+                           logit_bias=torch.tensor([[.5, -.5], [1.0, -1.0]]))
+    x = torch.tensor([[2.0, -2.0], [-3.0, 3.0], [4.0, -4.0]])
+    O.adjust_logits(x, info, owner)
+    assert torch.equal(x, torch.tensor([[1.5, -4.5], [-.5, 5.0], [9.0, -3.0]]))
+
+
+def test_adjustments_alias_and_noop():
+    from types import SimpleNamespace
+    # tests/test_logit_adjustments.py:105-115: the additive name wins, never both
+    info = SimpleNamespace(acc_linear_penalties=torch.tensor([[1.0, -1.0]]),
+                           acc_additive_penalties=torch.tensor([[.5, -.5]]))
+    x = torch.tensor([[2.0, -2.0]])
+    O.adjust_logits(x, info, torch.tensor([0]))
+    assert torch.equal(x, torch.tensor([[2.5, -2.5]]))
+    # :118-129: no adjustments leave every bit untouched
+    x = torch.tensor([[float("nan"), -0.0, 0.0, -3.0, float("inf")]])
+    before = x.view(torch.int32).clone()
+    O.adjust_logits(x, SimpleNamespace(), torch.tensor([0]))
+    assert torch.equal(x.view(torch.int32), before)
+
+
+def test_history_penalties_closed_form():
+    hist = torch.tensor([[3, 1, 3, -1], [0, 2, -1, -1]], dtype=torch.int32)
+    add, scl = O.penalties_from_history(hist, torch.tensor([0.5, 1.0]), torch.tensor([1.25, 2.0]), 5)
+    assert add.tolist() == [[0, -0.5, 0, -0.5, 0], [-1.0, 0, -1.0, 0, 0]]
+    assert scl.tolist() == [[1, 1.25, 1, 1.25, 1], [2.0, 1, 2.0, 1, 1]]
+    from types import SimpleNamespace
+    x = torch.tensor([[1.0, 2.0, 3.0, -4.0, 5.0], [-1.0, 2.0, -2.0, 0.0, 3.0]]).bfloat16()
+    O.adjust_logits(x, SimpleNamespace(acc_additive_penalties=add, acc_scaling_penalties=scl),
+                    torch.tensor([0, 1]))
+    # history tokens: (x - pres) then x<0 ? x*r : x/r, rounded to bf16 after each step
+    expected = torch.tensor([[1.0, 1.5 / 1.25, 3.0, -4.5 * 1.25, 5.0],
+                             [-2.0 * 2.0, 2.0, -3.0 * 2.0, 0.0, 3.0]]).bfloat16()
+    assert torch.equal(x, expected)
+
+
+# ---------------------------------------------------------------------------------------
+# S3 chain rejection
+# ---------------------------------------------------------------------------------------
+def _pure_python_reference(p, candidates, qids, qvals, caps, u, uf, prefix):
+    """tests/test_sparse_accept_compact.py:22-53, restated: dense CPU rejection with float64
+    sums, written independently of the oracle's vectorised form."""
+    answer, offset = [], 0
+    for b, length in enumerate(caps):
+        a = 0
+        while a < length - 1:
+            token = candidates[b][a + 1]
+            q = sum(v for k, v in zip(qids[b][a], qvals[b][a]) if k == token)
+            if q > 0 and q <= 1 and float(np.float32(np.float32(u[b][a]) * np.float32(q))) < p[offset + a][token]:
+                a += 1
+            else:
+                break
+        row = p[offset + a]
+        weights = list(row)
+        if a != length - 1:
+            q = dict(zip(qids[b][a], qvals[b][a]))
+            weights = [max(v - q.get(k, 0), 0) for k, v in enumerate(row)]
+            if sum(weights) <= 0:
+                weights = list(row)
+        threshold = uf[b] * sum(weights)
+        cumulative, bonus = 0, len(row) - 1
+        for k, value in enumerate(weights):
+            cumulative += value
+            if cumulative > threshold:
+                bonus = k
+                break
+        T = len(candidates[b])
+        emitted = candidates[b][1:a + 1] + [bonus] + [0] * (T - 1 - a)
+        answer.append((a, a + 1, bonus, emitted, prefix[b] + a + 1))
+        offset += length
+    return answer
+
+
+@pytest.mark.parametrize("bs", [1, 9, 32])
+def test_chain_accept_matches_pure_python(bs):
+    rng = torch.Generator().manual_seed(713)
+    vocab, T, K = 257, 16, 16
+    caps = (torch.arange(bs) % T + 1).tolist()
+    caps[0] = T
+    rows = sum(caps)
+    p = torch.zeros(rows, vocab)
+    support = torch.tensor([0, 2, 3, 7, 11, 13, 15])
+    p[:, support] = torch.softmax(torch.randn(rows, len(support), generator=rng), -1)
+    qids = torch.arange(16).expand(bs, T - 1, K).contiguous()
+    qvals = torch.softmax(torch.randn(bs, T - 1, K, generator=rng), -1)
+    cand = torch.zeros(bs, T, dtype=torch.int64)
+    cand[:, 1:] = torch.multinomial(qvals.reshape(-1, K), 1, generator=rng).view(bs, T - 1)
+    u = torch.full((bs, T - 1), .371)
+    uf = torch.linspace(.071, .917, bs)
+    prefix = torch.arange(bs) + 8191
+    cand[0, 1:] = 0
+    u[0] = 0  # all accepted
+    offsets = np.concatenate(([0], np.cumsum(caps)))[:-1]
+    if bs > 1:  # zero residual with u = 1 must resample p
+        lo, hi = int(offsets[1]), int(offsets[1]) + caps[1]
+        same = torch.softmax(torch.arange(16, dtype=torch.float32), 0)
+        p[lo:hi] = 0
+        p[lo:hi, :16] = same
+        qvals[1] = same
+        u[1] = 1
+    pn = p.numpy()
+    expected = _pure_python_reference(pn.tolist(), cand.tolist(), qids.tolist(), qvals.tolist(), caps,
+                                      u.tolist(), uf.tolist(), prefix.tolist())
+    got = O.chain_accept(lambda r: pn[r], cand.numpy(), qids.numpy(), qvals.numpy(), caps, u.numpy(),
+                         uf.numpy(), prefix.numpy(), row_offsets=offsets)
+    for b, (a, c, bonus, emitted, ns) in enumerate(expected):
+        assert (int(got[0][b]), int(got[1][b]), int(got[2][b]), got[3][b].tolist(), int(got[4][b])) == \
+            (a, c, bonus, emitted, ns), b
+
+
+def test_chain_accept_is_lossless_monte_carlo():
+    """Committed tokens at every reached position follow the target row (chi-square)."""
+    from scipy.stats import chisquare
+
+    rng = np.random.default_rng(0)
+    V, T, K, trials = 12, 4, 4, 20000
+    target = rng.dirichlet(np.ones(V) * 0.7, size=T).astype(np.float32)
+    target[:, 5] = 0
+    target /= target.sum(1, keepdims=True)
+    target = target.astype(np.float32)
+    qids = np.array([[0, 3, 5, 9], [1, 2, 3, 4], [0, 6, 7, 11]])
+    qv = rng.dirichlet(np.ones(K), size=T - 1).astype(np.float32)
+    lanes = np.stack([rng.choice(K, size=trials, p=qv[i] / qv[i].sum()) for i in range(T - 1)], 1)
+    drafts = qids[np.arange(T - 1)[None, :], lanes]
+    cand = np.concatenate([np.zeros((trials, 1), np.int64), drafts], 1)
+    u = rng.random((trials, T - 1), dtype=np.float32)
+    uf = rng.random(trials, dtype=np.float32)
+    out = O.chain_accept(lambda r: target[r % T], cand, np.broadcast_to(qids, (trials, T - 1, K)),
+                         np.broadcast_to(qv, (trials, T - 1, K)), np.full(trials, T), u, uf,
+                         np.zeros(trials), row_offsets=np.arange(trials) * T)
+    acc, output = out[0], out[3]
+    for pos in range(T):
+        toks = output[acc >= pos, pos]
+        counts = np.bincount(toks, minlength=V)
+        assert counts[target[pos] == 0].sum() == 0
+        live = target[pos] > 0
+        exp = target[pos][live] / target[pos][live].sum() * toks.size
+        assert chisquare(counts[live], exp).pvalue > 1e-4, pos
+
+
+# ---------------------------------------------------------------------------------------
+# S4, S6, S8, S10, S11, a19
+# ---------------------------------------------------------------------------------------
+def test_greedy_accept_brute_force():
+    rng = random.Random(3)
+    for _ in range(200):
+        T = rng.randint(1, 6)
+        bs = rng.randint(1, 4)
+        top1 = [[rng.randint(0, 3) for _ in range(T)] for _ in range(bs)]
+        cand = [[rng.randint(0, 3) for _ in range(T)] for _ in range(bs)]
+        caps = [rng.randint(1, T) for _ in range(bs)]
+        got = O.greedy_accept(np.array(top1).reshape(-1), np.array(cand), caps, [5] * bs)
+        for b in range(bs):
+            a = next((i for i in range(caps[b] - 1) if cand[b][i + 1] != top1[b][i]), caps[b] - 1)
+            out = [top1[b][a] if i == a else (cand[b][i + 1] if i < T - 1 else 0) for i in range(T)]
+            assert int(got[0][b]) == a and int(got[2][b]) == top1[b][a] and got[3][b].tolist() == out
+            assert int(got[4][b]) == 5 + a + 1
+
+
+@pytest.mark.parametrize("k", [16, 128])
+def test_topk_known_answer(k):
+    # tests/test_topk_compat.py:70-84
+    scores = torch.arange(257).remainder(7).float().repeat(2, 1)
+    scores[1, 254:] = -torch.inf
+    expected = torch.tensor([sorted(range(257), key=lambda i: (-row[i], i))[:k] for row in scores.tolist()])
+    v, ids = O.topk(scores, k)
+    assert torch.equal(ids, expected) and torch.equal(v, scores.gather(-1, expected))
+
+
+def test_topk_merge_rule():
+    # tests/test_tp_head.py:49-53: [[9, 8, 8]] on ids [0,1,2] and [4,5,6] -> [0, 4, 1, 2]
+    values = torch.tensor([[9.0, 8.0, 8.0, 9.0, 8.0, 8.0]])
+    ids = torch.tensor([[0, 1, 2, 4, 5, 6]])
+    v, pos = O.topk(values, 4)
+    assert ids.gather(-1, pos).tolist() == [[0, 4, 1, 2]] and v.tolist() == [[9, 9, 8, 8]]
+
+
+def test_compress_invariants():
+    p = torch.zeros(3, 40)
+    p[0, [3, 7, 9]] = torch.tensor([.2, .3, .5])
+    p[1, :] = 1 / 40
+    p[2, 5] = -0.1
+    ids, vals, lens, ovf = O.compress(p, 8)
+    assert ids[0, :3].tolist() == [3, 7, 9] and lens.tolist() == [3, 8, 0] and ovf.tolist() == [0, 1, 1]
+    assert ids[0, 3:].tolist() == [-1] * 5 and bool((ids[1, 1:] > ids[1, :-1]).all())
+
+
+def test_window_index_and_kv_slots():
+    lens = [1, 3, 16, 2]
+    assert O.window_index(lens, 16).tolist() == [b * 16 + d for b, n in enumerate(lens) for d in range(n)]
+    pt = np.arange(4 * 30).reshape(4, 30)
+    slots = O.kv_slots(pt, [0, 5, 10, 28], [0, 2, 15, 1], 16)
+    assert slots[1].tolist()[:4] == [35, 36, 37, -1] and slots[3].tolist()[:3] == [118, 119, -1]
+
+
+def test_padding_rows_are_one_point():
+    # tests/test_release.py:45-67
+    padded = O.logits_padding(torch.empty(2, 3), (4, 3))
+    assert torch.equal(padded.softmax(-1), torch.tensor([[1.0, 0.0, 0.0]]).expand(4, 3))
+
+
+def test_sample_chain_ties_to_lower_lane():
+    # tests/test_cuda.py:213-232
+    T, k = 3, 8
+    table = np.zeros((T - 1, k, k), np.float32)
+    table[:, :, 2] = 5.0
+    table[:, :, 6] = 5.0
+    cand = np.arange(k)[None].repeat(T - 1, 0) + 100
+    tok, q = O.sample_chain(table, [1.0], [1], [1.0], [0.0], [0], np.zeros(T - 1), cand, cand[:, 0], T)
+    assert tok.tolist() == [102, 102] and q[:, 2].tolist() == [1.0, 1.0]
+
+
+def test_sample_chain_brute_force_distribution():
+    """The sampled lane follows q exactly: u sweeps [0, 1) and each lane's share equals q."""
+    k, T = 6, 2
+    table = np.random.default_rng(1).normal(size=(1, k, k)).astype(np.float32) * 2
+    cand = np.arange(k)[None] + 10
+    n = 4000
+    us = (np.arange(n) + 0.5) / n
+    counts = np.zeros(k)
+    q_ref = None
+    for uval in us:
+        tok, q = O.sample_chain(table, [1.0], [4], [0.9], [0.0], [0], np.array([uval]), cand, cand[:, 0], T)
+        counts[int(tok[0]) - 10] += 1
+        q_ref = q[0]
+    np.testing.assert_allclose(counts / n, q_ref, atol=2.0 / n)
