@@ -2,20 +2,23 @@
 // residual resample, accepted-prefix compaction and KV-slot gather.
 //
 // Launches of one verify step (no host synchronisation):
-//   k_plan   (1 workgroup)      lists the nucleus rows (top-p / min-p cut with a large top-k)
-//   k_nuc    (side stream)      nucleus rows: one workgroup per row builds an LDS histogram of the
-//                               65536 bf16 values; Z, the top-k/top-p/min-p cut (key + tie count)
-//                               and the normaliser follow from value counts
+//   k_prep   (requests)         penalty bitmap of each request's token history
+//   k_nuc    (side stream)      nucleus rows (a top-p / min-p cut with a large top-k): one
+//                               workgroup per row builds an LDS histogram of the 65536 bf16
+//                               values; Z, the cut (key + tie count) and the normaliser follow
+//                               from value counts
 //   k_chunk  (rows x C)         every other row, in chunks of 20480 bf16 / 10240 fp32 values held
 //                               in registers: max/argmax, softmax partial sums, exact top-k
 //                               candidates -- one nontemporal read of the logits
-//   k_merge  (rows)             per row (one wave): merge the chunk partials -> Z, the filtered
-//                               top-k support (id, P), P at the draft token and the step's
-//                               accept/reject decision
-//   k_bonus  (32 x requests)    accepted length from the row decisions; when the bonus row has a
-//                               dense support, per-chunk residual masses, and the last chunk
-//                               workgroup to finish draws the bonus token; else one workgroup
-//                               draws from the support list.  Writes the outputs and KV slots.
+//   k_merge  (rows)             per row: Z, the filtered top-k support (id, P), P at the draft
+//                               token and the step's accept/reject decision
+//   k_bonus  (chunks x requests) a dense bonus row (unfiltered / nucleus) summed per thread in one
+//                               vector pass
+//   k_final  (requests)         accepted length from the row decisions, the bonus draw (support
+//                               list, or the dense row's chunk -> thread -> element), outputs and
+//                               KV slots
+// Workgroups never wait on one another inside a kernel: on this multi-XCD part a device-scope
+// fence writes back and invalidates the whole L2, so every hand-off is a kernel boundary.
 //
 // Semantics follow runtime/worker.py:440-508 (target P, pytorch backend), sampling/rejection.py
 // :36-98 and sampling/sparse/accept.py:239-307 (chain rejection and residual resample).
@@ -27,24 +30,28 @@
 
 namespace dsv {
 
+constexpr int EPT_MAX = 40;  // bonus elements per thread: vocab <= NCH * BCT * 40 = 327680
+
 struct KParams {
   dsv_verify_args a;
-  RowSum* rowsum;       // [rows]
-  ListEntry* lists;     // [rows, DSV_LIST_K]
-  ChunkStat* cstat;     // [rows, C]
-  uint64_t* cand;       // [rows, C, kcand]
-  BonusChunk* bchunks;  // [bs, NCH]
-  int32_t* qrank;       // [bs, QMAX]
-  int32_t* step_ok;     // [rows]: 1 when the draft token verified by the row is accepted
-  int32_t* done;        // [bs]: chunk workgroups of the bonus row that have finished
-  int32_t* nuc_rows;    // [rows]
-  int32_t* nuc_count;   // [1]
-  int64_t bchunk;       // elements per bonus chunk (multiple of 8)
-  int32_t C;            // chunks per row
-  int32_t kcand;        // candidate slots per chunk
-  int32_t aligned;      // logits rows are 16-byte aligned
-  int32_t force_greedy; // greedy-verify entry: every row is GREEDY
-  int32_t softmax;      // chunk pass computes softmax partial sums
+  RowSum* rowsum;         // [rows]
+  ListEntry* lists;       // [rows, DSV_LIST_K]
+  ChunkStat* cstat;       // [rows, C]
+  uint64_t* cand;         // [rows, C, kcand]
+  BonusChunk* bchunks;    // [bs, NCH]
+  int32_t* qrank;         // [bs, QMAX]: ties at the cut key before the q id, within its chunk
+  double* tmass;          // [bs, NCH * BCT]: per-thread mass of the bonus row above the cut
+  int32_t* tties;         // [bs, NCH * BCT]: per-thread count of values at the cut key
+  int32_t* step_ok;       // [rows]: 1 when the draft token verified by the row is accepted
+  uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
+  int64_t pwords;
+  int64_t bchunk;         // elements per bonus chunk = BCT * ept
+  int32_t ept, nch;       // bonus elements per thread (multiple of 8), bonus chunks
+  int32_t C;              // chunks per row
+  int32_t kcand;          // candidate slots per chunk
+  int32_t aligned;        // logits rows are 16-byte aligned
+  int32_t force_greedy;   // greedy-verify entry: every row is GREEDY
+  int32_t softmax;        // chunk pass computes softmax partial sums (the verify entry)
   int32_t pad;
 };
 
@@ -59,6 +66,39 @@ __device__ __forceinline__ int64_t step_token(const dsv_verify_args& a, int b, i
   return (s < cap - 1 && s + 1 < a.T) ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
 }
 
+// History bits of request b: bit j is set when token j is in the history.
+__device__ __forceinline__ uint32_t pen_word(const KParams& P, int b, int64_t w) {
+  return P.pbits[(int64_t)b * P.pwords + w];
+}
+// Bits of tokens [j, j + n) for j a multiple of n and n in {4, 8}.
+__device__ __forceinline__ uint32_t pen_bits(const KParams& P, int b, int64_t j, int n) {
+  return (pen_word(P, b, j >> 5) >> (j & 31)) & ((1u << n) - 1u);
+}
+__device__ __forceinline__ bool pen_test(const KParams& P, int b, int64_t j) {
+  return (pen_word(P, b, j >> 5) >> (j & 31)) & 1u;
+}
+
+// ---------------------------------------------------------------------------------------
+// k_prep: history bitmaps
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(BCT) void k_prep(KParams P) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  const dsv_verify_args& a = P.a;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  uint32_t* bm = reinterpret_cast<uint32_t*>(dyn);
+  const int words = (int)P.pwords;
+  for (int i = tid; i < words; i += BCT) bm[i] = 0u;
+  __syncthreads();
+  const int32_t* h = a.hist_ids + (int64_t)b * a.hist_len;
+  for (int i = tid; i < a.hist_len; i += BCT) {
+    const int64_t t = h[i];
+    if (t >= 0 && t < a.vocab) atomicOr(&bm[t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  uint32_t* dst = P.pbits + (int64_t)b * P.pwords;
+  for (int i = tid; i < words; i += BCT) dst[i] = bm[i];
+}
+
 // ---------------------------------------------------------------------------------------
 // Candidate refill: the chunk holds more values at or above the admission bound than the
 // LDS buffer.  The K-th largest buffered value is a higher bound; re-read the chunk from
@@ -66,9 +106,9 @@ __device__ __forceinline__ int64_t step_token(const dsv_verify_args& a, int b, i
 // buffered values, so a chunk of at most 20480 values needs at most 80 rounds.
 // ---------------------------------------------------------------------------------------
 template <int DT>
-__device__ __noinline__ int refill_candidates(const char* rowp, int64_t lo, int64_t hi, int K, bool pen,
-                                              const uint32_t* bm, float pres, float rep, uint64_t* cbuf,
-                                              uint32_t* hist256, uint64_t* su, int32_t* cnt) {
+__device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char* rowp, int64_t lo, int64_t hi,
+                                              int K, float pres, float rep, uint64_t* cbuf, uint32_t* hist256,
+                                              uint64_t* su, int32_t* cnt) {
   constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
   int nb = CAND_CAP + 1;
   for (int iter = 0; iter < 128 && nb > CAND_CAP; ++iter) {
@@ -83,7 +123,7 @@ __device__ __noinline__ int refill_candidates(const char* rowp, int64_t lo, int6
     const uint64_t thr = su[0];
     for (int64_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
       float x = load_elem<DT>(rowp, j);
-      if (pen && bitmap_test(bm, j - lo)) x = penalize<DT>(x, pres, rep);
+      if (pbits && ((pbits[j >> 5] >> (j & 31)) & 1u)) x = penalize<DT>(x, pres, rep);
       const uint64_t pk = pack(key_of<DT>(x), j);
       if (pk >= thr) {
         const int slot = atomicAdd(cnt, 1);
@@ -98,6 +138,166 @@ __device__ __noinline__ int refill_candidates(const char* rowp, int64_t lo, int6
 }
 
 // ---------------------------------------------------------------------------------------
+// Row merge (the last chunk workgroup of a row): chunk partials -> RowSum, support list and
+// the step decision.  Rank selection of the row's top-K uses the whole workgroup; the rest
+// runs on wave 0.
+// ---------------------------------------------------------------------------------------
+struct MergeShared {
+  uint64_t buf[16 * DSV_LIST_K];
+  uint64_t top[DSV_LIST_K];
+  int32_t off[17];
+};
+
+template <int DT>
+__device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, int s, int mode, float T, MergeShared& ms) {
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int C = P.C;
+  const ChunkStat* cs = P.cstat + r * C;
+  int kk = 0;
+  if (mode == M_LIST) {
+    const int K = a.top_ks[b] < 1 ? 1 : a.top_ks[b];
+    if (tid == 0) {
+      int o = 0;
+      for (int c = 0; c < C; ++c) {
+        ms.off[c] = o;
+        o += cs[c].ncand;
+      }
+      ms.off[C] = o;
+    }
+    __syncthreads();
+    const int n_all = ms.off[C];
+    for (int c = 0; c < C; ++c) {
+      const int o = ms.off[c], nc = ms.off[c + 1] - o;
+      const uint64_t* src = P.cand + (r * C + c) * (int64_t)P.kcand;
+      for (int i = tid; i < nc; i += CT) ms.buf[o + i] = src[i];
+    }
+    __syncthreads();
+    // rank of each candidate among the row's candidates (values are distinct)
+    for (int i = tid; i < n_all; i += CT) {
+      const uint64_t v = ms.buf[i];
+      int rank = 0;
+      for (int j = 0; j < n_all; ++j) rank += ms.buf[j] > v;
+      if (rank < K) ms.top[rank] = v;
+    }
+    __syncthreads();
+    kk = K < n_all ? K : n_all;
+  }
+  if (tid >= WAVE) return;  // wave 0 finishes the row
+
+  float m_l = -INFINITY;
+  int32_t arg_l = INT_MAX;
+  double s_l = 0.0;
+  if (lane < C) {
+    m_l = cs[lane].m;
+    arg_l = cs[lane].arg;
+    s_l = cs[lane].s;
+  }
+  // the row max and the first id attaining it (chunks cover increasing ids)
+  float M = m_l;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+  const uint64_t at_max = __ballot(lane < C && m_l == M);
+  int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
+  if (arg == INT_MAX) arg = 0;  // every value is -inf: the first id
+  const int64_t tok = step_token(a, b, s);
+  RowSum rs;
+  rs.mode = mode;
+  rs.argmax = arg;
+  rs.kmax = key_of<DT>(M);
+  rs.vcut = 0u;
+  rs.ktie = INT_MAX;
+  rs.nlist = 0;
+  rs.flags = 0;
+  rs.norm = 0;
+  rs.S_f = 1.f;
+  rs.S_kept = 1.0;
+  rs.Z = 1.0;
+  rs.m_f = M;
+  rs.invZ = 1.f;
+  rs.p_draft = 0.f;
+  ListEntry* list = P.lists + r * DSV_LIST_K;
+  if (mode == M_GREEDY) {
+    rs.nlist = 1;
+    rs.p_draft = tok == arg ? 1.f : 0.f;
+    const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
+    if (lane == 0) {
+      list[0] = ListEntry{arg, 1.f};
+      P.rowsum[r] = rs;
+      P.step_ok[r] = ok;
+    }
+    return;
+  }
+  const float c2 = log2e_over(T);
+  const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
+  const float m_f = M / T;
+  const float invZ = (float)(1.0 / Z);
+  rs.Z = Z;
+  rs.m_f = m_f;
+  rs.invZ = invZ;
+  // the draft token's adjusted logit
+  float xt = -INFINITY;
+  if (tok >= 0 && tok < a.vocab) {
+    xt = load_elem<DT>(row_ptr(a, r), tok);
+    if (P.pbits && pen_test(P, b, tok)) {
+      const float pres = a.presence ? a.presence[b] : 0.f;
+      const float rep = a.repetition ? a.repetition[b] : 1.f;
+      xt = penalize<DT>(xt, pres, rep);
+    }
+  }
+  if (mode == M_UNF) {
+    const float p = (tok >= 0 && tok < a.vocab) ? prob_of(xt, T, m_f, invZ) : 0.f;
+    if (a.filter) {  // filtered request with nothing cut: P = p / sum(p)
+      rs.norm = 1;
+      rs.S_kept = Z * (double)invZ;
+      rs.S_f = (float)rs.S_kept;
+      rs.p_draft = p / rs.S_f;
+    } else {
+      rs.p_draft = p;
+    }
+  } else {
+    // LIST: lane j holds the j-th largest candidate
+    const bool live = lane < kk;
+    const uint64_t pk = live ? ms.top[lane] : 0ull;
+    const int32_t id = live ? unpack_id(pk) : INT_MAX;
+    const float p = live ? prob_of(value_of_key<DT>(unpack_key(pk)), T, m_f, invZ) : 0.f;
+    double lo_p, hi_p;
+    const double S_all = wave_tiles((double)p, lo_p, hi_p);
+    const float top_p = a.top_ps[b];
+    const float min_p = a.min_ps ? a.min_ps[b] : 0.f;
+    bool keep = live && lane < a.top_ks[b] && !topp_fails(a.backend, lo_p, p, top_p);
+    if (a.need_min_p) {
+      if (a.backend == DSV_BACKEND_FLASHINFER) {
+        // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
+        double lo_a, hi_a;
+        wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
+        keep = live && lane < a.top_ks[b] && lo_a <= (double)top_p;
+      }
+      const float thr = __shfl(p, 0, WAVE) * min_p;
+      if (p < thr) keep = false;
+    }
+    const double Sk = wave_sum(keep ? (double)p : 0.0);
+    const float S_f = (float)Sk;
+    rs.S_kept = Sk;
+    rs.S_f = S_f;
+    const float Pj = p / S_f;
+    const uint64_t at_tok = __ballot(keep && (int64_t)id == tok);
+    rs.p_draft = at_tok ? __shfl(Pj, __ffsll((long long)at_tok) - 1, WAVE) : 0.f;
+    // the kept support, sorted by id
+    const int32_t kid = keep ? id : INT_MAX;
+    int rank = 0;
+    for (int i = 0; i < kk; ++i) rank += __shfl(kid, i, WAVE) < kid;
+    if (keep) list[rank] = ListEntry{id, Pj};
+    rs.nlist = __popcll(__ballot(keep));
+  }
+  const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
+  if (lane == 0) {
+    P.rowsum[r] = rs;
+    P.step_ok[r] = ok;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // k_chunk: one pass over a 20480-value (bf16) / 10240-value (fp32) chunk held in registers
 // ---------------------------------------------------------------------------------------
 template <int DT>
@@ -107,7 +307,6 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
   __shared__ uint64_t cbuf[CAND_CAP];
   __shared__ uint64_t top[TOPK_MAX];
-  __shared__ uint32_t bm[CHE / 32];
   __shared__ uint32_t hist256[256];
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
@@ -123,6 +322,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     if (P.softmax) {
       if (!row_request(a, r, b, s)) return;
       b = __builtin_amdgcn_readfirstlane(b);
+      s = __builtin_amdgcn_readfirstlane(s);
       mode = row_mode(a, b, 0);
       if (mode == M_HIST) return;
     } else {
@@ -142,20 +342,23 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 #pragma unroll
   for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, aligned);
 
-  const bool pen = P.softmax && a.hist_ids != nullptr;
+  const bool pen = P.softmax && P.pbits != nullptr;
   float pres = 0.f, rep = 1.f;
   if (pen) {
-    build_bitmap(a, b, lo, CHE / 32, bm);
     pres = a.presence ? a.presence[b] : 0.f;
     rep = a.repetition ? a.repetition[b] : 1.f;
+    uint32_t bits[CV];
 #pragma unroll
     for (int u = 0; u < CV; ++u) {
-      const int64_t o = (int64_t)u * CT * n + (int64_t)tid * n;  // offset of the vector in the chunk
-      const uint32_t bits = (bm[o >> 5] >> (o & 31)) & ((1u << n) - 1u);
-      if (bits) {
+      const int64_t j = (v0 + (int64_t)u * CT + tid) * n;
+      bits[u] = j < hi ? pen_bits(P, b, j, n) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      if (bits[u]) {
 #pragma unroll
         for (int e = 0; e < n; ++e)
-          if ((bits >> e) & 1u) vec_set<DT>(v[u], e, penalize<DT>(vec_elem<DT>(v[u], e), pres, rep));
+          if ((bits[u] >> e) & 1u) vec_set<DT>(v[u], e, penalize<DT>(vec_elem<DT>(v[u], e), pres, rep));
       }
     }
   }
@@ -249,7 +452,9 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
     __syncthreads();
     int nb = s_cnt;
-    if (nb > CAND_CAP) nb = refill_candidates<DT>(rowp, lo, hi, K, pen, bm, pres, rep, cbuf, hist256, su, &s_cnt);
+    if (nb > CAND_CAP)
+      nb = refill_candidates<DT>(pen ? P.pbits + (int64_t)b * P.pwords : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
+                                 hist256, su, &s_cnt);
     const int kk = select_top<TOP_SHIFT>(cbuf, nb, K, top, hist256, su, &s_cnt2);
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;
     for (int i = tid; i < kk; i += CT) dst[i] = cbuf[i];
@@ -259,186 +464,24 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 }
 
 // ---------------------------------------------------------------------------------------
-// k_merge: per row, chunk partials -> RowSum and the step decision (one wave per row)
+// k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0)
 // ---------------------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(WAVE) void k_merge(KParams P) {
-  constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
-  __shared__ uint64_t buf[16 * DSV_LIST_K];
-  __shared__ uint64_t top[DSV_LIST_K];
-  __shared__ int32_t s_ids[DSV_LIST_K];
-  __shared__ uint32_t hist256[256];
-  __shared__ uint64_t su[2];
-  __shared__ int32_t s_cnt;
+__global__ __launch_bounds__(CT) void k_merge(KParams P) {
+  __shared__ MergeShared ms;
   const dsv_verify_args& a = P.a;
   const int64_t r = blockIdx.x;
-  const int lane = threadIdx.x;
   int b, s;
   if (!row_request(a, r, b, s)) {
-    if (lane == 0) {
+    if (threadIdx.x == 0) {
       P.rowsum[r].mode = M_SKIP;
       P.step_ok[r] = 0;
     }
     return;
   }
-  if (s == 0 && lane == 0) P.done[b] = 0;
-  const int mode = row_mode(a, b, P.force_greedy);
+  const int mode = row_mode(a, b, 0);
   if (mode == M_HIST) return;  // k_nuc
-  const int C = P.C;
-  const ChunkStat* cs = P.cstat + r * C;
-  float m_l = -INFINITY;
-  int32_t arg_l = INT_MAX, nc_l = 0;
-  double s_l = 0.0;
-  if (lane < C) {
-    m_l = cs[lane].m;
-    arg_l = cs[lane].arg;
-    s_l = cs[lane].s;
-    nc_l = cs[lane].ncand;
-  }
-  // the row max and the first id attaining it (chunks cover increasing ids)
-  float M = m_l;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
-  const uint64_t at_max = __ballot(lane < C && m_l == M);
-  int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
-  if (arg == INT_MAX) arg = 0;  // every value is -inf: the first id
-  const int64_t tok = step_token(a, b, s);
-  const char* rowp = row_ptr(a, r);
-  RowSum rs;
-  rs.mode = mode;
-  rs.argmax = arg;
-  rs.kmax = key_of<DT>(M);
-  rs.vcut = 0u;
-  rs.ktie = INT_MAX;
-  rs.nlist = 0;
-  rs.flags = 0;
-  rs.norm = 0;
-  rs.S_f = 1.f;
-  rs.S_kept = 1.0;
-  rs.Z = 1.0;
-  rs.m_f = M;
-  rs.invZ = 1.f;
-  rs.p_draft = 0.f;
-  ListEntry* list = P.lists + r * DSV_LIST_K;
-  if (mode == M_GREEDY) {
-    rs.nlist = 1;
-    rs.p_draft = tok == arg ? 1.f : 0.f;
-    const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
-    if (lane == 0) {
-      list[0] = ListEntry{arg, 1.f};
-      P.rowsum[r] = rs;
-      P.step_ok[r] = ok;
-    }
-    return;
-  }
-  const float T = a.temperatures[b];
-  const float c2 = log2e_over(T);
-  const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
-  const float m_f = M / T;
-  const float invZ = (float)(1.0 / Z);
-  rs.Z = Z;
-  rs.m_f = m_f;
-  rs.invZ = invZ;
-  // the draft token's adjusted logit
-  float xt = -INFINITY;
-  if (tok >= 0 && tok < a.vocab) {
-    xt = load_elem<DT>(rowp, tok);
-    if (a.hist_ids && in_history_wave(a, b, tok)) {
-      const float pres = a.presence ? a.presence[b] : 0.f;
-      const float rep = a.repetition ? a.repetition[b] : 1.f;
-      xt = penalize<DT>(xt, pres, rep);
-    }
-  }
-  if (mode == M_UNF) {
-    const float p = (tok >= 0 && tok < a.vocab) ? prob_of(xt, T, m_f, invZ) : 0.f;
-    if (a.filter) {  // filtered request with nothing cut: P = p / sum(p)
-      rs.norm = 1;
-      rs.S_kept = Z * (double)invZ;
-      rs.S_f = (float)rs.S_kept;
-      rs.p_draft = p / rs.S_f;
-    } else {
-      rs.p_draft = p;
-    }
-  } else {
-    // LIST: gather the chunk candidates and select the row's top-K (sorted, value desc / id asc)
-    const int K = a.top_ks[b] < 1 ? 1 : a.top_ks[b];
-    int nc_excl = nc_l;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int t = __shfl_up(nc_excl, o, WAVE);
-      if (lane >= o) nc_excl += t;
-    }
-    const int n_all = __shfl(nc_excl, WAVE - 1, WAVE);
-    nc_excl -= nc_l;
-    for (int cc = 0; cc < C; ++cc) {
-      const int nc = __shfl(nc_l, cc, WAVE);
-      const int off = __shfl(nc_excl, cc, WAVE);
-      const uint64_t* src = P.cand + (r * C + cc) * (int64_t)P.kcand;
-      for (int i = lane; i < nc; i += WAVE) buf[off + i] = src[i];
-    }
-    __syncthreads();
-    const int kk = select_top<TOP_SHIFT>(buf, n_all, K, top, hist256, su, &s_cnt);
-    // lane j holds the j-th largest
-    const bool live = lane < kk;
-    const uint64_t pk = live ? buf[lane] : 0ull;
-    const int32_t id = live ? unpack_id(pk) : INT_MAX;
-    const float p = live ? prob_of(value_of_key<DT>(unpack_key(pk)), T, m_f, invZ) : 0.f;
-    double lo_p, hi_p;
-    const double S_all = wave_tiles((double)p, lo_p, hi_p);
-    const float top_p = a.top_ps[b];
-    const float min_p = a.min_ps ? a.min_ps[b] : 0.f;
-    bool keep = live && lane < a.top_ks[b] && !topp_fails(a.backend, lo_p, p, top_p);
-    if (a.need_min_p) {
-      if (a.backend == DSV_BACKEND_FLASHINFER) {
-        // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
-        double lo_a, hi_a;
-        wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
-        keep = live && lane < a.top_ks[b] && lo_a <= (double)top_p;
-      }
-      const float thr = __shfl(p, 0, WAVE) * min_p;
-      if (p < thr) keep = false;
-    }
-    const double Sk = wave_sum(keep ? (double)p : 0.0);
-    const float S_f = (float)Sk;
-    rs.S_kept = Sk;
-    rs.S_f = S_f;
-    const float Pj = p / S_f;
-    const uint64_t at_tok = __ballot(keep && (int64_t)id == tok);
-    rs.p_draft = at_tok ? __shfl(Pj, __ffsll((long long)at_tok) - 1, WAVE) : 0.f;
-    // the kept support, sorted by id
-    s_ids[lane] = keep ? id : INT_MAX;
-    __syncthreads();
-    int rank = 0;
-    for (int i = 0; i < kk; ++i) rank += s_ids[i] < id;
-    if (keep) list[rank] = ListEntry{id, Pj};
-    rs.nlist = __popcll(__ballot(keep));
-  }
-  const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
-  if (lane == 0) {
-    P.rowsum[r] = rs;
-    P.step_ok[r] = ok;
-  }
-}
-
-// ---------------------------------------------------------------------------------------
-// k_plan: deterministic list of the nucleus rows
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_plan(KParams P) {
-  __shared__ int32_t red[32];
-  const dsv_verify_args& a = P.a;
-  int32_t base = 0;
-  for (int64_t r0 = 0; r0 < a.rows; r0 += 1024) {
-    const int64_t r = r0 + threadIdx.x;
-    int b, s;
-    int32_t f = 0;
-    if (r < a.rows && row_request(a, r, b, s)) f = row_mode(a, b, 0) == M_HIST;
-    int32_t tot = 0;
-    const int32_t pos = block_excl_scan<16>(f, red, &tot);
-    if (f) P.nuc_rows[base + pos] = (int32_t)r;
-    base += tot;
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) *P.nuc_count = base;
+  merge_row<DT>(P, r, b, s, mode, a.temperatures[b], ms);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -455,6 +498,9 @@ struct NucShared {
   uint64_t u[NUC_WAVES];
   uint64_t cut[NUC_WAVES];  // (tie << 32 | key) of each wave's first failing key, ~0 if none
   double cutS[NUC_WAVES];
+  int32_t ri[NUC_WAVES];
+  int32_t mine[NUC_THREADS];  // this workgroup's rows among the current 512
+  int32_t nmine;
   float xtok;
   uint32_t ktok;
 };
@@ -467,7 +513,7 @@ __device__ __forceinline__ int nuc_word(int wid, int i, int lane) {
 }
 
 template <int DT>
-__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, uint32_t* bm, NucShared& sh) {
+__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   int b = 0, s = 0;
@@ -477,7 +523,7 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   const bool aligned = P.aligned != 0;
   const float T = a.temperatures[b];
   const int topk = a.top_ks[b];
-  const bool pen = a.hist_ids != nullptr;
+  const bool pen = P.pbits != nullptr;
   float pres = 0.f, rep = 1.f;
   {
     uint4* h4 = reinterpret_cast<uint4*>(hist);
@@ -486,14 +532,13 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   if (pen) {
     pres = a.presence ? a.presence[b] : 0.f;
     rep = a.repetition ? a.repetition[b] : 1.f;
-    build_bitmap(a, b, 0, (int)((V + 31) / 32), bm);
   }
   const int64_t tok = step_token(a, b, s);
   if (tid == 0) {
     float xt = -INFINITY;
     if (tok >= 0 && tok < V) {
       xt = load_elem<DT>(rowp, tok);
-      if (pen && bitmap_test(bm, tok)) xt = penalize<DT>(xt, pres, rep);
+      if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
     }
     sh.xtok = xt;
     sh.ktok = key_of<DT>(xt);
@@ -506,19 +551,22 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   uint32_t tie_before = 0, nfin = 0;
   for (int64_t q0 = 0; q0 < NVt; q0 += (int64_t)NUC_THREADS * U) {
     uint4 w[U];
+    uint32_t bits[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = load_vec<DT>(rowp, q0 + (int64_t)u * NUC_THREADS + tid, V, aligned);
+    for (int u = 0; u < U; ++u) {
+      const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
+      w[u] = load_vec<DT>(rowp, vi, V, aligned);
+      bits[u] = (pen && vi < NVt) ? pen_bits(P, b, vi * 8, 8) : 0u;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
       if (vi >= NVt) continue;
-      uint32_t bits = 0;
-      if (pen) bits = (bm[vi >> 2] >> ((vi & 3) * 8)) & 0xFFu;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int64_t j = vi * 8 + e;
         float x = vec_elem<DT>(w[u], e);
-        if ((bits >> e) & 1u) x = penalize<DT>(x, pres, rep);
+        if ((bits[u] >> e) & 1u) x = penalize<DT>(x, pres, rep);
         const uint32_t k = key_of<DT>(x);
         if (j < V) {
           const uint64_t pk = pack(k, j);
@@ -703,21 +751,42 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   __syncthreads();
 }
 
+// Persistent workgroups: the i-th nucleus row in row order goes to workgroup i % gridDim.x.
 template <int DT>
 __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ NucShared sh;
+  const dsv_verify_args& a = P.a;
   uint32_t* hist = reinterpret_cast<uint32_t*>(dyn);
-  uint32_t* bm = reinterpret_cast<uint32_t*>(dyn + (size_t)HIST_WORDS * 4);
-  const int count = *P.nuc_count;
-  for (int i = blockIdx.x; i < count; i += gridDim.x) {
-    if constexpr (DT == DSV_BF16) nuc_row<DT>(P, P.nuc_rows[i], hist, bm, sh);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
+  int64_t seen = 0;  // nucleus rows before the current block of rows
+  for (int64_t r0 = 0; r0 < a.rows; r0 += NUC_THREADS) {
+    const int64_t r = r0 + tid;
+    int b, s;
+    const bool f = r < a.rows && row_request(a, r, b, s) && row_mode(a, b, 0) == M_HIST;
+    const uint64_t bal = __ballot(f);
+    if (lane == 0) sh.ri[wid] = __popcll(bal);
+    if (tid == 0) sh.nmine = 0;
+    __syncthreads();
+    int64_t before = seen, total = 0;
+    for (int i = 0; i < NUC_WAVES; ++i) {
+      if (i < wid) before += sh.ri[i];
+      total += sh.ri[i];
+    }
+    const int64_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
+    if (f && rank % gridDim.x == blockIdx.x) sh.mine[atomicAdd(&sh.nmine, 1)] = (int32_t)r;
+    __syncthreads();
+    const int nm = sh.nmine;
+    for (int i = 0; i < nm; ++i) {
+      if constexpr (DT == DSV_BF16) nuc_row<DT>(P, sh.mine[i], hist, sh);
+    }
+    seen += total;
+    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// k_bonus: accepted length, bonus draw and outputs
-// (sampling/sparse/accept.py:249-307 and :179-204; runtime/worker.py:1048-1089)
+// Bonus draw helpers
 // ---------------------------------------------------------------------------------------
 // P at one element of a dense-support bonus row.
 __device__ __forceinline__ double dense_P(const RowSum& rs, float T, float x) {
@@ -725,20 +794,8 @@ __device__ __forceinline__ double dense_P(const RowSum& rs, float T, float x) {
   return (rs.mode == M_HIST || rs.norm) ? (double)(p / rs.S_f) : (double)p;
 }
 
-struct BonusShared {
-  double red_d[BCT / WAVE];
-  int32_t red_i[BCT / WAVE];
-  uint64_t red_u[BCT / WAVE];
-  int64_t qid[QMAX];
-  float qv[QMAX];       // clamped q of the lane
-  int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
-  int32_t qrank[QMAX];
-  int64_t bonus;
-  double chunk_lo, thr;
-  int32_t acc, last, chunk, tieq, use_r, claimed;
-};
 
-__device__ void write_outputs(const dsv_verify_args& a, int b, int acc, int64_t bonus) {
+__device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, int acc, int64_t bonus) {
   const int T = a.T;
   for (int i = threadIdx.x; i < T; i += blockDim.x) {
     int64_t val = 0;
@@ -764,24 +821,68 @@ __device__ void write_outputs(const dsv_verify_args& a, int b, int acc, int64_t 
   }
 }
 
+// The elements [lo_t, lo_t + cnt) of a thread's bonus range, penalised, as floats.
 template <int DT>
-__global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
-  extern __shared__ __align__(16) unsigned char dyn[];  // penalty bitmap
-  __shared__ BonusShared sh;
+__device__ __forceinline__ void load_range(const KParams& P, int b, const char* rowp, int64_t lo_t, int64_t hi_t,
+                                           float pres, float rep, float (&x)[EPT_MAX]) {
+  constexpr int n = Elems<DT>::n;
+  constexpr int NV = EPT_MAX / n;
+  uint4 v[NV];
+  const int nv = (P.ept + n - 1) / n;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+    v[u] = u < nv ? load_vec<DT>(rowp, lo_t / n + u, hi_t, P.aligned != 0) : make_uint4(0, 0, 0, 0);
+  uint64_t bits = 0;
+  if (P.pbits && lo_t < hi_t) {
+    const int64_t w0 = lo_t >> 5;
+    bits = pen_word(P, b, w0);
+    if (w0 + 1 < P.pwords) bits |= (uint64_t)pen_word(P, b, w0 + 1) << 32;
+    bits >>= (lo_t & 31);
+  }
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+#pragma unroll
+    for (int e = 0; e < n; ++e) {
+      const int i = u * n + e;
+      float xv = vec_elem<DT>(v[u], e);
+      if ((bits >> i) & 1ull) xv = penalize<DT>(xv, pres, rep);
+      x[i] = xv;
+    }
+}
+
+// Accepted length of request b: the first rejected step (all threads get it; uses sh.acc).
+struct BonusShared {
+  double red_d[BCT / WAVE];
+  int32_t red_i[BCT / WAVE];
+  uint64_t red_u[BCT / WAVE];
+  int64_t qid[QMAX];
+  float qv[QMAX];       // clamped q of the lane
+  int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
+  double qd[QMAX];      // P - max(P - q, 0) of a kept q id (the residual's reduction), else 0
+  int64_t bonus;
+  double chunk_lo, thr;
+  int32_t acc, chunk, tieq, use_r, pick_thread;
+};
+
+struct ReqView {
+  int64_t row0;
+  int cap, acc;
+  bool rows_ok, all;
+};
+
+__device__ __forceinline__ ReqView request_view(const KParams& P, int b, BonusShared& sh) {
   const dsv_verify_args& a = P.a;
-  const int b = blockIdx.y, c = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-  const int64_t V = a.vocab;
-  const int64_t row0 = request_row0(a, b);
-  int cap = req_cap(a, b);
-  const bool rows_ok = row0 >= 0 && row0 < a.rows;
-  if (rows_ok && row0 + cap > a.rows) cap = (int)(a.rows - row0);
-  // accepted length: the first rejected step
+  ReqView q;
+  q.row0 = request_row0(a, b);
+  q.cap = req_cap(a, b);
+  q.rows_ok = q.row0 >= 0 && q.row0 < a.rows;
+  if (q.rows_ok && q.row0 + q.cap > a.rows) q.cap = (int)(a.rows - q.row0);
   if (tid < WAVE) {
-    int acc = rows_ok ? cap - 1 : 0;
+    int acc = q.rows_ok ? q.cap - 1 : 0;
     for (int s0 = 0; s0 < acc; s0 += WAVE) {
       const int s = s0 + lane;
-      const uint64_t rej = __ballot(s < cap - 1 && P.step_ok[row0 + s] == 0);
+      const uint64_t rej = __ballot(s < q.cap - 1 && P.step_ok[q.row0 + s] == 0);
       if (rej) {
         acc = s0 + __ffsll((long long)rej) - 1;
         break;
@@ -790,36 +891,123 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
     if (tid == 0) sh.acc = acc;
   }
   __syncthreads();
-  const int acc = sh.acc;
-  if (!rows_ok) {  // inconsistent row offsets: no row of this request can be read
-    if (c == 0) write_outputs(a, b, 0, V - 1);
-    return;
-  }
-  const bool all = acc == cap - 1;
-  const int64_t rstar = row0 + acc;
-  const RowSum rs = P.rowsum[rstar];
-  const bool dense = rs.mode == M_UNF || rs.mode == M_HIST;
-  if (!dense && c != 0) return;
-  const int64_t qi = ((int64_t)b * (a.T - 1) + acc) * a.K;
-  for (int l = tid; l < QMAX; l += BCT) {
-    const bool live = !all && l < a.K;
+  q.acc = sh.acc;
+  q.all = q.acc == q.cap - 1;
+  return q;
+}
+
+// Stage the sparse q of the rejected step: ids, clamped values, and which lane of a repeated
+// id carries the residual's q (the last one).
+__device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, const ReqView& q, BonusShared& sh) {
+  const int tid = threadIdx.x;
+  const int64_t qi = ((int64_t)b * (a.T - 1) + q.acc) * a.K;
+  for (int l = tid; l < QMAX; l += blockDim.x) {
+    const bool live = !q.all && l < a.K;
     sh.qid[l] = live ? load_index(a.q_ids, a.q_ids_i64, qi + l) : -1;
     sh.qv[l] = live ? clamp01(a.q_values[qi + l]) : 0.f;
-    sh.qrank[l] = 0;
+    sh.qd[l] = 0.0;
   }
   __syncthreads();
-  for (int l = tid; l < QMAX; l += BCT) {
-    bool last = sh.qid[l] >= 0 && sh.qid[l] < V;
+  for (int l = tid; l < QMAX; l += blockDim.x) {
+    bool last = sh.qid[l] >= 0 && sh.qid[l] < a.vocab;
     for (int l2 = l + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != sh.qid[l];
     sh.qlast[l] = last;
   }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------
+// k_bonus: per-thread masses of each dense bonus row (one vector pass; chunks x requests)
+// ---------------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
+  __shared__ BonusShared sh;
+  const dsv_verify_args& a = P.a;
+  const int b = blockIdx.y, c = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  const ReqView q = request_view(P, b, sh);
+  if (!q.rows_ok) return;
+  const int64_t rstar = q.row0 + q.acc;
+  const RowSum rs = P.rowsum[rstar];
+  if (rs.mode != M_UNF && rs.mode != M_HIST) return;  // support list: drawn by k_final
+  const bool hist_mode = rs.mode == M_HIST;
+  if (hist_mode && !q.all) stage_q(a, b, q, sh);
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const float T = a.temperatures[b];
+  const char* rowp = row_ptr(a, rstar);
+  const int ept = P.ept;
+  const int64_t lo_t = (int64_t)c * P.bchunk + (int64_t)tid * ept;
+  const int64_t hi_t = lo_t + ept < V ? lo_t + ept : V;
+  const int cnt = hi_t > lo_t ? (int)(hi_t - lo_t) : 0;
+  float x[EPT_MAX];
+  load_range<DT>(P, b, rowp, lo_t, hi_t, pres, rep, x);
+  double mgt = 0.0;
+  int32_t ties = 0;
+#pragma unroll
+  for (int i = 0; i < EPT_MAX; ++i) {
+    if (i < cnt) {
+      const uint32_t k = key_of<DT>(x[i]);
+      if (!hist_mode || k > rs.vcut)
+        mgt += dense_P(rs, T, x[i]);
+      else if (k == rs.vcut)
+        ++ties;
+    }
+  }
+  int32_t tie_tot = 0;
+  const int32_t tie_before = block_excl_scan<BCT / WAVE>(ties, sh.red_i, &tie_tot);
+  const double msum = block_sum<BCT / WAVE>(mgt, sh.red_d);
+  const int64_t slot = (int64_t)b * NCH * BCT + (int64_t)c * BCT + tid;
+  P.tmass[slot] = mgt;
+  P.tties[slot] = ties;
+  if (tid == 0) P.bchunks[(int64_t)b * NCH + c] = BonusChunk{msum, tie_tot, 0};
+  // chunk-relative tie rank of each q id that sits at the cut key in this thread's range
+  if (hist_mode && !q.all && ties)
+    for (int l = 0; l < a.K; ++l) {
+      const int64_t id = sh.qid[l];
+      if (id < lo_t || id >= hi_t) continue;
+      int32_t before = 0;
+      bool at_cut = false;
+#pragma unroll
+      for (int i = 0; i < EPT_MAX; ++i)
+        if (i < cnt && key_of<DT>(x[i]) == rs.vcut) {
+          if (lo_t + i < id) ++before;
+          if (lo_t + i == id) at_cut = true;
+        }
+      if (at_cut) P.qrank[(int64_t)b * QMAX + l] = tie_before + before;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// k_final: bonus draw and outputs, one workgroup per request
+// (sampling/sparse/accept.py:249-307 and :179-204; runtime/worker.py:1048-1089)
+// ---------------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(BCT) void k_final(KParams P) {
+  __shared__ BonusShared sh;
+  const dsv_verify_args& a = P.a;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int64_t V = a.vocab;
+  const ReqView q = request_view(P, b, sh);
+  if (!q.rows_ok) {  // inconsistent row offsets: no row of this request can be read
+    write_outputs(a, b, 0, V - 1);
+    return;
+  }
+  const int acc = q.acc;
+  const bool all = q.all;
+  const int64_t rstar = q.row0 + acc;
+  const RowSum rs = P.rowsum[rstar];
+  const bool dense = rs.mode == M_UNF || rs.mode == M_HIST;
+  stage_q(a, b, q, sh);
   const float uf = a.uniform_final[b];
   const float T = a.temperatures[b];
   const char* rowp = row_ptr(a, rstar);
 
   if (!dense) {
     // support list (GREEDY / LIST rows): lanes hold the entries, sorted by id
-    __syncthreads();
     if (tid < WAVE) {
       const bool live = lane < rs.nlist;
       const ListEntry e = live ? P.lists[rstar * DSV_LIST_K + lane] : ListEntry{INT_MAX, 0.f};
@@ -842,58 +1030,14 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
     return;
   }
 
-  // ---- dense support: residual mass of chunk c --------------------------------------------
-  const bool pen = a.hist_ids != nullptr;
-  float pres = 0.f, rep = 1.f;
-  if (pen) {
-    pres = a.presence ? a.presence[b] : 0.f;
-    rep = a.repetition ? a.repetition[b] : 1.f;
-  }
-  uint32_t* bm = reinterpret_cast<uint32_t*>(dyn);
-  const int64_t lo = (int64_t)c * P.bchunk;
-  const int64_t hi = lo + P.bchunk < V ? lo + P.bchunk : V;
-  if (pen)
-    build_bitmap(a, b, lo, (int)((P.bchunk + 31) / 32), bm);
-  else
-    __syncthreads();
-  double mass = 0.0;
-  int32_t ties = 0;
-  for (int64_t j = lo + tid; j < hi; j += BCT) {
-    float x = load_elem<DT>(rowp, j);
-    if (pen && bitmap_test(bm, j - lo)) x = penalize<DT>(x, pres, rep);
-    if (rs.mode == M_UNF) {
-      mass += dense_P(rs, T, x);
-    } else {
-      const uint32_t k = key_of<DT>(x);
-      if (k > rs.vcut) {
-        mass += dense_P(rs, T, x);
-      } else if (k == rs.vcut) {
-        ++ties;
-        if (!all)
-          for (int l = 0; l < a.K; ++l)
-            if (sh.qid[l] > j && sh.qid[l] >= lo && sh.qid[l] < hi) atomicAdd(&sh.qrank[l], 1);
-      }
-    }
-  }
-  const double msum = block_sum<BCT / WAVE>(mass, sh.red_d);
-  const int32_t tsum = block_sum<BCT / WAVE>(ties, sh.red_i);
-  if (tid == 0) P.bchunks[(int64_t)b * NCH + c] = BonusChunk{msum, tsum, 0};
-  if (!all && rs.mode == M_HIST)
-    for (int l = tid; l < a.K; l += BCT)
-      if (sh.qid[l] >= lo && sh.qid[l] < hi) P.qrank[(int64_t)b * QMAX + l] = sh.qrank[l];
-  // the last chunk workgroup to finish draws the bonus token
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    sh.last = atomicAdd(&P.done[b], 1) == NCH - 1;
-    if (sh.last) P.done[b] = 0;  // every chunk has counted: ready for the next call
-  }
-  __syncthreads();
-  if (!sh.last) return;
-  __threadfence();
-  if (pen) build_bitmap(a, b, 0, (int)((V + 31) / 32), bm);
-  const int nch = (int)((V + P.bchunk - 1) / P.bchunk);
-  const double P_cut = rs.mode == M_HIST ? dense_P(rs, T, value_of_key<DT>(rs.vcut)) : 0.0;
+  // ---- dense support: chunk masses from k_bonus ---------------------------------------------
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const bool hist_mode = rs.mode == M_HIST;
+  const int ept = P.ept;
+  const int nch = P.nch;
+  const double P_cut = hist_mode ? dense_P(rs, T, value_of_key<DT>(rs.vcut)) : 0.0;
   if (tid < WAVE) {
     // lanes hold the chunks
     BonusChunk bc = BonusChunk{0.0, 0, 0};
@@ -905,32 +1049,33 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
       if (lane >= o) tie_prefix += t;
     }
     tie_prefix -= bc.ties;
+    // the residual's reduction at each q id (lanes hold the q lanes)
+    const bool qlive = !all && lane < a.K && sh.qlast[lane];
+    const int64_t qid = qlive ? sh.qid[lane] : 0;
+    const int32_t tp = __shfl(tie_prefix, (int)(qid / P.bchunk), WAVE);
+    if (qlive) {
+      float xq = load_elem<DT>(rowp, qid);
+      if (pen && pen_test(P, b, qid)) xq = penalize<DT>(xq, pres, rep);
+      const uint32_t k = key_of<DT>(xq);
+      const bool kept =
+          !hist_mode || k > rs.vcut ||
+          (k == rs.vcut && (int64_t)tp + P.qrank[(int64_t)b * QMAX + lane] < (int64_t)rs.ktie);
+      const double Pq = kept ? dense_P(rs, T, xq) : 0.0;
+      sh.qd[lane] = Pq - fmax(Pq - (double)sh.qv[lane], 0.0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     int32_t kt = 0;
-    if (rs.mode == M_HIST) {
+    if (hist_mode) {
       const int64_t room = (int64_t)rs.ktie - tie_prefix;
       kt = room <= 0 ? 0 : (room < bc.ties ? (int32_t)room : bc.ties);
     }
     const double Mp = bc.mass + (kt > 0 ? (double)kt * P_cut : 0.0);
     double Mr = Mp;
-    if (!all && lane < nch) {
-      for (int l = 0; l < a.K; ++l) {
-        if (!sh.qlast[l]) continue;
-        const int64_t id = sh.qid[l];
-        if (id / P.bchunk != lane) continue;
-        float x = load_elem<DT>(rowp, id);
-        if (pen && bitmap_test(bm, id)) x = penalize<DT>(x, pres, rep);
-        double Pq = 0.0;
-        if (rs.mode == M_UNF) {
-          Pq = dense_P(rs, T, x);
-        } else {
-          const uint32_t k = key_of<DT>(x);
-          const bool kept = k > rs.vcut ||
-                            (k == rs.vcut && (int64_t)tie_prefix + P.qrank[(int64_t)b * QMAX + l] < (int64_t)rs.ktie);
-          Pq = kept ? dense_P(rs, T, x) : 0.0;
-        }
-        Mr -= Pq - fmax(Pq - (double)sh.qv[l], 0.0);
-      }
-    }
+    if (!all && lane < nch)
+      for (int l = 0; l < a.K; ++l)
+        if (sh.qlast[l] && sh.qid[l] / P.bchunk == lane) Mr -= sh.qd[l];
     double lo_r, hi_r, lo_p, hi_p;
     const double mr = wave_tiles(lane < nch ? Mr : 0.0, lo_r, hi_r);
     const double mp = wave_tiles(lane < nch ? Mp : 0.0, lo_p, hi_p);
@@ -944,6 +1089,7 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
       sh.thr = thr;
       sh.use_r = use_r ? 1 : 0;
       sh.bonus = V - 1;
+      sh.pick_thread = -1;
     }
     if (cstar >= 0 && lane == cstar) {
       sh.chunk_lo = clo;
@@ -952,80 +1098,69 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
   }
   __syncthreads();
   const int cstar = sh.chunk;
-  if (cstar >= 0) {
-    const bool use_r = sh.use_r != 0;
-    const int64_t clo = (int64_t)cstar * P.bchunk;
-    const int64_t chi = clo + P.bchunk < V ? clo + P.bchunk : V;
-    const int64_t per = (chi - clo + BCT - 1) / BCT;
-    const int64_t mlo = clo + per * tid < chi ? clo + per * tid : chi;
-    const int64_t mhi = mlo + per < chi ? mlo + per : chi;
-    auto value = [&](int64_t j) -> float {
-      float x = load_elem<DT>(rowp, j);
-      if (pen && bitmap_test(bm, j)) x = penalize<DT>(x, pres, rep);
-      return x;
-    };
-    int32_t my_ties = 0;
-    if (rs.mode == M_HIST)
-      for (int64_t j = mlo; j < mhi; ++j) my_ties += key_of<DT>(value(j)) == rs.vcut;
-    int32_t tie_tot = 0;
-    const int32_t tie_before = block_excl_scan<BCT / WAVE>(my_ties, sh.red_i, &tie_tot);
-    const int32_t tieq = sh.tieq;
-    auto weight = [&](int64_t j, int32_t& tie_seen) -> double {
-      const float x = value(j);
+  if (cstar < 0) {
+    write_outputs(a, b, acc, sh.bonus);
+    return;
+  }
+  // the thread of chunk cstar whose mass holds the threshold
+  const bool use_r = sh.use_r != 0;
+  const int64_t slot = (int64_t)b * NCH * BCT + (int64_t)cstar * BCT + tid;
+  const int32_t tt = P.tties[slot];
+  int32_t tie_tot = 0;
+  const int32_t tbefore = sh.tieq + block_excl_scan<BCT / WAVE>(tt, sh.red_i, &tie_tot);
+  int32_t kept_t = 0;
+  if (hist_mode) {
+    const int64_t room = (int64_t)rs.ktie - tbefore;
+    kept_t = room <= 0 ? 0 : (room < tt ? (int32_t)room : tt);
+  }
+  const int64_t lo_t = (int64_t)cstar * P.bchunk + (int64_t)tid * ept;
+  const int64_t hi_t = lo_t + ept < V ? lo_t + ept : V;
+  double w_t = P.tmass[slot] + (kept_t > 0 ? (double)kept_t * P_cut : 0.0);
+  if (use_r)
+    for (int l = 0; l < a.K; ++l)
+      if (sh.qlast[l] && sh.qid[l] >= lo_t && sh.qid[l] < hi_t) w_t -= sh.qd[l];
+  double tlo, thi;
+  block_tiles<BCT / WAVE>(w_t, sh.red_d, tlo, thi);
+  const double base = sh.chunk_lo, thr = sh.thr;
+  if (base + tlo <= thr && thr < base + thi) sh.pick_thread = tid;
+  __syncthreads();
+  int pt = sh.pick_thread;
+  if (pt < 0) {
+    // rounding left the threshold past this chunk's recomputed mass: the last thread with mass
+    const uint64_t lp = block_max_u64<BCT / WAVE>(w_t > 0.0 ? (uint64_t)tid + 1 : 0ull, sh.red_u);
+    pt = lp ? (int)lp - 1 : -1;
+  }
+  if (tid == pt) {
+    // walk this thread's elements in id order
+    const int cnt = hi_t > lo_t ? (int)(hi_t - lo_t) : 0;
+    float x[EPT_MAX];
+    load_range<DT>(P, b, rowp, lo_t, hi_t, pres, rep, x);
+    double cdf = base + tlo;
+    int32_t seen = 0;
+    int64_t pick = -1, last_pos = -1;
+#pragma unroll
+    for (int i = 0; i < EPT_MAX; ++i) {
+      if (i >= cnt || pick >= 0) continue;
+      const int64_t j = lo_t + i;
+      const uint32_t k = key_of<DT>(x[i]);
       double Pj = 0.0;
-      if (rs.mode == M_UNF) {
-        Pj = dense_P(rs, T, x);
-      } else {
-        const uint32_t k = key_of<DT>(x);
-        bool kept = k > rs.vcut;
-        if (k == rs.vcut) {
-          kept = (int64_t)tieq + tie_before + tie_seen < (int64_t)rs.ktie;
-          ++tie_seen;
-        }
-        Pj = kept ? dense_P(rs, T, x) : 0.0;
+      if (!hist_mode || k > rs.vcut) {
+        Pj = dense_P(rs, T, x[i]);
+      } else if (k == rs.vcut) {
+        if ((int64_t)tbefore + seen < (int64_t)rs.ktie) Pj = P_cut;
+        ++seen;
       }
       if (use_r)
         for (int l = 0; l < a.K; ++l)
           if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
-      return Pj;
-    };
-    double mine = 0.0;
-    int64_t last_pos = -1;  // last element of this thread's range with positive weight
-    {
-      int32_t seen = 0;
-      for (int64_t j = mlo; j < mhi; ++j) {
-        const double w = weight(j, seen);
-        mine += w;
-        if (w > 0.0) last_pos = j;
-      }
+      if (Pj > 0.0) last_pos = j;
+      cdf += Pj;
+      if (cdf > thr) pick = j;
     }
-    double tlo, thi;
-    block_tiles<BCT / WAVE>(mine, sh.red_d, tlo, thi);
-    const double base = sh.chunk_lo, thr = sh.thr;
-    if (tid == 0) sh.claimed = 0;
-    __syncthreads();
-    if (base + tlo <= thr && thr < base + thi) {
-      sh.claimed = 1;
-      double cdf = base + tlo;
-      int32_t seen = 0;
-      int64_t pick = last_pos;  // rounding fallback: the walk ends past the threshold
-      for (int64_t j = mlo; j < mhi; ++j) {
-        cdf += weight(j, seen);
-        if (cdf > thr) {
-          pick = j;
-          break;
-        }
-      }
-      sh.bonus = pick;
-    }
-    __syncthreads();
-    if (!sh.claimed) {
-      // the recomputed chunk mass ended below the threshold: the last positive element
-      const uint64_t lp = block_max_u64<BCT / WAVE>(last_pos >= 0 ? (uint64_t)last_pos + 1 : 0ull, sh.red_u);
-      if (tid == 0 && lp) sh.bonus = (int64_t)lp - 1;
-    }
-    __syncthreads();
+    if (pick < 0) pick = last_pos;  // rounding: the walk ended at or below the threshold
+    if (pick >= 0) sh.bonus = pick;
   }
+  __syncthreads();
   write_outputs(a, b, acc, sh.bonus);
 }
 
@@ -1111,22 +1246,23 @@ __global__ __launch_bounds__(256) void k_topk_merge(const ChunkStat* cstat, cons
 
 }  // namespace dsv
 
+
 // =========================================================================================
 // Host entry points
 // =========================================================================================
 using namespace dsv;
 
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
-static const size_t LDS_LIMIT = 160 * 1024;
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, bchunks, qrank, step_ok, done, nuc_rows, nuc_count, total;
+  int64_t rowsum, lists, cstat, cand, bchunks, qrank, tmass, tties, step_ok, pbits, total;
 };
 static int chunks_per_row(int64_t vocab, int dtype) {
   const int64_t che = dtype == DSV_BF16 ? Elems<DSV_BF16>::chunk : Elems<DSV_F32>::chunk;
   return (int)((vocab + che - 1) / che);
 }
-static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, int kcand) {
+static int64_t pen_words(int64_t vocab) { return (vocab + 31) / 32; }
+static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, int kcand, bool history) {
   WsLayout w;
   const int C = chunks_per_row(vocab, dtype);
   int64_t o = 0;
@@ -1140,20 +1276,20 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.cand, rows * C * (int64_t)kcand * 8);
   take(w.bchunks, (int64_t)bs * NCH * (int64_t)sizeof(BonusChunk));
   take(w.qrank, (int64_t)bs * QMAX * 4);
+  take(w.tmass, (int64_t)bs * NCH * BCT * 8);
+  take(w.tties, (int64_t)bs * NCH * BCT * 4);
   take(w.step_ok, rows * 4);
-  take(w.done, (int64_t)bs * 4);
-  take(w.nuc_rows, rows * 4);
-  take(w.nuc_count, 4);
+  take(w.pbits, history ? (int64_t)bs * pen_words(vocab) * 4 : 0);
   w.total = o;
   return w;
 }
 
 extern "C" int64_t dsv_verify_workspace_bytes(int64_t rows, int32_t bs, int32_t T, int64_t vocab) {
   (void)T;
-  return ws_layout(rows, bs, vocab, DSV_F32, DSV_LIST_K).total;  // float32 has more chunks
+  return ws_layout(rows, bs, vocab, DSV_F32, DSV_LIST_K, true).total;  // the largest layout
 }
 extern "C" int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab) {
-  return ws_layout(rows, 1, vocab, DSV_F32, 0).total;
+  return ws_layout(rows, 1, vocab, DSV_F32, 0, false).total;
 }
 
 // Side stream + events per device for the nucleus kernel (default priority).
@@ -1224,7 +1360,8 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
              DSV_LIST_K);
   const int C = chunks_per_row(a.vocab, a.logits_dtype);
   if (C > 16) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab %lld needs %d chunks (> 16)", (long long)a.vocab, C);
-  const WsLayout w = ws_layout(a.rows, a.bs, a.vocab, a.logits_dtype, DSV_LIST_K);
+  const bool history = a.hist_ids && a.hist_len > 0;
+  const WsLayout w = ws_layout(a.rows, a.bs, a.vocab, a.logits_dtype, DSV_LIST_K, history);
   if (a.workspace_bytes < w.total)
     DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_verify: workspace %lld < %lld bytes", (long long)a.workspace_bytes,
              (long long)w.total);
@@ -1232,6 +1369,7 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   KParams P;
   memset(&P, 0, sizeof(P));
   P.a = a;
+  if (!history) P.a.hist_ids = nullptr;
   char* ws = reinterpret_cast<char*>(a.workspace);
   P.rowsum = reinterpret_cast<RowSum*>(ws + w.rowsum);
   P.lists = reinterpret_cast<ListEntry*>(ws + w.lists);
@@ -1239,31 +1377,35 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.cand = reinterpret_cast<uint64_t*>(ws + w.cand);
   P.bchunks = reinterpret_cast<BonusChunk*>(ws + w.bchunks);
   P.qrank = reinterpret_cast<int32_t*>(ws + w.qrank);
+  P.tmass = reinterpret_cast<double*>(ws + w.tmass);
+  P.tties = reinterpret_cast<int32_t*>(ws + w.tties);
   P.step_ok = reinterpret_cast<int32_t*>(ws + w.step_ok);
-  P.done = reinterpret_cast<int32_t*>(ws + w.done);
-  P.nuc_rows = reinterpret_cast<int32_t*>(ws + w.nuc_rows);
-  P.nuc_count = reinterpret_cast<int32_t*>(ws + w.nuc_count);
-  P.bchunk = align_up((a.vocab + NCH - 1) / NCH, 8);
+  P.pbits = history ? reinterpret_cast<uint32_t*>(ws + w.pbits) : nullptr;
+  P.pwords = pen_words(a.vocab);
+  int64_t ept = align_up((a.vocab + (int64_t)NCH * BCT - 1) / ((int64_t)NCH * BCT), 8);
+  if (ept > EPT_MAX) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab %lld is too large", (long long)a.vocab);
+  P.ept = (int32_t)ept;
+  P.bchunk = (int64_t)BCT * ept;
+  P.nch = (int32_t)((a.vocab + P.bchunk - 1) / P.bchunk);
   P.C = C;
   P.kcand = DSV_LIST_K;
   P.aligned = ((uintptr_t)a.logits % 16 == 0) && ((a.row_stride * (int64_t)esize) % 16 == 0);
   P.softmax = 1;
-  if (!(a.hist_ids && a.hist_len > 0)) P.a.hist_ids = nullptr;
   if (a.rows == 0) return DSV_OK;
   const int stages = a.stages ? a.stages : 7;
-  const size_t bitmap_bytes = P.a.hist_ids ? (size_t)((a.vocab + 31) / 32) * 4 : 0;
-  if (bitmap_bytes > 64 * 1024) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab too large for the penalty bitmap");
-  const size_t nuc_lds = (size_t)HIST_WORDS * 4 + bitmap_bytes;
-  if (hist_possible && nuc_lds + sizeof(NucShared) > LDS_LIMIT)
-    DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab %lld with history penalties exceeds the LDS budget",
-             (long long)a.vocab);
+  const size_t prep_lds = history ? (size_t)P.pwords * 4 : 0;
+  const size_t nuc_lds = (size_t)HIST_WORDS * 4;
+  if (prep_lds > 64 * 1024) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab too large for the history bitmap");
   if (stages & 1) {
+    if (history) {
+      (void)hipFuncSetAttribute((const void*)k_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)prep_lds);
+      hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
+      DSV_CHECK_LAUNCH("k_prep");
+    }
     SideStream* side = nullptr;
     if (hist_possible) {
       int rc = side_stream(&side);
       if (rc) return rc;
-      hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, stream, P);
-      DSV_CHECK_LAUNCH("k_plan");
       if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
         DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot fork the side stream");
       const int ncu = num_cus();
@@ -1276,22 +1418,29 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
     }
     if (a.logits_dtype == DSV_BF16) {
       hipLaunchKernelGGL(k_chunk<DSV_BF16>, dim3((unsigned)(a.rows * C)), dim3(CT), 0, stream, P);
-      hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(WAVE), 0, stream, P);
+      hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
     } else {
       hipLaunchKernelGGL(k_chunk<DSV_F32>, dim3((unsigned)(a.rows * C)), dim3(CT), 0, stream, P);
-      hipLaunchKernelGGL(k_merge<DSV_F32>, dim3((unsigned)a.rows), dim3(WAVE), 0, stream, P);
+      hipLaunchKernelGGL(k_merge<DSV_F32>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
     }
-    DSV_CHECK_LAUNCH("k_chunk/k_merge");
+    DSV_CHECK_LAUNCH("k_chunk / k_merge");
     if (side && hipStreamWaitEvent(stream, side->join, 0) != hipSuccess)
       DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot join the side stream");
   }
-  if (!(stages & 6)) return DSV_OK;
-  const size_t bonus_lds = bitmap_bytes;  // the finishing workgroup holds the whole row's bitmap
-  if (a.logits_dtype == DSV_BF16)
-    hipLaunchKernelGGL(k_bonus<DSV_BF16>, dim3(NCH, a.bs), dim3(BCT), bonus_lds, stream, P);
-  else
-    hipLaunchKernelGGL(k_bonus<DSV_F32>, dim3(NCH, a.bs), dim3(BCT), bonus_lds, stream, P);
-  DSV_CHECK_LAUNCH("k_bonus");
+  if (stages & 2) {
+    if (a.logits_dtype == DSV_BF16)
+      hipLaunchKernelGGL(k_bonus<DSV_BF16>, dim3(P.nch, a.bs), dim3(BCT), 0, stream, P);
+    else
+      hipLaunchKernelGGL(k_bonus<DSV_F32>, dim3(P.nch, a.bs), dim3(BCT), 0, stream, P);
+    DSV_CHECK_LAUNCH("k_bonus");
+  }
+  if (stages & 4) {
+    if (a.logits_dtype == DSV_BF16)
+      hipLaunchKernelGGL(k_final<DSV_BF16>, dim3(a.bs), dim3(BCT), 0, stream, P);
+    else
+      hipLaunchKernelGGL(k_final<DSV_F32>, dim3(a.bs), dim3(BCT), 0, stream, P);
+    DSV_CHECK_LAUNCH("k_final");
+  }
   return DSV_OK;
 }
 
@@ -1312,7 +1461,7 @@ extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows
     DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: cap %d outside [1, %d]", cap, T);
   if (!logits || !candidates || !prefix_lens || !accept || !commit || !bonus || !output || !new_seq || !workspace)
     DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: required pointer is null");
-  const WsLayout w = ws_layout(rows, 1, vocab, dtype, 0);
+  const WsLayout w = ws_layout(rows, 1, vocab, dtype, 0, false);
   if (workspace_bytes < w.total)
     DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_greedy_verify: workspace %lld < %lld", (long long)workspace_bytes,
              (long long)w.total);
