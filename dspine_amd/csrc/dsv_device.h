@@ -204,6 +204,52 @@ __device__ __forceinline__ void reg_fence1(uint4& v, float& acc) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(acc));
 }
 
+// Element e (a run-time index) of a vector, and its replacement.
+template <int DT>
+__device__ __forceinline__ float vec_elem_dyn(const uint4& v, int e) {
+  constexpr int per = DT == DSV_BF16 ? 2 : 1;  // elements per 32-bit word
+  const int wi = e / per;
+  const uint32_t w = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
+  if constexpr (DT == DSV_BF16)
+    return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  else
+    return __uint_as_float(w);
+}
+template <int DT>
+__device__ __forceinline__ void vec_set_dyn(uint4& v, int e, float x) {
+  constexpr int per = DT == DSV_BF16 ? 2 : 1;
+  const int wi = e / per;
+  uint32_t w = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
+  if constexpr (DT == DSV_BF16) {
+    const uint32_t bb = __float_as_uint(x) >> 16;
+    w = (e & 1) ? ((w & 0xffffu) | (bb << 16)) : ((w & 0xffff0000u) | bb);
+  } else {
+    w = __float_as_uint(x);
+  }
+  v.x = wi == 0 ? w : v.x;
+  v.y = wi == 1 ? w : v.y;
+  v.z = wi == 2 ? w : v.z;
+  v.w = wi == 3 ? w : v.w;
+}
+
+// Vector vi of a 16-byte-aligned row when vi < nfull (vectors lying wholly inside the row),
+// the -inf fill otherwise.  Branch-free (the address is clamped to vector nfull - 1 and the
+// result selected), so a thread keeps all of its loads in flight.  Needs nfull >= 1.
+template <int DT>
+__device__ __forceinline__ uint4 load_vec_fast(const char* rowp, int64_t vi, int64_t nfull) {
+  const uint32_t fill = DT == DSV_BF16 ? FILL_BF16 : FILL_F32;
+  const bool ok = vi < nfull;
+  const int64_t vc = ok ? vi : nfull - 1;
+  const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(rowp) + vc);
+  return make_uint4(ok ? t.x : fill, ok ? t.y : fill, ok ? t.z : fill, ok ? t.w : fill);
+}
+
+// Vector vi of a 16-byte-aligned row, no bounds check (the caller knows it is inside).
+__device__ __forceinline__ uint4 load_vec_raw(const char* rowp, int64_t vi) {
+  const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(rowp) + vi);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 // Replace element e of a vector by x (bf16 values are exact: the penalty rounds to bf16).
 template <int DT>
 __device__ __forceinline__ void vec_set(uint4& v, int e, float x) {

@@ -300,22 +300,39 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
 // ---------------------------------------------------------------------------------------
 // k_chunk: one pass over a 20480-value (bf16) / 10240-value (fp32) chunk held in registers
 // ---------------------------------------------------------------------------------------
-template <int DT>
+template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   constexpr int n = Elems<DT>::n;
   constexpr int CHE = Elems<DT>::chunk;
-  constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
   __shared__ uint64_t cbuf[CAND_CAP];
-  __shared__ uint64_t top[TOPK_MAX];
   __shared__ uint32_t hist256[256];
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
-  __shared__ int32_t s_cnt, s_cnt2;
+  __shared__ int32_t s_cnt;
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
   const int c = (int)(blockIdx.x - r * C);
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
+  const int64_t V = a.vocab;
+  const int64_t lo = (int64_t)c * CHE;
+  const int64_t hi = lo + CHE < V ? lo + CHE : V;
+  const char* rowp = row_ptr(a, r);
+  const int64_t v0 = lo / n;
+  // the chunk's loads go out first, unconditionally (addresses clamped into the row); the
+  // row's request and mode are looked up under them
+  uint4 v[CV];
+  const int64_t nfull = hi / n;  // vectors wholly inside the row end before this one
+  if constexpr (ALIGNED) {
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      const int64_t vi = v0 + (int64_t)u * CT + tid;
+      v[u] = load_vec_raw(rowp, vi < nfull ? vi : nfull - 1);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, false);
+  }
   int b = 0, s = 0;
   int mode = M_GREEDY;
   if (!P.force_greedy) {
@@ -331,16 +348,17 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   }
   const float T = P.softmax && mode != M_GREEDY ? a.temperatures[b] : 1.f;
   ChunkStat* st = P.cstat + r * C + c;
-  const int64_t V = a.vocab;
-  const int64_t lo = (int64_t)c * CHE;
-  const int64_t hi = lo + CHE < V ? lo + CHE : V;
-  const char* rowp = row_ptr(a, r);
-  const bool aligned = P.aligned != 0;
-  const int64_t v0 = lo / n;
-
-  uint4 v[CV];
+  if (ALIGNED && hi - lo < CHE) {
+    // the row's last chunk: -inf past the row, and the partial last vector element by element
+    const uint32_t fill = DT == DSV_BF16 ? FILL_BF16 : FILL_F32;
+    const int64_t rel = nfull - v0;
 #pragma unroll
-  for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, aligned);
+    for (int u = 0; u < CV; ++u) {
+      const int64_t vi = v0 + (int64_t)u * CT + tid;
+      if (vi >= nfull) v[u] = make_uint4(fill, fill, fill, fill);
+      if (hi % n && u == rel / CT && tid == rel % CT) v[u] = load_vec<DT>(rowp, nfull, hi, false);
+    }
+  }
 
   const bool pen = P.softmax && P.pbits != nullptr;
   float pres = 0.f, rep = 1.f;
@@ -351,14 +369,17 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 #pragma unroll
     for (int u = 0; u < CV; ++u) {
       const int64_t j = (v0 + (int64_t)u * CT + tid) * n;
-      bits[u] = j < hi ? pen_bits(P, b, j, n) : 0u;
+      const uint32_t w = pen_bits(P, b, j < hi ? j : lo, n);
+      bits[u] = j < hi ? w : 0u;
     }
+    // history tokens are rare: visit only the set bits (about 0.3% of the values)
 #pragma unroll
     for (int u = 0; u < CV; ++u) {
-      if (bits[u]) {
-#pragma unroll
-        for (int e = 0; e < n; ++e)
-          if ((bits[u] >> e) & 1u) vec_set<DT>(v[u], e, penalize<DT>(vec_elem<DT>(v[u], e), pres, rep));
+      uint32_t bu = bits[u];
+      while (bu) {
+        const int e = __ffs(bu) - 1;
+        bu &= bu - 1u;
+        vec_set_dyn<DT>(v[u], e, penalize<DT>(vec_elem_dyn<DT>(v[u], e), pres, rep));
       }
     }
   }
@@ -455,9 +476,15 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     if (nb > CAND_CAP)
       nb = refill_candidates<DT>(pen ? P.pbits + (int64_t)b * P.pwords : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
                                  hist256, su, &s_cnt);
-    const int kk = select_top<TOP_SHIFT>(cbuf, nb, K, top, hist256, su, &s_cnt2);
+    // rank of each admitted value among them (values are distinct): the top K, in order
+    const int kk = K < nb ? K : nb;
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;
-    for (int i = tid; i < kk; i += CT) dst[i] = cbuf[i];
+    for (int i = tid; i < nb; i += CT) {
+      const uint64_t v_i = cbuf[i];
+      int rank = 0;
+      for (int j = 0; j < nb; ++j) rank += cbuf[j] > v_i;
+      if (rank < kk) dst[rank] = v_i;
+    }
     out.ncand = kk;
   }
   if (tid == 0) *st = out;
@@ -512,7 +539,7 @@ __device__ __forceinline__ int nuc_word(int wid, int i, int lane) {
   return HIST_WORDS - 1 - wid * NUC_WPW - WAVE * i - lane;
 }
 
-template <int DT>
+template <int DT, bool ALIGNED>
 __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
@@ -520,7 +547,6 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   row_request(a, r, b, s);
   const int64_t V = a.vocab;
   const char* rowp = row_ptr(a, r);
-  const bool aligned = P.aligned != 0;
   const float T = a.temperatures[b];
   const int topk = a.top_ks[b];
   const bool pen = P.pbits != nullptr;
@@ -546,40 +572,51 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   __syncthreads();
   const uint32_t ktok = sh.ktok;
   constexpr int U = 4;
-  const int64_t NVt = (V + 7) / 8;
+  const int64_t NVf = ALIGNED ? V / 8 : (V + 7) / 8;  // vectors read whole (the rest: thread 0)
   uint64_t best = 0ull;
   uint32_t tie_before = 0, nfin = 0;
-  for (int64_t q0 = 0; q0 < NVt; q0 += (int64_t)NUC_THREADS * U) {
+  auto count = [&](float x, int64_t j) {
+    const uint32_t k = key_of<DT>(x);
+    const uint64_t pk = pack(k, j);
+    best = pk > best ? pk : best;
+    if (k != NEG_INF_BF16_KEY) {
+      atomicAdd(&hist[k >> 1], 1u << ((k & 1u) * 16u));
+      ++nfin;
+      tie_before += (k == ktok && j < tok) ? 1u : 0u;
+    }
+  };
+  for (int64_t q0 = 0; q0 < NVf; q0 += (int64_t)NUC_THREADS * U) {
     uint4 w[U];
     uint32_t bits[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
-      w[u] = load_vec<DT>(rowp, vi, V, aligned);
-      bits[u] = (pen && vi < NVt) ? pen_bits(P, b, vi * 8, 8) : 0u;
+      if constexpr (ALIGNED)
+        w[u] = load_vec_raw(rowp, vi < NVf ? vi : NVf - 1);
+      else
+        w[u] = load_vec<DT>(rowp, vi, V, false);
+      const uint32_t bw = pen ? pen_bits(P, b, (vi < NVf ? vi : 0) * 8, 8) : 0u;
+      bits[u] = vi < NVf ? bw : 0u;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
-      if (vi >= NVt) continue;
+      if (vi >= NVf) continue;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int64_t j = vi * 8 + e;
         float x = vec_elem<DT>(w[u], e);
         if ((bits[u] >> e) & 1u) x = penalize<DT>(x, pres, rep);
-        const uint32_t k = key_of<DT>(x);
-        if (j < V) {
-          const uint64_t pk = pack(k, j);
-          best = pk > best ? pk : best;
-          if (k != NEG_INF_BF16_KEY) {
-            atomicAdd(&hist[k >> 1], 1u << ((k & 1u) * 16u));
-            ++nfin;
-            tie_before += (k == ktok && j < tok) ? 1u : 0u;
-          }
-        }
+        if (ALIGNED || j < V) count(x, j);
       }
     }
   }
+  if (ALIGNED && tid == 0)
+    for (int64_t j = NVf * 8; j < V; ++j) {  // the row's partial last vector
+      float x = load_elem<DT>(rowp, j);
+      if (pen && pen_test(P, b, j)) x = penalize<DT>(x, pres, rep);
+      count(x, j);
+    }
   __syncthreads();
   const uint64_t gbest = block_max_u64<NUC_WAVES>(best, sh.u);
   const uint32_t kmax = unpack_key(gbest);
@@ -752,7 +789,7 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
 }
 
 // Persistent workgroups: the i-th nucleus row in row order goes to workgroup i % gridDim.x.
-template <int DT>
+template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ NucShared sh;
@@ -778,7 +815,7 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
     __syncthreads();
     const int nm = sh.nmine;
     for (int i = 0; i < nm; ++i) {
-      if constexpr (DT == DSV_BF16) nuc_row<DT>(P, sh.mine[i], hist, sh);
+      if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, sh.mine[i], hist, sh);
     }
     seen += total;
     __syncthreads();
@@ -822,16 +859,33 @@ __device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, i
 }
 
 // The elements [lo_t, lo_t + cnt) of a thread's bonus range, penalised, as floats.
-template <int DT>
+template <int DT, bool ALIGNED>
 __device__ __forceinline__ void load_range(const KParams& P, int b, const char* rowp, int64_t lo_t, int64_t hi_t,
                                            float pres, float rep, float (&x)[EPT_MAX]) {
   constexpr int n = Elems<DT>::n;
   constexpr int NV = EPT_MAX / n;
   uint4 v[NV];
   const int nv = (P.ept + n - 1) / n;
+  if constexpr (ALIGNED) {
+    // whole vectors inside the row: clamped, unconditional loads; the rest filled below
+    const int64_t nfull = P.a.vocab / n;
+    const uint32_t fill = DT == DSV_BF16 ? FILL_BF16 : FILL_F32;
 #pragma unroll
-  for (int u = 0; u < NV; ++u)
-    v[u] = u < nv ? load_vec<DT>(rowp, lo_t / n + u, hi_t, P.aligned != 0) : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < NV; ++u) {
+      const int64_t vi = lo_t / n + u;
+      v[u] = load_vec_raw(rowp, vi < nfull ? vi : nfull - 1);
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int64_t vi = lo_t / n + u;
+      if (u >= nv || vi * n >= hi_t) v[u] = make_uint4(fill, fill, fill, fill);
+      else if (vi >= nfull) v[u] = load_vec<DT>(rowp, vi, hi_t, false);  // the row's partial last vector
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+      v[u] = u < nv ? load_vec<DT>(rowp, lo_t / n + u, hi_t, false) : make_uint4(0, 0, 0, 0);
+  }
   uint64_t bits = 0;
   if (P.pbits && lo_t < hi_t) {
     const int64_t w0 = lo_t >> 5;
@@ -860,8 +914,8 @@ struct BonusShared {
   int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
   double qd[QMAX];      // P - max(P - q, 0) of a kept q id (the residual's reduction), else 0
   int64_t bonus;
-  double chunk_lo, thr;
-  int32_t acc, chunk, tieq, use_r, pick_thread;
+  double chunk_lo, thr, pick_lo;
+  int32_t acc, chunk, tieq, use_r, pick_thread, tb_pick;
 };
 
 struct ReqView {
@@ -919,7 +973,7 @@ __device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, const R
 // ---------------------------------------------------------------------------------------
 // k_bonus: per-thread masses of each dense bonus row (one vector pass; chunks x requests)
 // ---------------------------------------------------------------------------------------
-template <int DT>
+template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
   __shared__ BonusShared sh;
   const dsv_verify_args& a = P.a;
@@ -943,7 +997,7 @@ __global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
   const int64_t hi_t = lo_t + ept < V ? lo_t + ept : V;
   const int cnt = hi_t > lo_t ? (int)(hi_t - lo_t) : 0;
   float x[EPT_MAX];
-  load_range<DT>(P, b, rowp, lo_t, hi_t, pres, rep, x);
+  load_range<DT, ALIGNED>(P, b, rowp, lo_t, hi_t, pres, rep, x);
   double mgt = 0.0;
   int32_t ties = 0;
 #pragma unroll
@@ -1131,34 +1185,43 @@ __global__ __launch_bounds__(BCT) void k_final(KParams P) {
     pt = lp ? (int)lp - 1 : -1;
   }
   if (tid == pt) {
-    // walk this thread's elements in id order
-    const int cnt = hi_t > lo_t ? (int)(hi_t - lo_t) : 0;
-    float x[EPT_MAX];
-    load_range<DT>(P, b, rowp, lo_t, hi_t, pres, rep, x);
-    double cdf = base + tlo;
-    int32_t seen = 0;
-    int64_t pick = -1, last_pos = -1;
-#pragma unroll
-    for (int i = 0; i < EPT_MAX; ++i) {
-      if (i >= cnt || pick >= 0) continue;
-      const int64_t j = lo_t + i;
-      const uint32_t k = key_of<DT>(x[i]);
-      double Pj = 0.0;
-      if (!hist_mode || k > rs.vcut) {
-        Pj = dense_P(rs, T, x[i]);
-      } else if (k == rs.vcut) {
-        if ((int64_t)tbefore + seen < (int64_t)rs.ktie) Pj = P_cut;
-        ++seen;
-      }
+    sh.tb_pick = tbefore;
+    sh.pick_lo = base + tlo;
+  }
+  __syncthreads();
+  if (pt >= 0 && tid < WAVE) {
+    // thread pt's elements in id order, one per lane: weights, then the running sum
+    const int64_t plo = (int64_t)cstar * P.bchunk + (int64_t)pt * ept;
+    const int64_t phi = plo + ept < V ? plo + ept : V;
+    const int64_t j = plo + lane;
+    const bool live = j < phi;
+    float xj = live ? load_elem<DT>(rowp, j) : -INFINITY;
+    if (live && pen && pen_test(P, b, j)) xj = penalize<DT>(xj, pres, rep);
+    const uint32_t k = key_of<DT>(xj);
+    const bool tie = live && hist_mode && k == rs.vcut;
+    const uint64_t tmask = __ballot(tie);
+    const int32_t seen = __popcll(tmask & ((1ull << lane) - 1ull));
+    double Pj = 0.0;
+    if (live) {
+      if (!hist_mode || k > rs.vcut)
+        Pj = dense_P(rs, T, xj);
+      else if (tie && (int64_t)sh.tb_pick + seen < (int64_t)rs.ktie)
+        Pj = P_cut;
       if (use_r)
         for (int l = 0; l < a.K; ++l)
           if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
-      if (Pj > 0.0) last_pos = j;
-      cdf += Pj;
-      if (cdf > thr) pick = j;
     }
-    if (pick < 0) pick = last_pos;  // rounding: the walk ended at or below the threshold
-    if (pick >= 0) sh.bonus = pick;
+    double wlo, whi;
+    wave_tiles(Pj, wlo, whi);
+    const double start = sh.pick_lo;
+    const uint64_t hit = __ballot(live && start + whi > thr);
+    const uint64_t pos = __ballot(live && Pj > 0.0);
+    int64_t pick = -1;
+    if (hit)
+      pick = plo + (__ffsll((long long)hit) - 1);
+    else if (pos)
+      pick = plo + (63 - __clzll((long long)pos));  // rounding: the last element with mass
+    if (lane == 0 && pick >= 0) sh.bonus = pick;
   }
   __syncthreads();
   write_outputs(a, b, acc, sh.bonus);
@@ -1257,6 +1320,20 @@ static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; 
 struct WsLayout {
   int64_t rowsum, lists, cstat, cand, bchunks, qrank, tmass, tties, step_ok, pbits, total;
 };
+static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
+  if (dtype == DSV_BF16) {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_chunk<DSV_BF16, true>), dim3(grid), dim3(CT), 0, stream, P);
+    else
+      hipLaunchKernelGGL((k_chunk<DSV_BF16, false>), dim3(grid), dim3(CT), 0, stream, P);
+  } else {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_chunk<DSV_F32, true>), dim3(grid), dim3(CT), 0, stream, P);
+    else
+      hipLaunchKernelGGL((k_chunk<DSV_F32, false>), dim3(grid), dim3(CT), 0, stream, P);
+  }
+}
+
 static int chunks_per_row(int64_t vocab, int dtype) {
   const int64_t che = dtype == DSV_BF16 ? Elems<DSV_BF16>::chunk : Elems<DSV_F32>::chunk;
   return (int)((vocab + che - 1) / che);
@@ -1389,7 +1466,8 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.nch = (int32_t)((a.vocab + P.bchunk - 1) / P.bchunk);
   P.C = C;
   P.kcand = DSV_LIST_K;
-  P.aligned = ((uintptr_t)a.logits % 16 == 0) && ((a.row_stride * (int64_t)esize) % 16 == 0);
+  P.aligned = ((uintptr_t)a.logits % 16 == 0) && ((a.row_stride * (int64_t)esize) % 16 == 0) &&
+              a.vocab * (int64_t)esize >= 16;
   P.softmax = 1;
   if (a.rows == 0) return DSV_OK;
   const int stages = a.stages ? a.stages : 7;
@@ -1410,28 +1488,41 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
         DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot fork the side stream");
       const int ncu = num_cus();
       const int grid = (int)(a.rows < ncu ? a.rows : ncu);
-      (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)nuc_lds);
-      hipLaunchKernelGGL(k_nuc<DSV_BF16>, dim3(grid), dim3(NUC_THREADS), nuc_lds, side->s, P);
+      if (P.aligned) {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, side->s, P);
+      } else {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, side->s, P);
+      }
       DSV_CHECK_LAUNCH("k_nuc");
       if (hipEventRecord(side->join, side->s) != hipSuccess)
         DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the side-stream join");
     }
-    if (a.logits_dtype == DSV_BF16) {
-      hipLaunchKernelGGL(k_chunk<DSV_BF16>, dim3((unsigned)(a.rows * C)), dim3(CT), 0, stream, P);
+    launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * C), stream);
+    if (a.logits_dtype == DSV_BF16)
       hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-    } else {
-      hipLaunchKernelGGL(k_chunk<DSV_F32>, dim3((unsigned)(a.rows * C)), dim3(CT), 0, stream, P);
+    else
       hipLaunchKernelGGL(k_merge<DSV_F32>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-    }
     DSV_CHECK_LAUNCH("k_chunk / k_merge");
     if (side && hipStreamWaitEvent(stream, side->join, 0) != hipSuccess)
       DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot join the side stream");
   }
   if (stages & 2) {
-    if (a.logits_dtype == DSV_BF16)
-      hipLaunchKernelGGL(k_bonus<DSV_BF16>, dim3(P.nch, a.bs), dim3(BCT), 0, stream, P);
-    else
-      hipLaunchKernelGGL(k_bonus<DSV_F32>, dim3(P.nch, a.bs), dim3(BCT), 0, stream, P);
+    const dim3 grid(P.nch, a.bs);
+    if (a.logits_dtype == DSV_BF16) {
+      if (P.aligned)
+        hipLaunchKernelGGL((k_bonus<DSV_BF16, true>), grid, dim3(BCT), 0, stream, P);
+      else
+        hipLaunchKernelGGL((k_bonus<DSV_BF16, false>), grid, dim3(BCT), 0, stream, P);
+    } else {
+      if (P.aligned)
+        hipLaunchKernelGGL((k_bonus<DSV_F32, true>), grid, dim3(BCT), 0, stream, P);
+      else
+        hipLaunchKernelGGL((k_bonus<DSV_F32, false>), grid, dim3(BCT), 0, stream, P);
+    }
     DSV_CHECK_LAUNCH("k_bonus");
   }
   if (stages & 4) {
@@ -1479,12 +1570,10 @@ extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows
   char* ws = reinterpret_cast<char*>(workspace);
   P.cstat = reinterpret_cast<ChunkStat*>(ws + w.cstat);
   P.C = chunks_per_row(vocab, dtype);
-  P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0);
+  P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0) &&
+              vocab * (int64_t)esize >= 16;
   P.force_greedy = 1;
-  if (dtype == DSV_BF16)
-    hipLaunchKernelGGL(k_chunk<DSV_BF16>, dim3((unsigned)(rows * P.C)), dim3(CT), 0, stream, P);
-  else
-    hipLaunchKernelGGL(k_chunk<DSV_F32>, dim3((unsigned)(rows * P.C)), dim3(CT), 0, stream, P);
+  launch_chunk(P, dtype, (unsigned)(rows * P.C), stream);
   DSV_CHECK_LAUNCH("k_chunk");
   hipLaunchKernelGGL(k_greedy_accept, dim3((bs + 63) / 64), dim3(64), 0, stream, P.cstat, P.C, candidates,
                      verify_lens, cap, prefix_lens, bs, T, accept, commit, bonus, output, new_seq, top1_out);
@@ -1525,15 +1614,15 @@ extern "C" int dsv_topk(const void* logits, int32_t dtype, int64_t rows, int64_t
   P.cand = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + (size_t)rows * C * sizeof(ChunkStat));
   P.C = C;
   P.kcand = k;
-  P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0);
+  P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0) &&
+              vocab * (int64_t)esize >= 16;
+  launch_chunk(P, dtype, (unsigned)(rows * C), stream);
   if (dtype == DSV_BF16) {
-    hipLaunchKernelGGL(k_chunk<DSV_BF16>, dim3((unsigned)(rows * C)), dim3(CT), 0, stream, P);
     (void)hipFuncSetAttribute((const void*)k_topk_merge<DSV_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)merge_lds);
     hipLaunchKernelGGL(k_topk_merge<DSV_BF16>, dim3((unsigned)rows), dim3(256), merge_lds, stream, P.cstat, P.cand, C,
                        k, k, values_out, ids_out, sort_by_id);
   } else {
-    hipLaunchKernelGGL(k_chunk<DSV_F32>, dim3((unsigned)(rows * C)), dim3(CT), 0, stream, P);
     (void)hipFuncSetAttribute((const void*)k_topk_merge<DSV_F32>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)merge_lds);
     hipLaunchKernelGGL(k_topk_merge<DSV_F32>, dim3((unsigned)rows), dim3(256), merge_lds, stream, P.cstat, P.cand, C,

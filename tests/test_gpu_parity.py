@@ -41,10 +41,20 @@ def compare_outputs(gpu, ref, requests, tag):
     return near
 
 
-def run_gpu_verify(batch, device, backend="pytorch"):
+def _padded(x, device, width):
+    """x [rows, V] on the device as a view of a [rows, width] buffer (row stride `width`)."""
+    buf = torch.full((x.shape[0], width), float("nan"), dtype=x.dtype, device=device)
+    buf[:, : x.shape[1]] = x.to(device)
+    return buf[:, : x.shape[1]]
+
+
+def run_gpu_verify(batch, device, backend="pytorch", row_stride=None):
     from dspine_amd.verify import History, verify_step
 
     d = W.to_device(batch, device)
+    if row_stride is not None:
+        d["logits"] = _padded(batch["logits"], device, row_stride)
+        assert d["logits"].stride(0) == row_stride
     hist = None
     if "hist_ids" in d:
         hist = History(d["hist_ids"], d["presence"], d["repetition"])
@@ -255,6 +265,44 @@ def test_verify_small_ragged(device, seed):
     gpu = run_gpu_verify(batch, device)
     ref = run_oracle(batch, list(range(bs)))
     assert len(compare_outputs(gpu, ref, range(bs), f"ragged seed={seed}")) <= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V,stride", [(997, 1000), (20483, 20488), (41000, 41000), (5, 8)])
+def test_verify_row_layouts(device, dtype, V, stride):
+    # 16-byte aligned rows whose vocab leaves a partial last vector, a vocab that ends a
+    # chunk exactly plus 3, a vocab ending inside the second chunk, and a vocab shorter than
+    # one vector (the byte-wise load path)
+    mixed = dtype == torch.bfloat16
+    batch = _small_batch(11, bs=12, T=5, V=V, K=4, dtype=dtype, mixed=mixed, penalties=True)
+    bs = batch["candidates"].shape[0]
+    gpu = run_gpu_verify(batch, device, row_stride=stride)
+    ref = run_oracle(batch, list(range(bs)))
+    assert len(compare_outputs(gpu, ref, range(bs), f"layout V={V} stride={stride}")) <= 1
+
+
+@pytest.mark.parametrize("V,stride", [(997, 1000), (70001, 70008)])
+def test_greedy_and_topk_row_layouts(device, V, stride):
+    from dspine_amd.kernels.dspine import topk
+    from dspine_amd.verification.caps import accept_greedy
+
+    O = _oracle()
+    g = torch.Generator().manual_seed(9)
+    bs, T = 4, 6
+    x = torch.randn(bs * T, V, generator=g).to(torch.bfloat16)
+    xd = _padded(x, device, stride)
+    vals, ids = topk(xd, 20)
+    rv, ri = O.topk(x.float(), 20)
+    assert torch.equal(ids.cpu(), ri) and torch.equal(vals.cpu(), rv)
+    top1 = O.argmax_rows(x)
+    cand = torch.zeros(bs, T, dtype=torch.int64)
+    cand[:, 1:] = torch.as_tensor(top1).view(bs, T)[:, : T - 1]
+    cand[1, 3] = (cand[1, 3] + 1) % V
+    prefix = torch.arange(bs, dtype=torch.int32)
+    ref = O.greedy_accept(top1, cand.numpy(), [T] * bs, prefix.numpy())
+    outs = accept_greedy(candidates=cand.to(device), next_token_logits=xd, prefix_lens=prefix.to(device), cap=T)
+    for got, r in zip(outs, ref):
+        assert np.array_equal(got.cpu().numpy(), r)
 
 
 def test_verify_unfiltered(device):
