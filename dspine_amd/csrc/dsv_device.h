@@ -40,7 +40,8 @@ struct ChunkStat {
   double s;       // sum exp((x - m) / T) over the chunk
   int32_t ncand;  // candidates written (LIST)
   int32_t flags;
-  int32_t pad[2];
+  uint32_t wlo;   // nucleus rows: lowest key of the chunk's value-count window (WIN_EMPTY: none)
+  uint32_t kx;    // nucleus rows: largest key below the window (0: none)
 };
 static_assert(sizeof(ChunkStat) == 32, "ChunkStat layout");
 
@@ -54,12 +55,15 @@ constexpr int CT = 256;              // threads of a chunk workgroup
 constexpr int CV = 10;               // 16-byte vectors per thread per chunk
 constexpr int CAND_CAP = 512;        // LDS candidate buffer of a chunk (> largest k)
 constexpr int TOPK_MAX = 256;        // largest k of the top-k entry point
-constexpr int NUC_THREADS = 512;     // nucleus-row workgroup
+constexpr int NUC_THREADS = 512;     // full-histogram nucleus workgroup
 constexpr int HIST_WORDS = 32768;    // 65536 16-bit counters
+constexpr int NUC_SLICE = 65528;     // values per 16-bit histogram pass (no counter can wrap)
+constexpr int HWIN = 4096;           // keys of a chunk's value-count window (nucleus rows)
+constexpr uint32_t WIN_EMPTY = 0x10000u;
 constexpr int NCH = 32;              // bonus-row chunks
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
-constexpr int FLAG_HIST_OVERFLOW = 1;
+constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram
 
 template <int DT>
 struct Elems {  // elements per 16-byte vector
@@ -204,44 +208,30 @@ __device__ __forceinline__ void reg_fence1(uint4& v, float& acc) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(acc));
 }
 
-// Element e (a run-time index) of a vector, and its replacement.
+// Element e (a run-time index) of a vector, and its replacement: branch-free, through the two
+// 64-bit halves of the vector.
 template <int DT>
 __device__ __forceinline__ float vec_elem_dyn(const uint4& v, int e) {
-  constexpr int per = DT == DSV_BF16 ? 2 : 1;  // elements per 32-bit word
-  const int wi = e / per;
-  const uint32_t w = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
-  if constexpr (DT == DSV_BF16)
-    return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
-  else
-    return __uint_as_float(w);
+  constexpr int per_half = DT == DSV_BF16 ? 4 : 2;
+  constexpr int bits = DT == DSV_BF16 ? 16 : 32;
+  const uint64_t lo = ((uint64_t)v.y << 32) | v.x, hi = ((uint64_t)v.w << 32) | v.z;
+  const uint64_t h = e >= per_half ? hi : lo;
+  const uint32_t w = (uint32_t)(h >> (bits * (e & (per_half - 1))));
+  return DT == DSV_BF16 ? __uint_as_float(w << 16) : __uint_as_float(w);
 }
 template <int DT>
 __device__ __forceinline__ void vec_set_dyn(uint4& v, int e, float x) {
-  constexpr int per = DT == DSV_BF16 ? 2 : 1;
-  const int wi = e / per;
-  uint32_t w = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
-  if constexpr (DT == DSV_BF16) {
-    const uint32_t bb = __float_as_uint(x) >> 16;
-    w = (e & 1) ? ((w & 0xffffu) | (bb << 16)) : ((w & 0xffff0000u) | bb);
-  } else {
-    w = __float_as_uint(x);
-  }
-  v.x = wi == 0 ? w : v.x;
-  v.y = wi == 1 ? w : v.y;
-  v.z = wi == 2 ? w : v.z;
-  v.w = wi == 3 ? w : v.w;
-}
-
-// Vector vi of a 16-byte-aligned row when vi < nfull (vectors lying wholly inside the row),
-// the -inf fill otherwise.  Branch-free (the address is clamped to vector nfull - 1 and the
-// result selected), so a thread keeps all of its loads in flight.  Needs nfull >= 1.
-template <int DT>
-__device__ __forceinline__ uint4 load_vec_fast(const char* rowp, int64_t vi, int64_t nfull) {
-  const uint32_t fill = DT == DSV_BF16 ? FILL_BF16 : FILL_F32;
-  const bool ok = vi < nfull;
-  const int64_t vc = ok ? vi : nfull - 1;
-  const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(rowp) + vc);
-  return make_uint4(ok ? t.x : fill, ok ? t.y : fill, ok ? t.z : fill, ok ? t.w : fill);
+  constexpr int per_half = DT == DSV_BF16 ? 4 : 2;
+  constexpr int bits = DT == DSV_BF16 ? 16 : 32;
+  constexpr uint64_t ones = DT == DSV_BF16 ? 0xffffull : 0xffffffffull;
+  uint64_t lo = ((uint64_t)v.y << 32) | v.x, hi = ((uint64_t)v.w << 32) | v.z;
+  const bool upper = e >= per_half;
+  const int sh = bits * (e & (per_half - 1));
+  const uint64_t nv = (uint64_t)(DT == DSV_BF16 ? (__float_as_uint(x) >> 16) : __float_as_uint(x));
+  const uint64_t h = ((upper ? hi : lo) & ~(ones << sh)) | (nv << sh);
+  lo = upper ? lo : h;
+  hi = upper ? h : hi;
+  v = make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
 }
 
 // Vector vi of a 16-byte-aligned row, no bounds check (the caller knows it is inside).
@@ -265,12 +255,20 @@ __device__ __forceinline__ void vec_set(uint4& v, int e, float x) {
 
 // Presence (additive) then repetition (multiplicative) penalty of one history token, each
 // step rounded to the logits dtype as the reference's in-place tensor ops do.
+// Branch-free (both the product and the quotient are formed); finite and infinite inputs.
+__device__ __forceinline__ float round_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
 template <int DT>
 __device__ __forceinline__ float penalize(float x, float presence, float repetition) {
   float x1 = x + (-presence);
-  if constexpr (DT == DSV_BF16) x1 = bf16_bits_to_f32(f32_to_bf16_bits(x1));
-  float x2 = x1 < 0.f ? x1 * repetition : x1 / repetition;
-  if constexpr (DT == DSV_BF16) x2 = bf16_bits_to_f32(f32_to_bf16_bits(x2));
+  if constexpr (DT == DSV_BF16) x1 = round_bf16(x1);
+  const float scaled = x1 * repetition;
+  const float divided = x1 / repetition;
+  float x2 = x1 < 0.f ? scaled : divided;
+  if constexpr (DT == DSV_BF16) x2 = round_bf16(x2);
   return x2;
 }
 
@@ -426,6 +424,31 @@ __device__ __forceinline__ bool topp_fails(int backend, double S_before, float p
 }
 
 __device__ __forceinline__ float clamp01(float q) { return (q >= 0.f && q <= 1.f) ? q : 0.f; }
+
+// The first cut tie of a key held by cnt values of probability p each, with mass sb and cb values
+// ahead of it in (value desc, id asc) order: the top-k rank, the min-p floor and the top-p test
+// are each monotone along that order.  Returns cnt when none of the ties is cut.
+__device__ __forceinline__ int64_t cut_index(int backend, int64_t cnt, float p, double sb, int64_t cb, int topk,
+                                             float min_p, float thr_minp, float top_p) {
+  int64_t fail = cnt;
+  if (min_p > 0.f && p < thr_minp) fail = 0;
+  if (cb >= (int64_t)topk)
+    fail = 0;
+  else if (cb + cnt > (int64_t)topk)
+    fail = fail < (int64_t)topk - cb ? fail : (int64_t)topk - cb;
+  if (fail > 0 && topp_fails(backend, sb + (double)(cnt - 1) * (double)p, p, top_p)) {
+    int64_t l0 = 0, l1 = cnt - 1;  // smallest failing tie
+    while (l0 < l1) {
+      const int64_t mid = (l0 + l1) >> 1;
+      if (topp_fails(backend, sb + (double)mid * (double)p, p, top_p))
+        l1 = mid;
+      else
+        l0 = mid + 1;
+    }
+    fail = fail < l0 ? fail : l0;
+  }
+  return fail;
+}
 
 // Append the lanes' values with h set to buf (slots from an LDS counter; values past cap are
 // counted but dropped).

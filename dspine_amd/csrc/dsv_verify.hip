@@ -3,15 +3,15 @@
 //
 // Launches of one verify step (no host synchronisation):
 //   k_prep   (requests)         penalty bitmap of each request's token history
-//   k_nuc    (side stream)      nucleus rows (a top-p / min-p cut with a large top-k): one
-//                               workgroup per row builds an LDS histogram of the 65536 bf16
-//                               values; Z, the cut (key + tie count) and the normaliser follow
-//                               from value counts
-//   k_chunk  (rows x C)         every other row, in chunks of 20480 bf16 / 10240 fp32 values held
-//                               in registers: max/argmax, softmax partial sums, exact top-k
-//                               candidates -- one nontemporal read of the logits
+//   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 10240 fp32 values held in
+//                               registers: max/argmax, softmax partial sums, exact top-k
+//                               candidates, nucleus value counts -- one read of the logits
 //   k_merge  (rows)             per row: Z, the filtered top-k support (id, P), P at the draft
-//                               token and the step's accept/reject decision
+//                               token and the step's accept/reject decision; nucleus rows (a
+//                               top-p / min-p cut with top-k > 64) find their cut from the chunk
+//                               pass's value counts
+//   k_nuc    (<= 64 workgroups) nucleus rows those counts do not settle: the full 65536-key
+//                               value histogram of the row
 //   k_bonus  (chunks x requests) a dense bonus row (unfiltered / nucleus) summed per thread in one
 //                               vector pass
 //   k_final  (requests)         accepted length from the row decisions, the bonus draw (support
@@ -23,7 +23,6 @@
 // Semantics follow runtime/worker.py:440-508 (target P, pytorch backend), sampling/rejection.py
 // :36-98 and sampling/sparse/accept.py:239-307 (chain rejection and residual resample).
 #include <float.h>
-#include <mutex>
 #include <string.h>
 
 #include "dsv_device.h"
@@ -44,6 +43,8 @@ struct KParams {
   int32_t* tties;         // [bs, NCH * BCT]: per-thread count of values at the cut key
   int32_t* step_ok;       // [rows]: 1 when the draft token verified by the row is accepted
   uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
+  uint32_t* hpart;        // [rows, C, HWIN / 2]: nucleus rows' per-chunk window counts (16-bit pairs)
+  uint32_t* nhist;        // [NUC_GRID, 65536]: full-histogram counts, one area per k_nuc workgroup
   int64_t pwords;
   int64_t bchunk;         // elements per bonus chunk = BCT * ept
   int32_t ept, nch;       // bonus elements per thread (multiple of 8), bonus chunks
@@ -298,6 +299,547 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
 }
 
 // ---------------------------------------------------------------------------------------
+// Nucleus rows (a top-p / min-p cut with top-k > 64).
+//
+// The chunk pass counts, per chunk, the values whose key lies in a window [wlo, kmax] below the
+// chunk max, where wlo is the lowest key whose probability bound exp((x - m_c) / T) / s_c (the
+// chunk's own softmax sum understates Z, so the bound is an upper bound on p) reaches half of
+// the row floor eps.  The row merge knows Z and the exact floor eps = (sum p - top_p - 1e-6) / V:
+// the values with p < eps hold less than sum p - top_p together, so the cut -- the first value
+// in (value desc, id asc) order that top-k, min-p or top-p removes -- is at or above the first
+// value below the lowest key kb with p(kb) >= eps.  When every chunk window reaches down to kb
+// the merged window counts decide the cut exactly; otherwise the row takes the full-histogram
+// path (k_nuc).
+// ---------------------------------------------------------------------------------------
+struct NucMergeShared {
+  uint32_t h[HWIN];  // merged counts, position q = kmax - key
+  uint32_t cw[16], ck[16];
+  double wm[CT / WAVE];
+  int64_t wc[CT / WAVE];
+  uint64_t cut[CT / WAVE];
+  double cutS[CT / WAVE];
+  uint64_t u[CT / WAVE];
+  int32_t red_i[CT / WAVE];
+  uint32_t kb_row;
+  float xtok;
+};
+
+// p of a nucleus row at its draft token and the step decision; RowSum out (wave 0).
+template <int DT>
+__device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int b, int s, RowSum rs, float T,
+                                               float xtok, int64_t tok, int64_t tie_tok) {
+  const bool kept = key_of<DT>(xtok) > rs.vcut || (key_of<DT>(xtok) == rs.vcut && tie_tok < (int64_t)rs.ktie);
+  rs.p_draft = (tok >= 0 && tok < P.a.vocab && kept) ? prob_of(xtok, T, rs.m_f, rs.invZ) / rs.S_f : 0.f;
+  const int32_t ok = tok >= 0 ? step_accept_wave(P.a, b, s, tok, rs.p_draft) : 0;
+  if (threadIdx.x == 0) {
+    P.rowsum[r] = rs;
+    P.step_ok[r] = ok;
+  }
+}
+
+// Values at key kv among ids [0, tok) of row r (penalised), summed over the workgroup.
+template <int DT, int NW>
+__device__ __forceinline__ int64_t ties_before(const KParams& P, int64_t r, int b, uint32_t kv, int64_t tok,
+                                               int32_t* red) {
+  const dsv_verify_args& a = P.a;
+  const char* rowp = row_ptr(a, r);
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  int32_t n = 0;
+  for (int64_t j = threadIdx.x; j < tok; j += blockDim.x) {
+    float x = load_elem<DT>(rowp, j);
+    if (pen && pen_test(P, b, j)) x = penalize<DT>(x, pres, rep);
+    n += key_of<DT>(x) == kv;
+  }
+  return block_sum<NW>(n, red);
+}
+
+template <int DT>
+__device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh) {
+  constexpr int NW = CT / WAVE;
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
+  const int C = P.C;
+  const ChunkStat* cs = P.cstat + r * C;
+  float m_l = -INFINITY;
+  int32_t arg_l = INT_MAX;
+  double s_l = 0.0;
+  uint32_t w_l = WIN_EMPTY, x_l = 0;
+  if (lane < C) {
+    m_l = cs[lane].m;
+    arg_l = cs[lane].arg;
+    s_l = cs[lane].s;
+    w_l = cs[lane].wlo;
+    x_l = cs[lane].kx;
+  }
+  float M = m_l;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+  const uint64_t at_max = __ballot(lane < C && m_l == M);
+  int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
+  if (arg == INT_MAX) arg = 0;
+  const float c2 = log2e_over(T);
+  const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
+  const float m_f = M / T;
+  const float invZ = (float)(1.0 / Z);
+  const uint32_t kmax = key_of<DT>(M);
+  uint32_t kcov = (lane < C && w_l != WIN_EMPTY) ? w_l : 0u;  // every chunk counted each key >= kcov
+  kcov = wave_max_u32(kcov);
+  if (tid < C) {
+    sh.cw[tid] = w_l;
+    sh.ck[tid] = w_l != WIN_EMPTY ? key_of<DT>(m_l) : 0u;
+  }
+  const float top_p = a.top_ps[b];
+  const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
+  const int topk = a.top_ks[b];
+  const int64_t tok = step_token(a, b, s);
+  if (tid == 0) {
+    const double eps = (Z * (double)invZ - (double)top_p - 1e-6) / (double)a.vocab;
+    uint32_t kb = 0x80u;  // the lowest finite key: no floor
+    if (eps > 0.0 && kmax >= 0x80u) {
+      uint32_t lo = 0x80u, hi = kmax;  // smallest key with p >= eps (p is non-decreasing in the key)
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if ((double)prob_of(value_of_key<DT>(mid), T, m_f, invZ) >= eps)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      kb = lo;
+    }
+    sh.kb_row = kb;
+    float xt = -INFINITY;
+    if (tok >= 0 && tok < a.vocab) {
+      xt = load_elem<DT>(row_ptr(a, r), tok);
+      if (P.pbits && pen_test(P, b, tok)) {
+        const float pres = a.presence ? a.presence[b] : 0.f;
+        const float rep = a.repetition ? a.repetition[b] : 1.f;
+        xt = penalize<DT>(xt, pres, rep);
+      }
+    }
+    sh.xtok = xt;
+  }
+  __syncthreads();
+  RowSum rs;
+  rs.mode = M_HIST;
+  rs.argmax = arg;
+  rs.kmax = kmax;
+  rs.vcut = 0u;
+  rs.ktie = INT_MAX;
+  rs.nlist = 0;
+  rs.flags = 0;
+  rs.norm = 0;
+  rs.m_f = m_f;
+  rs.invZ = invZ;
+  rs.Z = Z;
+  rs.S_kept = 1.0;
+  rs.S_f = 1.f;
+  rs.p_draft = 0.f;
+  if (kmax < 0x80u || kcov > sh.kb_row) {  // a window stops above the floor: full histogram
+    if (tid == 0) {
+      rs.flags = FLAG_FULL_HIST;
+      P.rowsum[r] = rs;
+      P.step_ok[r] = 0;
+    }
+    return;
+  }
+  // The cut is at or above the first value below the floor kb: only keys >= kb are scanned
+  // (the first value below kb, if the scan keeps every value, is found separately).
+  const uint32_t kscan = sh.kb_row > kcov ? sh.kb_row : kcov;
+  const int W = (int)(kmax - kscan) + 1;  // <= HWIN: the max's own chunk window ends at kmax
+  for (int q = tid; q < W; q += CT) {
+    const uint32_t k = kmax - (uint32_t)q;
+    uint32_t cnt = 0;
+    for (int c = 0; c < C; ++c) {
+      const uint32_t wl = sh.cw[c];
+      if (wl == WIN_EMPTY || k < wl || k > sh.ck[c]) continue;
+      const uint32_t o = k - wl;
+      const uint32_t word = P.hpart[(r * C + c) * (int64_t)(HWIN / 2) + (o >> 1)];
+      cnt += (word >> ((o & 1u) * 16u)) & 0xFFFFu;
+    }
+    sh.h[q] = cnt;
+  }
+  __syncthreads();
+  // descending scan: wave w owns positions [w*SL, (w+1)*SL)
+  const int SL = ((W + NW * WAVE - 1) / (NW * WAVE)) * WAVE;
+  const int q_end = (wid + 1) * SL < W ? (wid + 1) * SL : W;
+  const float thr_minp = prob_of(M, T, m_f, invZ) * min_p;
+  double mt = 0.0;
+  int64_t cw = 0;
+  for (int q = wid * SL + lane; q < q_end; q += WAVE) {
+    const uint32_t cnt = sh.h[q];
+    if (!cnt) continue;
+    mt += (double)cnt * (double)prob_of(value_of_key<DT>(kmax - (uint32_t)q), T, m_f, invZ);
+    cw += cnt;
+  }
+  mt = wave_sum(mt);
+  cw = wave_sum(cw);
+  if (lane == 0) {
+    sh.wm[wid] = mt;
+    sh.wc[wid] = cw;
+  }
+  __syncthreads();
+  double run_S = 0.0, m_total = 0.0;
+  int64_t run_C = 0;
+  for (int i = 0; i < NW; ++i) {
+    if (i < wid) {
+      run_S += sh.wm[i];
+      run_C += sh.wc[i];
+    }
+    m_total += sh.wm[i];
+  }
+  uint64_t cut = ~0ull;
+  double cutS = 0.0;
+  for (int q0 = wid * SL; q0 < q_end && cut == ~0ull; q0 += WAVE) {
+    const int q = q0 + lane;
+    const uint32_t cnt = q < q_end ? sh.h[q] : 0u;
+    if (__ballot(cnt != 0u) == 0ull) continue;
+    const uint32_t k = kmax - (uint32_t)q;
+    const float p = cnt ? prob_of(value_of_key<DT>(k), T, m_f, invZ) : 0.f;
+    double lo_m, hi_m;
+    const double it_m = wave_tiles((double)cnt * (double)p, lo_m, hi_m);
+    int64_t c_excl = cnt;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int64_t t = __shfl_up(c_excl, o, WAVE);
+      if (lane >= o) c_excl += t;
+    }
+    const int64_t it_c = __shfl(c_excl, WAVE - 1, WAVE);
+    c_excl -= cnt;
+    uint64_t f = ~0ull;
+    double fS = 0.0;
+    if (cnt) {
+      const double sb = run_S + lo_m;
+      const int64_t fail = cut_index(a.backend, cnt, p, sb, run_C + c_excl, topk, min_p, thr_minp, top_p);
+      if (fail < (int64_t)cnt) {
+        f = ((uint64_t)(uint32_t)fail << 32) | k;
+        fS = sb + (double)fail * (double)p;
+      }
+    }
+    const uint64_t who = __ballot(f != ~0ull);
+    if (who) {
+      const int src = __ffsll((long long)who) - 1;
+      cut = __shfl(f, src, WAVE);
+      cutS = __shfl(fS, src, WAVE);
+    }
+    run_S += it_m;
+    run_C += it_c;
+  }
+  if (lane == 0) {
+    sh.cut[wid] = cut;
+    sh.cutS[wid] = cutS;
+  }
+  __syncthreads();
+  uint64_t fc = ~0ull;
+  double fS = 0.0;
+  for (int i = 0; i < NW && fc == ~0ull; ++i) {
+    fc = sh.cut[i];
+    fS = sh.cutS[i];
+  }
+  if (fc != ~0ull) {
+    rs.vcut = (uint32_t)fc;
+    rs.ktie = (int32_t)(fc >> 32);
+    rs.S_kept = fS;
+  } else {
+    // every value at or above kscan is kept: the cut is the first value below kscan (tie 0)
+    uint64_t below = 0;
+    for (int c = 0; c < C; ++c) {
+      const uint32_t wl = sh.cw[c];
+      if (wl == WIN_EMPTY) continue;
+      const uint32_t kh = sh.ck[c] < kscan ? sh.ck[c] : kscan - 1u;
+      for (uint32_t k = wl + (uint32_t)tid; wl <= kh && k <= kh; k += CT) {
+        const uint32_t o = k - wl;
+        const uint32_t word = P.hpart[(r * C + c) * (int64_t)(HWIN / 2) + (o >> 1)];
+        if ((word >> ((o & 1u) * 16u)) & 0xFFFFu) below = below > k ? below : k;
+      }
+    }
+    if (lane < C) below = below > x_l ? below : x_l;
+    below = block_max_u64<NW>(below, sh.u);
+    rs.vcut = (uint32_t)below;
+    rs.ktie = below ? 0 : INT_MAX;
+    rs.S_kept = m_total;
+  }
+  rs.S_f = (float)rs.S_kept;
+  const float xt = sh.xtok;
+  int64_t tie_tok = 0;
+  if (tok >= 0 && key_of<DT>(xt) == rs.vcut && rs.ktie > 0 && rs.ktie != INT_MAX)
+    tie_tok = ties_before<DT, NW>(P, r, b, rs.vcut, tok, sh.red_i);
+  if (tid < WAVE) nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok);
+}
+
+// ---------------------------------------------------------------------------------------
+// k_nuc: nucleus rows whose windows fall short -- the full 65536-key value histogram, built in
+// LDS slices of at most NUC_SLICE values (16-bit counters cannot wrap) and accumulated in
+// registers; one workgroup per row, persistent over the rows.
+// ---------------------------------------------------------------------------------------
+constexpr int NUC_GRID = 64;  // k_nuc workgroups (persistent over the full-histogram rows)
+constexpr int NUC_WAVES = NUC_THREADS / WAVE;
+constexpr int NUC_WPW = HIST_WORDS / NUC_WAVES;  // histogram words per wave
+constexpr int NUC_ITERS = NUC_WPW / WAVE;        // words per lane
+
+struct NucShared {
+  double d[NUC_WAVES];
+  double wm[NUC_WAVES];
+  int64_t wc[NUC_WAVES];
+  uint64_t cut[NUC_WAVES];  // (tie << 32 | key) of each wave's first cut key, ~0 if none
+  double cutS[NUC_WAVES];
+  int32_t ri[NUC_WAVES];
+  int32_t mine[NUC_THREADS];  // this workgroup's rows among the current block of rows
+  int32_t nmine;
+  float xtok;
+  uint32_t ktok;
+};
+
+// Word wd of the histogram holds the 16-bit counts of keys 2wd (low half) and 2wd+1 (high).
+// Wave w owns words HIST_WORDS-1-w*NUC_WPW-64*i-lane for i = 0, 1, ...: consecutive lanes read
+// consecutive words (no bank conflicts) and each wave's slice runs in descending key order.
+__device__ __forceinline__ int nuc_word(int wid, int i, int lane) {
+  return HIST_WORDS - 1 - wid * NUC_WPW - WAVE * i - lane;
+}
+
+template <int DT, bool ALIGNED>
+__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh) {
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
+  int b = 0, s = 0;
+  row_request(a, r, b, s);
+  RowSum rs = P.rowsum[r];
+  const int64_t V = a.vocab;
+  const char* rowp = row_ptr(a, r);
+  const float T = a.temperatures[b];
+  const int topk = a.top_ks[b];
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const int64_t tok = step_token(a, b, s);
+  if (tid == 0) {
+    float xt = -INFINITY;
+    if (tok >= 0 && tok < V) {
+      xt = load_elem<DT>(rowp, tok);
+      if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
+    }
+    sh.xtok = xt;
+    sh.ktok = key_of<DT>(xt);
+  }
+  __syncthreads();
+  const uint32_t ktok = sh.ktok;
+  // 32-bit counts of key pairs, this workgroup's own area: (key 2wd, key 2wd + 1) at index wd
+  uint2* gsum = reinterpret_cast<uint2*>(P.nhist) + (int64_t)blockIdx.x * HIST_WORDS;
+  uint32_t tie_before = 0;
+  auto count = [&](float x, int64_t j) {
+    const uint32_t k = key_of<DT>(x);
+    if (k != NEG_INF_BF16_KEY) {
+      atomicAdd(&hist[k >> 1], 1u << ((k & 1u) * 16u));
+      tie_before += (k == ktok && j < tok) ? 1u : 0u;
+    }
+  };
+  constexpr int U = 4;
+  for (int64_t s0 = 0; s0 < V; s0 += NUC_SLICE) {
+    const int64_t s1 = s0 + NUC_SLICE < V ? s0 + NUC_SLICE : V;
+    {
+      uint4* h4 = reinterpret_cast<uint4*>(hist);
+      for (int i = tid; i < HIST_WORDS / 4; i += NUC_THREADS) h4[i] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const int64_t vb = s0 / 8;                              // NUC_SLICE is a multiple of 8
+    const int64_t ve = ALIGNED ? s1 / 8 : (s1 + 7) / 8;     // vectors read whole
+    for (int64_t q0 = vb; q0 < ve; q0 += (int64_t)NUC_THREADS * U) {
+      uint4 w[U];
+      uint32_t bits[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
+        if constexpr (ALIGNED)
+          w[u] = load_vec_raw(rowp, vi < ve ? vi : ve - 1);
+        else
+          w[u] = load_vec<DT>(rowp, vi, s1, false);
+        const uint32_t bw = pen ? pen_bits(P, b, (vi < ve ? vi : vb) * 8, 8) : 0u;
+        bits[u] = vi < ve ? bw : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
+        if (vi >= ve) continue;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t j = vi * 8 + e;
+          float x = vec_elem<DT>(w[u], e);
+          if ((bits[u] >> e) & 1u) x = penalize<DT>(x, pres, rep);
+          if (ALIGNED || j < s1) count(x, j);
+        }
+      }
+    }
+    if (ALIGNED && tid == 0)
+      for (int64_t j = ve * 8; j < s1; ++j) {  // the row's partial last vector
+        float x = load_elem<DT>(rowp, j);
+        if (pen && pen_test(P, b, j)) x = penalize<DT>(x, pres, rep);
+        count(x, j);
+      }
+    __syncthreads();
+    for (int i = 0; i < NUC_ITERS; ++i) {  // each thread owns its words: no atomics
+      const int wd = nuc_word(wid, i, lane);
+      const uint32_t h = hist[wd];
+      uint2 g = s0 ? gsum[wd] : make_uint2(0u, 0u);
+      g.x += h & 0xFFFFu;
+      g.y += h >> 16;
+      gsum[wd] = g;
+    }
+    __syncthreads();
+  }
+  const int64_t tie_tok = (int64_t)block_sum<NUC_WAVES>((double)tie_before, sh.d);
+  const float m_f = rs.m_f, invZ = rs.invZ;
+  const float M = value_of_key<DT>(rs.kmax);
+  // mass per wave (descending-key slices), then each wave's starting prefix
+  double mt = 0.0;
+  int64_t cw = 0;
+  for (int i = 0; i < NUC_ITERS; ++i) {
+    const int wd = nuc_word(wid, i, lane);
+    const uint2 g = gsum[wd];
+    if (g.y) {
+      mt += (double)g.y * (double)prob_of(value_of_key<DT>(2u * (uint32_t)wd + 1u), T, m_f, invZ);
+      cw += g.y;
+    }
+    if (g.x) {
+      mt += (double)g.x * (double)prob_of(value_of_key<DT>(2u * (uint32_t)wd), T, m_f, invZ);
+      cw += g.x;
+    }
+  }
+  mt = wave_sum(mt);
+  cw = wave_sum(cw);
+  if (lane == 0) {
+    sh.wm[wid] = mt;
+    sh.wc[wid] = cw;
+  }
+  __syncthreads();
+  double run_S = 0.0, m_total = 0.0;
+  int64_t run_C = 0;
+  for (int i = 0; i < NUC_WAVES; ++i) {
+    if (i < wid) {
+      run_S += sh.wm[i];
+      run_C += sh.wc[i];
+    }
+    m_total += sh.wm[i];
+  }
+  const float top_p = a.top_ps[b];
+  const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
+  const float thr_minp = prob_of(M, T, m_f, invZ) * min_p;
+  uint64_t cut = ~0ull;
+  double cutS = 0.0;
+  for (int i = 0; i < NUC_ITERS && cut == ~0ull; ++i) {
+    const int wd = nuc_word(wid, i, lane);
+    const uint2 g = gsum[wd];
+    const uint32_t c_hi = g.y, c_lo = g.x;
+    if (__ballot((c_hi | c_lo) != 0u) == 0ull) continue;
+    const uint32_t k_hi = 2u * (uint32_t)wd + 1u, k_lo = 2u * (uint32_t)wd;
+    const float p_hi = c_hi ? prob_of(value_of_key<DT>(k_hi), T, m_f, invZ) : 0.f;
+    const float p_lo = c_lo ? prob_of(value_of_key<DT>(k_lo), T, m_f, invZ) : 0.f;
+    double lo_m, hi_m;
+    const double it_m = wave_tiles((double)c_hi * (double)p_hi + (double)c_lo * (double)p_lo, lo_m, hi_m);
+    const int64_t c_word = (int64_t)c_hi + c_lo;
+    int64_t c_excl = c_word;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int64_t t = __shfl_up(c_excl, o, WAVE);
+      if (lane >= o) c_excl += t;
+    }
+    const int64_t it_c = __shfl(c_excl, WAVE - 1, WAVE);
+    c_excl -= c_word;
+    uint64_t f = ~0ull;
+    double fS = 0.0;
+    double sb = run_S + lo_m;
+    int64_t cb = run_C + c_excl;
+    if (c_hi) {
+      const int64_t fail = cut_index(a.backend, c_hi, p_hi, sb, cb, topk, min_p, thr_minp, top_p);
+      if (fail < (int64_t)c_hi) {
+        f = ((uint64_t)(uint32_t)fail << 32) | k_hi;
+        fS = sb + (double)fail * (double)p_hi;
+      } else {
+        sb += (double)c_hi * (double)p_hi;
+        cb += c_hi;
+      }
+    }
+    if (c_lo && f == ~0ull) {
+      const int64_t fail = cut_index(a.backend, c_lo, p_lo, sb, cb, topk, min_p, thr_minp, top_p);
+      if (fail < (int64_t)c_lo) {
+        f = ((uint64_t)(uint32_t)fail << 32) | k_lo;
+        fS = sb + (double)fail * (double)p_lo;
+      }
+    }
+    const uint64_t who = __ballot(f != ~0ull);
+    if (who) {
+      const int src = __ffsll((long long)who) - 1;
+      cut = __shfl(f, src, WAVE);
+      cutS = __shfl(fS, src, WAVE);
+    }
+    run_S += it_m;
+    run_C += it_c;
+  }
+  if (lane == 0) {
+    sh.cut[wid] = cut;
+    sh.cutS[wid] = cutS;
+  }
+  __syncthreads();
+  if (tid < WAVE) {
+    uint64_t fc = ~0ull;
+    double fS = 0.0;
+    for (int i = 0; i < NUC_WAVES && fc == ~0ull; ++i) {
+      fc = sh.cut[i];
+      fS = sh.cutS[i];
+    }
+    if (fc == ~0ull) {
+      rs.vcut = 0u;
+      rs.ktie = INT_MAX;
+      rs.S_kept = m_total;
+    } else {
+      rs.vcut = (uint32_t)fc;
+      rs.ktie = (int32_t)(fc >> 32);
+      rs.S_kept = fS;
+    }
+    rs.S_f = (float)rs.S_kept;
+    nucleus_finish<DT>(P, r, b, s, rs, T, sh.xtok, tok, tie_tok);
+  }
+  __syncthreads();
+}
+
+// The i-th full-histogram row in row order goes to workgroup i % gridDim.x.
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ NucShared sh;
+  const dsv_verify_args& a = P.a;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(dyn);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
+  int64_t seen = 0;  // full-histogram rows before the current block of rows
+  for (int64_t r0 = 0; r0 < a.rows; r0 += NUC_THREADS) {
+    const int64_t r = r0 + tid;
+    bool f = false;
+    if (r < a.rows) {
+      const RowSum& rs = P.rowsum[r];
+      f = rs.mode == M_HIST && (rs.flags & FLAG_FULL_HIST);
+    }
+    const uint64_t bal = __ballot(f);
+    if (lane == 0) sh.ri[wid] = __popcll(bal);
+    if (tid == 0) sh.nmine = 0;
+    __syncthreads();
+    int64_t before = seen, total = 0;
+    for (int i = 0; i < NUC_WAVES; ++i) {
+      if (i < wid) before += sh.ri[i];
+      total += sh.ri[i];
+    }
+    const int64_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
+    if (f && rank % gridDim.x == blockIdx.x) sh.mine[atomicAdd(&sh.nmine, 1)] = (int32_t)r;
+    __syncthreads();
+    const int nm = sh.nmine;
+    for (int i = 0; i < nm; ++i) {
+      if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, sh.mine[i], hist, sh);
+    }
+    seen += total;
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // k_chunk: one pass over a 20480-value (bf16) / 10240-value (fp32) chunk held in registers
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
@@ -306,9 +848,11 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   constexpr int CHE = Elems<DT>::chunk;
   __shared__ uint64_t cbuf[CAND_CAP];
   __shared__ uint32_t hist256[256];
+  __shared__ uint32_t hwin[HWIN / 2];
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
   __shared__ int32_t s_cnt;
+  __shared__ uint32_t s_wlo;
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
@@ -341,7 +885,6 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       b = __builtin_amdgcn_readfirstlane(b);
       s = __builtin_amdgcn_readfirstlane(s);
       mode = row_mode(a, b, 0);
-      if (mode == M_HIST) return;
     } else {
       mode = M_LIST;  // top-k rows
     }
@@ -417,7 +960,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   out.s = 0.0;
   out.ncand = 0;
   out.flags = 0;
-  out.pad[0] = out.pad[1] = 0;
+  out.wlo = WIN_EMPTY;
+  out.kx = 0u;
 
   if (P.softmax && mode != M_GREEDY && cbest) {
     const float c2 = log2e_over(T);
@@ -431,6 +975,64 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
     out.s = block_sum<CT / WAVE>((double)st_, sd);
     reg_fence(v);
+  }
+
+  if constexpr (DT == DSV_BF16) {
+    if (mode == M_HIST) {
+      // counts of the values in the window [wlo, kmax] that can reach the nucleus cut: wlo is
+      // the higher of kmax - (HWIN - 1) and the lowest key whose bound exp((x - m) / T) / s
+      // reaches half of the row floor (1 - top_p - 1e-5) / V (the nucleus section above)
+      if (tid == 0) {
+        uint32_t wlo = WIN_EMPTY;
+        if (cbest) {
+          const uint32_t kmax = unpack_key(cbest);
+          uint32_t kb = 0x80u;  // the lowest finite key
+          const float eps = (0.99998f - a.top_ps[b]) / (float)V * 0.5f;
+          if (eps > 0.f && kmax > 0x80u) {
+            const float c2 = log2e_over(T);
+            const float inv_s = (float)(1.0 / out.s);
+            uint32_t l0 = 0x80u, l1 = kmax;
+            while (l0 < l1) {
+              const uint32_t mid = (l0 + l1) >> 1;
+              if (__builtin_amdgcn_exp2f((value_of_key<DT>(mid) - out.m) * c2) * inv_s >= eps)
+                l1 = mid;
+              else
+                l0 = mid + 1;
+            }
+            kb = l0;
+          }
+          const uint32_t wfloor = kmax >= (uint32_t)HWIN - 1u ? kmax - ((uint32_t)HWIN - 1u) : 0u;
+          wlo = kb > wfloor ? kb : wfloor;
+        }
+        s_wlo = wlo;
+      }
+      for (int i = tid; i < HWIN / 2; i += CT) hwin[i] = 0u;
+      __syncthreads();
+      const uint32_t wlo = s_wlo;
+      uint32_t kx = 0u;
+      if (wlo != WIN_EMPTY) {
+#pragma unroll
+        for (int u = 0; u < CV; ++u) {
+          reg_fence1(v[u]);
+#pragma unroll
+          for (int e = 0; e < n; ++e) {
+            const uint32_t k = key_of<DT>(vec_elem<DT>(v[u], e));
+            if (k >= wlo)
+              atomicAdd(&hwin[(k - wlo) >> 1], 1u << (((k - wlo) & 1u) * 16u));
+            else
+              kx = k > kx ? k : kx;
+          }
+        }
+      }
+      kx = (uint32_t)block_max_u64<CT / WAVE>((uint64_t)kx, su);  // (its barriers order the counts)
+      if (wlo != WIN_EMPTY) {
+        const int nw = (int)((unpack_key(cbest) - wlo) >> 1) + 1;
+        uint32_t* dst = P.hpart + (r * C + c) * (int64_t)(HWIN / 2);
+        for (int i = tid; i < nw; i += CT) dst[i] = hwin[i];
+      }
+      out.wlo = wlo;
+      out.kx = kx;
+    }
   }
 
   if (mode == M_LIST) {
@@ -496,6 +1098,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 template <int DT>
 __global__ __launch_bounds__(CT) void k_merge(KParams P) {
   __shared__ MergeShared ms;
+  __shared__ NucMergeShared ns;
   const dsv_verify_args& a = P.a;
   const int64_t r = blockIdx.x;
   int b, s;
@@ -507,319 +1110,11 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
     return;
   }
   const int mode = row_mode(a, b, 0);
-  if (mode == M_HIST) return;  // k_nuc
+  if (mode == M_HIST) {
+    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, a.temperatures[b], ns);
+    return;
+  }
   merge_row<DT>(P, r, b, s, mode, a.temperatures[b], ms);
-}
-
-// ---------------------------------------------------------------------------------------
-// k_nuc: nucleus rows from an LDS histogram of the 65536 bf16 values (persistent workgroups)
-// ---------------------------------------------------------------------------------------
-constexpr int NUC_WAVES = NUC_THREADS / WAVE;
-constexpr int NUC_WPW = HIST_WORDS / NUC_WAVES;  // histogram words per wave
-constexpr int NUC_ITERS = NUC_WPW / WAVE;        // words per lane
-
-struct NucShared {
-  double d[NUC_WAVES];
-  double wm[NUC_WAVES];
-  int64_t wc[NUC_WAVES];
-  uint64_t u[NUC_WAVES];
-  uint64_t cut[NUC_WAVES];  // (tie << 32 | key) of each wave's first failing key, ~0 if none
-  double cutS[NUC_WAVES];
-  int32_t ri[NUC_WAVES];
-  int32_t mine[NUC_THREADS];  // this workgroup's rows among the current 512
-  int32_t nmine;
-  float xtok;
-  uint32_t ktok;
-};
-
-// Word wd of the histogram holds the 16-bit counts of keys 2wd (low half) and 2wd+1 (high).
-// Wave w scans words HIST_WORDS-1-w*NUC_WPW-64*i-lane for i = 0, 1, ...: consecutive lanes
-// read consecutive words (no bank conflicts) and the scan runs in descending key order.
-__device__ __forceinline__ int nuc_word(int wid, int i, int lane) {
-  return HIST_WORDS - 1 - wid * NUC_WPW - WAVE * i - lane;
-}
-
-template <int DT, bool ALIGNED>
-__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh) {
-  const dsv_verify_args& a = P.a;
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
-  int b = 0, s = 0;
-  row_request(a, r, b, s);
-  const int64_t V = a.vocab;
-  const char* rowp = row_ptr(a, r);
-  const float T = a.temperatures[b];
-  const int topk = a.top_ks[b];
-  const bool pen = P.pbits != nullptr;
-  float pres = 0.f, rep = 1.f;
-  {
-    uint4* h4 = reinterpret_cast<uint4*>(hist);
-    for (int i = tid; i < HIST_WORDS / 4; i += NUC_THREADS) h4[i] = make_uint4(0, 0, 0, 0);
-  }
-  if (pen) {
-    pres = a.presence ? a.presence[b] : 0.f;
-    rep = a.repetition ? a.repetition[b] : 1.f;
-  }
-  const int64_t tok = step_token(a, b, s);
-  if (tid == 0) {
-    float xt = -INFINITY;
-    if (tok >= 0 && tok < V) {
-      xt = load_elem<DT>(rowp, tok);
-      if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
-    }
-    sh.xtok = xt;
-    sh.ktok = key_of<DT>(xt);
-  }
-  __syncthreads();
-  const uint32_t ktok = sh.ktok;
-  constexpr int U = 4;
-  const int64_t NVf = ALIGNED ? V / 8 : (V + 7) / 8;  // vectors read whole (the rest: thread 0)
-  uint64_t best = 0ull;
-  uint32_t tie_before = 0, nfin = 0;
-  auto count = [&](float x, int64_t j) {
-    const uint32_t k = key_of<DT>(x);
-    const uint64_t pk = pack(k, j);
-    best = pk > best ? pk : best;
-    if (k != NEG_INF_BF16_KEY) {
-      atomicAdd(&hist[k >> 1], 1u << ((k & 1u) * 16u));
-      ++nfin;
-      tie_before += (k == ktok && j < tok) ? 1u : 0u;
-    }
-  };
-  for (int64_t q0 = 0; q0 < NVf; q0 += (int64_t)NUC_THREADS * U) {
-    uint4 w[U];
-    uint32_t bits[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
-      if constexpr (ALIGNED)
-        w[u] = load_vec_raw(rowp, vi < NVf ? vi : NVf - 1);
-      else
-        w[u] = load_vec<DT>(rowp, vi, V, false);
-      const uint32_t bw = pen ? pen_bits(P, b, (vi < NVf ? vi : 0) * 8, 8) : 0u;
-      bits[u] = vi < NVf ? bw : 0u;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
-      if (vi >= NVf) continue;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t j = vi * 8 + e;
-        float x = vec_elem<DT>(w[u], e);
-        if ((bits[u] >> e) & 1u) x = penalize<DT>(x, pres, rep);
-        if (ALIGNED || j < V) count(x, j);
-      }
-    }
-  }
-  if (ALIGNED && tid == 0)
-    for (int64_t j = NVf * 8; j < V; ++j) {  // the row's partial last vector
-      float x = load_elem<DT>(rowp, j);
-      if (pen && pen_test(P, b, j)) x = penalize<DT>(x, pres, rep);
-      count(x, j);
-    }
-  __syncthreads();
-  const uint64_t gbest = block_max_u64<NUC_WAVES>(best, sh.u);
-  const uint32_t kmax = unpack_key(gbest);
-  const float M = value_of_key<DT>(kmax);
-  const float m_f = M / T;
-  const uint32_t nfin_all = (uint32_t)block_sum<NUC_WAVES>((double)nfin, sh.d);
-  const uint32_t tie_tok = (uint32_t)block_sum<NUC_WAVES>((double)tie_before, sh.d);
-  // Z and the value counts
-  double zt = 0.0, ct = 0.0;
-  for (int i = 0; i < NUC_ITERS; ++i) {
-    const int wd = nuc_word(wid, i, lane);
-    const uint32_t h = hist[wd];
-    if (!h) continue;
-#pragma unroll
-    for (int half = 1; half >= 0; --half) {
-      const uint32_t cnt = (h >> (16 * half)) & 0xFFFFu;
-      if (!cnt) continue;
-      const uint32_t k = 2u * (uint32_t)wd + (uint32_t)half;
-      zt += (double)cnt * (double)expf(value_of_key<DT>(k) / T - m_f);
-      ct += (double)cnt;
-    }
-  }
-  const double Z = block_sum<NUC_WAVES>(zt, sh.d);
-  const double counted = block_sum<NUC_WAVES>(ct, sh.d);
-  const float invZ = (float)(1.0 / Z);
-  // mass per wave (descending-key slices), then each wave's starting prefix
-  double mt = 0.0;
-  int64_t cw = 0;
-  for (int i = 0; i < NUC_ITERS; ++i) {
-    const int wd = nuc_word(wid, i, lane);
-    const uint32_t h = hist[wd];
-    if (!h) continue;
-#pragma unroll
-    for (int half = 1; half >= 0; --half) {
-      const uint32_t cnt = (h >> (16 * half)) & 0xFFFFu;
-      if (!cnt) continue;
-      const uint32_t k = 2u * (uint32_t)wd + (uint32_t)half;
-      mt += (double)cnt * (double)prob_of(value_of_key<DT>(k), T, m_f, invZ);
-      cw += cnt;
-    }
-  }
-  mt = wave_sum(mt);
-  cw = wave_sum(cw);
-  if (lane == 0) {
-    sh.wm[wid] = mt;
-    sh.wc[wid] = cw;
-  }
-  __syncthreads();
-  double run_S = 0.0, m_total = 0.0;
-  int64_t run_C = 0;
-  for (int i = 0; i < NUC_WAVES; ++i) {
-    if (i < wid) {
-      run_S += sh.wm[i];
-      run_C += sh.wc[i];
-    }
-    m_total += sh.wm[i];
-  }
-  const float top_p = a.top_ps[b];
-  const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
-  const float thr_minp = prob_of(M, T, m_f, invZ) * min_p;
-  // walk this wave's slice in descending key order; first (key, tie) that is cut
-  uint64_t cut = ~0ull;
-  double cutS = 0.0;
-  for (int i = 0; i < NUC_ITERS && cut == ~0ull; ++i) {
-    const int wd = nuc_word(wid, i, lane);
-    const uint32_t h = hist[wd];
-    if (__ballot(h != 0u) == 0ull) continue;
-    const uint32_t c_hi = h >> 16, c_lo = h & 0xFFFFu;
-    const uint32_t k_hi = 2u * (uint32_t)wd + 1u, k_lo = 2u * (uint32_t)wd;
-    const float p_hi = c_hi ? prob_of(value_of_key<DT>(k_hi), T, m_f, invZ) : 0.f;
-    const float p_lo = c_lo ? prob_of(value_of_key<DT>(k_lo), T, m_f, invZ) : 0.f;
-    const double m_word = (double)c_hi * (double)p_hi + (double)c_lo * (double)p_lo;
-    const int64_t c_word = (int64_t)c_hi + c_lo;
-    double lo_m, hi_m;
-    const double it_m = wave_tiles(m_word, lo_m, hi_m);
-    int64_t c_excl = c_word;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int64_t t = __shfl_up(c_excl, o, WAVE);
-      if (lane >= o) c_excl += t;
-    }
-    const int64_t it_c = __shfl(c_excl, WAVE - 1, WAVE);
-    c_excl -= c_word;
-    // this lane's first failing (key, tie), if any
-    uint64_t f = ~0ull;
-    double fS = 0.0;
-    double sb = run_S + lo_m;
-    int64_t cb = run_C + c_excl;
-#pragma unroll
-    for (int half = 1; half >= 0; --half) {
-      const uint32_t cnt = half ? c_hi : c_lo;
-      const uint32_t k = half ? k_hi : k_lo;
-      const float p = half ? p_hi : p_lo;
-      if (!cnt || f != ~0ull) continue;
-      int64_t fail = cnt;
-      if (min_p > 0.f && p < thr_minp) fail = 0;
-      if (cb >= (int64_t)topk)
-        fail = 0;
-      else if (cb + (int64_t)cnt > (int64_t)topk)
-        fail = fail < (int64_t)topk - cb ? fail : (int64_t)topk - cb;
-      if (fail > 0 && topp_fails(a.backend, sb + (double)(cnt - 1) * (double)p, p, top_p)) {
-        int64_t l0 = 0, l1 = cnt - 1;  // smallest failing tie (monotone in the tie index)
-        while (l0 < l1) {
-          const int64_t mid = (l0 + l1) >> 1;
-          if (topp_fails(a.backend, sb + (double)mid * (double)p, p, top_p))
-            l1 = mid;
-          else
-            l0 = mid + 1;
-        }
-        fail = fail < l0 ? fail : l0;
-      }
-      if (fail < (int64_t)cnt) {
-        f = ((uint64_t)(uint32_t)fail << 32) | k;
-        fS = sb + (double)fail * (double)p;
-      } else {
-        sb += (double)cnt * (double)p;
-        cb += cnt;
-      }
-    }
-    const uint64_t who = __ballot(f != ~0ull);
-    if (who) {
-      const int src = __ffsll((long long)who) - 1;
-      cut = __shfl(f, src, WAVE);
-      cutS = __shfl(fS, src, WAVE);
-    }
-    run_S += it_m;
-    run_C += it_c;
-  }
-  if (lane == 0) {
-    sh.cut[wid] = cut;
-    sh.cutS[wid] = cutS;
-  }
-  __syncthreads();
-  if (tid < WAVE) {
-    uint64_t fc = ~0ull;
-    double fS = 0.0;
-    for (int i = 0; i < NUC_WAVES && fc == ~0ull; ++i) {
-      fc = sh.cut[i];
-      fS = sh.cutS[i];
-    }
-    RowSum rs;
-    rs.mode = M_HIST;
-    rs.argmax = gbest ? unpack_id(gbest) : 0;
-    rs.kmax = kmax;
-    rs.nlist = 0;
-    rs.flags = counted != (double)nfin_all ? FLAG_HIST_OVERFLOW : 0;
-    rs.norm = 0;
-    rs.m_f = m_f;
-    rs.invZ = invZ;
-    rs.Z = Z;
-    if (fc == ~0ull) {
-      rs.vcut = 0u;
-      rs.ktie = INT_MAX;
-      rs.S_kept = m_total;
-    } else {
-      rs.vcut = (uint32_t)fc;
-      rs.ktie = (int32_t)(fc >> 32);
-      rs.S_kept = fS;
-    }
-    rs.S_f = (float)rs.S_kept;
-    const bool kept = ktok > rs.vcut || (ktok == rs.vcut && (int64_t)tie_tok < (int64_t)rs.ktie);
-    rs.p_draft = (tok >= 0 && tok < V && kept) ? prob_of(sh.xtok, T, m_f, invZ) / rs.S_f : 0.f;
-    const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
-    if (tid == 0) {
-      P.rowsum[r] = rs;
-      P.step_ok[r] = ok;
-    }
-  }
-  __syncthreads();
-}
-
-// Persistent workgroups: the i-th nucleus row in row order goes to workgroup i % gridDim.x.
-template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
-  extern __shared__ __align__(16) unsigned char dyn[];
-  __shared__ NucShared sh;
-  const dsv_verify_args& a = P.a;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(dyn);
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
-  int64_t seen = 0;  // nucleus rows before the current block of rows
-  for (int64_t r0 = 0; r0 < a.rows; r0 += NUC_THREADS) {
-    const int64_t r = r0 + tid;
-    int b, s;
-    const bool f = r < a.rows && row_request(a, r, b, s) && row_mode(a, b, 0) == M_HIST;
-    const uint64_t bal = __ballot(f);
-    if (lane == 0) sh.ri[wid] = __popcll(bal);
-    if (tid == 0) sh.nmine = 0;
-    __syncthreads();
-    int64_t before = seen, total = 0;
-    for (int i = 0; i < NUC_WAVES; ++i) {
-      if (i < wid) before += sh.ri[i];
-      total += sh.ri[i];
-    }
-    const int64_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
-    if (f && rank % gridDim.x == blockIdx.x) sh.mine[atomicAdd(&sh.nmine, 1)] = (int32_t)r;
-    __syncthreads();
-    const int nm = sh.nmine;
-    for (int i = 0; i < nm; ++i) {
-      if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, sh.mine[i], hist, sh);
-    }
-    seen += total;
-    __syncthreads();
-  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1318,7 +1613,7 @@ using namespace dsv;
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, bchunks, qrank, tmass, tties, step_ok, pbits, total;
+  int64_t rowsum, lists, cstat, cand, hpart, nhist, bchunks, qrank, tmass, tties, step_ok, pbits, total;
 };
 static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
   if (dtype == DSV_BF16) {
@@ -1351,6 +1646,8 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.lists, rows * DSV_LIST_K * (int64_t)sizeof(ListEntry));
   take(w.cstat, rows * C * (int64_t)sizeof(ChunkStat));
   take(w.cand, rows * C * (int64_t)kcand * 8);
+  take(w.hpart, kcand ? rows * C * (int64_t)(HWIN / 2) * 4 : 0);
+  take(w.nhist, kcand ? (int64_t)NUC_GRID * 65536 * 4 : 0);
   take(w.bchunks, (int64_t)bs * NCH * (int64_t)sizeof(BonusChunk));
   take(w.qrank, (int64_t)bs * QMAX * 4);
   take(w.tmass, (int64_t)bs * NCH * BCT * 8);
@@ -1369,39 +1666,6 @@ extern "C" int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab) {
   return ws_layout(rows, 1, vocab, DSV_F32, 0, false).total;
 }
 
-// Side stream + events per device for the nucleus kernel (default priority).
-struct SideStream {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-static std::mutex g_side_mu;
-static SideStream g_side[64];
-
-static int side_stream(SideStream** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) DSV_FAIL(DSV_ERR_LAUNCH, "no current HIP device");
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream& ss = g_side[dev];
-  if (!ss.s) {
-    if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
-      DSV_FAIL(DSV_ERR_LAUNCH, "cannot create the side stream");
-  }
-  *out = &ss;
-  return DSV_OK;
-}
-
-static int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    hipDeviceProp_t prop;
-    cached[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
-  }
-  return cached[dev];
-}
 
 extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
@@ -1452,6 +1716,8 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.lists = reinterpret_cast<ListEntry*>(ws + w.lists);
   P.cstat = reinterpret_cast<ChunkStat*>(ws + w.cstat);
   P.cand = reinterpret_cast<uint64_t*>(ws + w.cand);
+  P.hpart = reinterpret_cast<uint32_t*>(ws + w.hpart);
+  P.nhist = reinterpret_cast<uint32_t*>(ws + w.nhist);
   P.bchunks = reinterpret_cast<BonusChunk*>(ws + w.bchunks);
   P.qrank = reinterpret_cast<int32_t*>(ws + w.qrank);
   P.tmass = reinterpret_cast<double*>(ws + w.tmass);
@@ -1480,35 +1746,25 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
       hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
       DSV_CHECK_LAUNCH("k_prep");
     }
-    SideStream* side = nullptr;
-    if (hist_possible) {
-      int rc = side_stream(&side);
-      if (rc) return rc;
-      if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
-        DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot fork the side stream");
-      const int ncu = num_cus();
-      const int grid = (int)(a.rows < ncu ? a.rows : ncu);
-      if (P.aligned) {
-        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)nuc_lds);
-        hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, side->s, P);
-      } else {
-        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)nuc_lds);
-        hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, side->s, P);
-      }
-      DSV_CHECK_LAUNCH("k_nuc");
-      if (hipEventRecord(side->join, side->s) != hipSuccess)
-        DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the side-stream join");
-    }
     launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * C), stream);
     if (a.logits_dtype == DSV_BF16)
       hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
     else
       hipLaunchKernelGGL(k_merge<DSV_F32>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
     DSV_CHECK_LAUNCH("k_chunk / k_merge");
-    if (side && hipStreamWaitEvent(stream, side->join, 0) != hipSuccess)
-      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot join the side stream");
+    if (hist_possible) {  // nucleus rows whose chunk windows fall short of the row floor
+      const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
+      if (P.aligned) {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      } else {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      }
+      DSV_CHECK_LAUNCH("k_nuc");
+    }
   }
   if (stages & 2) {
     const dim3 grid(P.nch, a.bs);

@@ -191,9 +191,20 @@ def penalties_from_history(hist_ids, presence, repetition, vocab: int):
 # S1 / S2. Target distribution (runtime/worker.py:440-508, :52-67)
 # ---------------------------------------------------------------------------------------
 
-def softmax_temp(logits: torch.Tensor, temperatures_rows: torch.Tensor) -> torch.Tensor:
-    """sampling/sparse/target.py:133 (CPU branch): softmax(logits.float() / T) per row."""
-    return torch.softmax(logits.float() / temperatures_rows.float().view(-1, 1), dim=-1)
+def softmax_temp(logits: torch.Tensor, temperatures_rows: torch.Tensor, exact: bool = False) -> torch.Tensor:
+    """sampling/sparse/target.py:133 (CPU branch): softmax(logits.float() / T) per row.
+
+    ``exact``: the softmax of the same float32 values x / T evaluated in float64 and rounded
+    once to float32.  CPU torch's float32 softmax accumulates its normaliser in float32; on
+    flat rows of ~10^5 near-equal values that sum is off by up to ~1e-4 relative (every p
+    carries the error), which moves a top-p cut inside a large tie group by a few ties.  The
+    exact form is what such rows are pinned against."""
+    x = logits.float() / temperatures_rows.float().view(-1, 1)
+    if not exact:
+        return torch.softmax(x, dim=-1)
+    xd = x.double()
+    e = torch.exp(xd - xd.max(dim=-1, keepdim=True).values)
+    return (e / e.sum(dim=-1, keepdim=True)).float()
 
 
 def torch_backend_filtered_probs(probs, top_ks, top_ps, min_ps, need_min_p):
@@ -262,12 +273,12 @@ def filter_target_probs(probs, info, t, bs, sampling_backend, normalize=True):
     return probs.view(bs, t, -1)
 
 
-def build_target_probs(logits, info, block_size, bs, sampling_backend="pytorch"):
+def build_target_probs(logits, info, block_size, bs, sampling_backend="pytorch", exact_softmax=False):
     """runtime/worker.py:440-470: softmax(logits/T) per request, backend filter, then rows of
     greedy requests (top_k <= 1) become one-hot at argmax(logits) (first maximal id)."""
     t = int(block_size)
     temps = torch.repeat_interleave(info.temperatures.view(-1).float(), t)
-    probs = softmax_temp(logits, temps)
+    probs = softmax_temp(logits, temps, exact=exact_softmax)
     filtered = filter_target_probs(probs, info, t, bs, sampling_backend)
     if getattr(info, "is_any_greedy", False):
         flat = filtered.reshape(bs * t, -1)
@@ -578,7 +589,8 @@ def request_of_rows(bs, T, verify_lens=None, row_offsets=None, rows=None):
 
 def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, uniforms,
                 uniform_final, prefix_lens, hist_ids=None, presence=None, repetition=None,
-                page_table=None, row_offsets=None, sampling_backend="pytorch", requests=None):
+                page_table=None, row_offsets=None, sampling_backend="pytorch", requests=None,
+                exact_softmax=False):
     """The fused verify step on the CPU: history penalties -> target P per verified row ->
     sparse-q chain rejection -> compaction + KV slots.  ``logits`` is [rows, V] (bf16/fp32) in
     the dense ``b*T+s`` layout or ragged with ``row_offsets``.  ``requests`` (optional) limits
@@ -605,7 +617,8 @@ def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, unifo
         adjust_logits(x, SimpleNamespace(acc_additive_penalties=add, acc_scaling_penalties=scl),
                       owner_t)
     rinfo = row_info(info, owner_t)
-    P = build_target_probs(x, rinfo, 1, len(rows), sampling_backend).reshape(len(rows), V)
+    P = build_target_probs(x, rinfo, 1, len(rows), sampling_backend,
+                           exact_softmax=exact_softmax).reshape(len(rows), V)
     probs = {r: P[i].numpy() for i, r in enumerate(rows)}
     sub = np.asarray(reqs, dtype=np.int64)
     qi = None if q_ids is None else np.asarray(q_ids)[sub]

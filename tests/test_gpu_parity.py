@@ -71,7 +71,7 @@ def run_gpu_verify(batch, device, backend="pytorch", row_stride=None):
     return res
 
 
-def run_oracle(batch, requests, backend="pytorch"):
+def run_oracle(batch, requests, backend="pytorch", exact_softmax=False):
     O = _oracle()
     bs, T = batch["candidates"].shape
     lens = batch.get("verify_lens")
@@ -84,7 +84,7 @@ def run_oracle(batch, requests, backend="pytorch"):
         presence=batch.get("presence"), repetition=batch.get("repetition"),
         page_table=batch.get("page_table"),
         row_offsets=None if batch.get("row_offsets") is None else batch["row_offsets"].numpy(),
-        sampling_backend=backend, requests=requests)
+        sampling_backend=backend, requests=requests, exact_softmax=exact_softmax)
 
 
 # ------------------------------------------------------------------------------------------
@@ -303,6 +303,46 @@ def test_greedy_and_topk_row_layouts(device, V, stride):
     outs = accept_greedy(candidates=cand.to(device), next_token_logits=xd, prefix_lens=prefix.to(device), cap=T)
     for got, r in zip(outs, ref):
         assert np.array_equal(got.cpu().numpy(), r)
+
+
+@pytest.mark.parametrize("case", ["flat", "constant", "peaked", "wide_tail"])
+def test_verify_nucleus_paths(device, case):
+    # nucleus rows (top-k off, top-p < 1) that exercise each way the cut is found: "flat"
+    # (temperature 40: the counted windows cannot reach the row floor -> full histogram),
+    # "constant" (151936 equal values: more ties than a 16-bit counter holds), "peaked" (one
+    # dominant token: every counted value is kept and the cut is the first value below the
+    # windows), "wide_tail" (heavy-tailed logits, T = 1)
+    V = 151936
+    bs, T = 4, 3
+    batch = _small_batch(21, bs=bs, T=T, V=V, K=4, dtype=torch.bfloat16, mixed=False, penalties=True)
+    g = torch.Generator().manual_seed(22)
+    rows = bs * T
+    if case == "flat":
+        logits = torch.randn(rows, V, generator=g) * 2.0
+        temps = [40.0] * bs
+    elif case == "constant":
+        logits = torch.zeros(rows, V)
+        logits[:, ::7919] = 0.5
+        temps = [1.0] * bs
+    elif case == "peaked":
+        logits = torch.randn(rows, V, generator=g)
+        logits[torch.arange(rows), torch.randint(0, V, (rows,), generator=g)] = 30.0
+        temps = [1.0] * bs
+    else:
+        logits = 2.0 * torch.distributions.StudentT(3.0).sample((rows, V))
+        temps = [1.0] * bs
+    batch["logits"] = logits.to(torch.bfloat16)
+    batch["info"] = W.sampling_info(temps, [0] * bs, [0.9, 0.5, 0.95, 0.99][:bs])
+    base = batch["logits"].float()
+    for b in range(bs):  # a likely token as a q lane, so some drafts are accepted
+        for s_ in range(T - 1):
+            batch["q_ids"][b, s_, 0] = int(base[b * T + s_].argmax())
+    batch["q_ids"], _ = batch["q_ids"].sort(-1)
+    gpu = run_gpu_verify(batch, device)
+    # pinned against the exact softmax: CPU torch's float32 normaliser is off by ~1e-4 on the
+    # flat and constant rows, which moves their cut by a few of the ~10^5 ties
+    ref = run_oracle(batch, list(range(bs)), exact_softmax=True)
+    assert len(compare_outputs(gpu, ref, range(bs), f"nucleus {case}")) <= 1
 
 
 def test_verify_unfiltered(device):

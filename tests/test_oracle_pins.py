@@ -383,3 +383,20 @@ def test_sample_chain_brute_force_distribution():
         counts[int(tok[0]) - 10] += 1
         q_ref = q[0]
     np.testing.assert_allclose(counts / n, q_ref, atol=2.0 / n)
+
+
+def test_exact_softmax_is_rounded_float64():
+    # the exact form equals float64 softmax of the float32 values x / T, rounded once; on a
+    # flat row it sums to 1 within float32 rounding while torch's float32 softmax does not
+    x = torch.zeros(2, 151936)
+    x[:, ::7919] = 0.5
+    x[1] = torch.randn(151936, generator=torch.Generator().manual_seed(0)) * 3
+    T = torch.tensor([1.0, 0.7])
+    ex = O.softmax_temp(x, T, exact=True)
+    xd = (x / T.view(-1, 1)).double()
+    ref = torch.softmax(xd, -1).float()
+    assert torch.equal(ex, ref)
+    assert abs(ex[0].double().sum().item() - 1.0) < 1e-6
+    # closed form on the flat row: p(0) = 1 / (V - 20 + 20 e^0.5)
+    p0 = 1.0 / (151936 - 20 + 20 * np.exp(0.5))
+    assert abs(ex[0, 1].item() / p0 - 1) < 1e-7
