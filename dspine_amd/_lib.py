@@ -23,7 +23,7 @@ LIST_K = 64
 EXPORTS = (
     "dsv_last_error", "dsv_device_count", "dsv_verify_workspace_bytes", "dsv_verify",
     "dsv_greedy_verify", "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_topk_workspace_bytes",
-    "dsv_uniforms",
+    "dsv_uniforms", "dsv_profile_events",
 )
 
 _c = ctypes
@@ -89,6 +89,8 @@ def load():
         lib.dsv_topk.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, i32, vp, i64, vp]
         lib.dsv_uniforms.restype = i32
         lib.dsv_uniforms.argtypes = [vp, vp, i32, i64, i32, i32, vp, vp]
+        lib.dsv_profile_events.restype = i32
+        lib.dsv_profile_events.argtypes = [vp, vp]
         _lib = lib
     return _lib
 

@@ -1667,6 +1667,15 @@ extern "C" int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab) {
 }
 
 
+// Profiling aid: events recorded around the chunk-pass launch of this thread's next verify
+// calls (NULL, NULL: off).
+static thread_local hipEvent_t g_prof_start = nullptr, g_prof_stop = nullptr;
+extern "C" int dsv_profile_events(void* start, void* stop) {
+  g_prof_start = reinterpret_cast<hipEvent_t>(start);
+  g_prof_stop = reinterpret_cast<hipEvent_t>(stop);
+  return DSV_OK;
+}
+
 extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: null arguments");
@@ -1746,7 +1755,11 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
       hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
       DSV_CHECK_LAUNCH("k_prep");
     }
+    if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
+      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling start event");
     launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * C), stream);
+    if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_stop, stream) != hipSuccess)
+      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling stop event");
     if (a.logits_dtype == DSV_BF16)
       hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
     else

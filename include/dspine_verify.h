@@ -117,6 +117,11 @@ typedef struct dsv_verify_args {
 int64_t dsv_verify_workspace_bytes(int64_t rows, int32_t bs, int32_t T, int64_t vocab);
 int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream);
 
+/* Profiling aid with no counterpart in the reference: the calling thread's later dsv_verify   */
+/* calls record `start` / `stop` (hipEvent_t, timing enabled) on their stream right before and */
+/* after the chunk-pass kernel, so a benchmark can time that kernel alone.  NULL, NULL: off.   */
+int dsv_profile_events(void* start, void* stop);
+
 /* Greedy verify (argmax acceptance): top1 = first argmax of each row, a = first mismatch   */
 /* below verify_lens[b]-1 (or cap-1), bonus = top1[a]; output keeps proposals after a.      */
 /* Rows are b*T + s (the full-width envelope).  top1_out [rows] (int64) is optional.        */
