@@ -39,7 +39,7 @@ struct ChunkStat {
   int32_t arg;    // first id attaining it
   double s;       // sum exp((x - m) / T) over the chunk
   int32_t ncand;  // candidates written (LIST)
-  int32_t flags;
+  int32_t tieq;   // nucleus rows: values of the chunk with the draft token's key and a lower id
   uint32_t wlo;   // nucleus rows: lowest key of the chunk's value-count window (WIN_EMPTY: none)
   uint32_t kx;    // nucleus rows: largest key below the window (0: none)
 };

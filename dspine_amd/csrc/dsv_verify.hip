@@ -337,24 +337,6 @@ __device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int 
   }
 }
 
-// Values at key kv among ids [0, tok) of row r (penalised), summed over the workgroup.
-template <int DT, int NW>
-__device__ __forceinline__ int64_t ties_before(const KParams& P, int64_t r, int b, uint32_t kv, int64_t tok,
-                                               int32_t* red) {
-  const dsv_verify_args& a = P.a;
-  const char* rowp = row_ptr(a, r);
-  const bool pen = P.pbits != nullptr;
-  const float pres = pen && a.presence ? a.presence[b] : 0.f;
-  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
-  int32_t n = 0;
-  for (int64_t j = threadIdx.x; j < tok; j += blockDim.x) {
-    float x = load_elem<DT>(rowp, j);
-    if (pen && pen_test(P, b, j)) x = penalize<DT>(x, pres, rep);
-    n += key_of<DT>(x) == kv;
-  }
-  return block_sum<NW>(n, red);
-}
-
 template <int DT>
 __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh) {
   constexpr int NW = CT / WAVE;
@@ -562,10 +544,10 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   }
   rs.S_f = (float)rs.S_kept;
   const float xt = sh.xtok;
-  int64_t tie_tok = 0;
-  if (tok >= 0 && key_of<DT>(xt) == rs.vcut && rs.ktie > 0 && rs.ktie != INT_MAX)
-    tie_tok = ties_before<DT, NW>(P, r, b, rs.vcut, tok, sh.red_i);
-  if (tid < WAVE) nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok);
+  if (tid < WAVE) {
+    const int64_t tie_tok = wave_sum((int64_t)(lane < C ? cs[lane].tieq : 0));
+    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -852,7 +834,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
   __shared__ int32_t s_cnt;
-  __shared__ uint32_t s_wlo;
+  __shared__ uint32_t s_wlo, s_ktok;
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
@@ -959,7 +941,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   out.arg = cbest ? unpack_id(cbest) : INT_MAX;
   out.s = 0.0;
   out.ncand = 0;
-  out.flags = 0;
+  out.tieq = 0;
   out.wlo = WIN_EMPTY;
   out.kx = 0u;
 
@@ -982,7 +964,16 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       // counts of the values in the window [wlo, kmax] that can reach the nucleus cut: wlo is
       // the higher of kmax - (HWIN - 1) and the lowest key whose bound exp((x - m) / T) / s
       // reaches half of the row floor (1 - top_p - 1e-5) / V (the nucleus section above)
+      const int64_t tok = step_token(a, b, s);
       if (tid == 0) {
+        // the draft token's key: this chunk counts its ties ahead of it (ids below tok)
+        uint32_t ktok = 0xFFFFFFFFu;
+        if (tok >= 0 && tok < V && lo < tok) {
+          float xt = load_elem<DT>(rowp, tok);
+          if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
+          ktok = key_of<DT>(xt);
+        }
+        s_ktok = ktok;
         uint32_t wlo = WIN_EMPTY;
         if (cbest) {
           const uint32_t kmax = unpack_key(cbest);
@@ -1008,8 +999,9 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       }
       for (int i = tid; i < HWIN / 2; i += CT) hwin[i] = 0u;
       __syncthreads();
-      const uint32_t wlo = s_wlo;
+      const uint32_t wlo = s_wlo, ktok = s_ktok;
       uint32_t kx = 0u;
+      int32_t tq = 0;
       if (wlo != WIN_EMPTY) {
 #pragma unroll
         for (int u = 0; u < CV; ++u) {
@@ -1021,10 +1013,12 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
               atomicAdd(&hwin[(k - wlo) >> 1], 1u << (((k - wlo) & 1u) * 16u));
             else
               kx = k > kx ? k : kx;
+            if (k == ktok) tq += (v0 + (int64_t)u * CT + tid) * n + e < tok;
           }
         }
       }
       kx = (uint32_t)block_max_u64<CT / WAVE>((uint64_t)kx, su);  // (its barriers order the counts)
+      out.tieq = block_sum<CT / WAVE>(tq, reinterpret_cast<int32_t*>(sd));
       if (wlo != WIN_EMPTY) {
         const int nw = (int)((unpack_key(cbest) - wlo) >> 1) + 1;
         uint32_t* dst = P.hpart + (r * C + c) * (int64_t)(HWIN / 2);
