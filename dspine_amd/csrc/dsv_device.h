@@ -41,7 +41,7 @@ struct ChunkStat {
   int32_t ncand;  // candidates written (LIST)
   int32_t tieq;   // nucleus rows: values of the chunk with the draft token's key and a lower id
   uint32_t wlo;   // nucleus rows: lowest key of the chunk's value-count window (WIN_EMPTY: none)
-  uint32_t kx;    // nucleus rows: largest key below the window (0: none)
+  uint32_t kx;    // nucleus rows: largest key below the window (0: none; KX_UNKNOWN: not tracked)
 };
 static_assert(sizeof(ChunkStat) == 32, "ChunkStat layout");
 
@@ -60,6 +60,9 @@ constexpr int HIST_WORDS = 32768;    // 65536 16-bit counters
 constexpr int NUC_SLICE = 65528;     // values per 16-bit histogram pass (no counter can wrap)
 constexpr int HWIN = 4096;           // keys of a chunk's value-count window (nucleus rows)
 constexpr uint32_t WIN_EMPTY = 0x10000u;
+constexpr uint32_t KX_UNKNOWN = 0xFFFFFFFFu;  // ChunkStat::kx when the chunk did not track it
+constexpr int STAGE_MAX = 96;        // list rows: threads whose vectors fit the LDS stage
+constexpr int WHITV = 64;            // LDS slots of a wave for vectors holding history hits
 constexpr int NCH = 32;              // bonus-row chunks
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
@@ -206,6 +209,32 @@ __device__ __forceinline__ void reg_fence1(uint4& v) {
 // unpacking of the next vector from being scheduled ahead of the current one.
 __device__ __forceinline__ void reg_fence1(uint4& v, float& acc) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(acc));
+}
+__device__ __forceinline__ void reg_fence1(uint4& v, int& acc) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(acc));
+}
+// Orders `acc` after the vector without redefining the vector (for passes inside a branch,
+// where a redefinition would make the compiler copy every vector at the join).
+__device__ __forceinline__ void order_after(const uint4& v, int& acc) {
+  asm volatile("" : "+v"(acc) : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
+
+// Two 16-bit differences a - b, each wrapping modulo 2^16.
+__device__ __forceinline__ uint32_t sub_u16x2(uint32_t a, uint32_t b) {
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+
+// The J-th largest (1 <= J <= 64) of the wave's BITS-bit keys: a radix select on ballots.
+template <int BITS>
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t k, int J) {
+  uint32_t pre = 0u;
+#pragma unroll
+  for (int bit = BITS - 1; bit >= 0; --bit) {
+    const uint32_t cand = pre | (1u << bit);
+    if (__popcll(__ballot(k >= cand)) >= J) pre = cand;
+  }
+  return pre;
 }
 
 // Element e (a run-time index) of a vector, and its replacement: branch-free, through the two

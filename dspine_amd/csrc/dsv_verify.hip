@@ -104,17 +104,18 @@ __global__ __launch_bounds__(BCT) void k_prep(KParams P) {
 // Candidate refill: the chunk holds more values at or above the admission bound than the
 // LDS buffer.  The K-th largest buffered value is a higher bound; re-read the chunk from
 // memory until the admitted values fit.  Each raise drops at least CAND_CAP - K >= 256 of the
-// buffered values, so a chunk of at most 20480 values needs at most 80 rounds.
+// buffered values, so a chunk of at most 20480 values needs at most 80 rounds.  With thr0
+// nonzero the buffer holds nothing yet and the first read admits the values >= thr0.
 // ---------------------------------------------------------------------------------------
 template <int DT>
 __device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char* rowp, int64_t lo, int64_t hi,
                                               int K, float pres, float rep, uint64_t* cbuf, uint32_t* hist256,
-                                              uint64_t* su, int32_t* cnt) {
+                                              uint64_t* su, int32_t* cnt, uint64_t thr0) {
   constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
   int nb = CAND_CAP + 1;
   for (int iter = 0; iter < 128 && nb > CAND_CAP; ++iter) {
     if (threadIdx.x < WAVE) {
-      const uint64_t t = wave_kth_largest(cbuf, CAND_CAP, K, hist256, TOP_SHIFT);
+      const uint64_t t = (iter == 0 && thr0) ? thr0 : wave_kth_largest(cbuf, CAND_CAP, K, hist256, TOP_SHIFT);
       if (threadIdx.x == 0) {
         su[0] = t;
         *cnt = 0;
@@ -418,7 +419,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   rs.S_kept = 1.0;
   rs.S_f = 1.f;
   rs.p_draft = 0.f;
-  if (kmax < 0x80u || kcov > sh.kb_row) {  // a window stops above the floor: full histogram
+  if (kmax < 0x80u) {  // no finite value
     if (tid == 0) {
       rs.flags = FLAG_FULL_HIST;
       P.rowsum[r] = rs;
@@ -426,8 +427,9 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     }
     return;
   }
-  // The cut is at or above the first value below the floor kb: only keys >= kb are scanned
-  // (the first value below kb, if the scan keeps every value, is found separately).
+  // Every chunk counted each key >= kcov, so a cut found at or above kcov is exact.  The cut
+  // is also at or above the first value below the floor kb: only keys >= max(kb, kcov) are
+  // scanned (the first value below kb, if the scan keeps every value, is found separately).
   const uint32_t kscan = sh.kb_row > kcov ? sh.kb_row : kcov;
   const int W = (int)(kmax - kscan) + 1;  // <= HWIN: the max's own chunk window ends at kmax
   for (int q = tid; q < W; q += CT) {
@@ -519,6 +521,17 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     fc = sh.cut[i];
     fS = sh.cutS[i];
   }
+  const bool x_untracked = __ballot(lane < C && x_l == KX_UNKNOWN) != 0ull;
+  if (fc == ~0ull && (kcov > sh.kb_row || x_untracked)) {
+    // the cut lies below a chunk's window (or below every window, where a chunk did not
+    // track its largest value): the full histogram decides it
+    if (tid == 0) {
+      rs.flags = FLAG_FULL_HIST;
+      P.rowsum[r] = rs;
+      P.step_ok[r] = 0;
+    }
+    return;
+  }
   if (fc != ~0ull) {
     rs.vcut = (uint32_t)fc;
     rs.ktie = (int32_t)(fc >> 32);
@@ -545,7 +558,25 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   rs.S_f = (float)rs.S_kept;
   const float xt = sh.xtok;
   if (tid < WAVE) {
-    const int64_t tie_tok = wave_sum((int64_t)(lane < C ? cs[lane].tieq : 0));
+    // values of the draft token's key ahead of it: the whole counts of the chunks before its
+    // chunk (the key is in every window when it is the cut key) and its chunk's own count
+    int64_t tie_tok = 0;
+    const uint32_t kt = key_of<DT>(xt);
+    if (tok >= 0 && kt == rs.vcut && rs.ktie > 0 && rs.ktie != INT_MAX && lane < C) {
+      constexpr int64_t CHE = Elems<DT>::chunk;
+      const int64_t c_lo = (int64_t)lane * CHE, c_hi = c_lo + CHE;
+      if (c_hi <= tok) {
+        const uint32_t wl = sh.cw[lane];
+        if (wl != WIN_EMPTY && kt >= wl && kt <= sh.ck[lane]) {
+          const uint32_t o = kt - wl;
+          const uint32_t word = P.hpart[(r * C + lane) * (int64_t)(HWIN / 2) + (o >> 1)];
+          tie_tok = (word >> ((o & 1u) * 16u)) & 0xFFFFu;
+        }
+      } else if (c_lo <= tok) {
+        tie_tok = cs[lane].tieq;
+      }
+    }
+    tie_tok = wave_sum(tie_tok);
     nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok);
   }
 }
@@ -830,10 +861,15 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   constexpr int CHE = Elems<DT>::chunk;
   __shared__ uint64_t cbuf[CAND_CAP];
   __shared__ uint32_t hist256[256];
-  __shared__ uint32_t hwin[HWIN / 2];
+  // nucleus rows: 32-bit value counts of the window; list rows: staged vectors
+  __shared__ uint4 big[HWIN / 4];
+  static_assert(STAGE_MAX * CV <= HWIN / 4, "list stage exceeds the window buffer");
+  __shared__ int16_t s_qtid[STAGE_MAX];
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
-  __shared__ int32_t s_cnt;
+  __shared__ uint4 s_hv[CT / WAVE * WHITV];  // history-hit vectors of each wave
+  __shared__ uint32_t s_hm[CT / WAVE * WHITV];
+  __shared__ int32_t s_cnt, s_nq;
   __shared__ uint32_t s_wlo, s_ktok;
   const dsv_verify_args& a = P.a;
   const int C = P.C;
@@ -888,6 +924,9 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   const bool pen = P.softmax && P.pbits != nullptr;
   float pres = 0.f, rep = 1.f;
   if (pen) {
+    // History hits (about 0.3% of the values).  Each lane copies its vectors that hold hits to
+    // LDS, one lane per copied vector penalises the hit elements there, and the owners read
+    // the vectors back: the registers end up penalised without a run-time register index.
     pres = a.presence ? a.presence[b] : 0.f;
     rep = a.repetition ? a.repetition[b] : 1.f;
     uint32_t bits[CV];
@@ -897,14 +936,63 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       const uint32_t w = pen_bits(P, b, j < hi ? j : lo, n);
       bits[u] = j < hi ? w : 0u;
     }
-    // history tokens are rare: visit only the set bits (about 0.3% of the values)
+    int hv = 0;
+#pragma unroll
+    for (int u = 0; u < CV; ++u) hv += bits[u] != 0u;
+    int pre = 0, tot = 0;  // exclusive prefix and total of the hit vectors over the wave
+    for (int k = 1;; ++k) {
+      const uint64_t bal = __ballot(hv >= k);
+      if (!bal) break;
+      pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      tot += __popcll(bal);
+    }
+    uint4* wv = s_hv + wid * WHITV;
+    uint32_t* wm = s_hm + wid * WHITV;
+    int slot = pre;
 #pragma unroll
     for (int u = 0; u < CV; ++u) {
-      uint32_t bu = bits[u];
-      while (bu) {
-        const int e = __ffs(bu) - 1;
-        bu &= bu - 1u;
-        vec_set_dyn<DT>(v[u], e, penalize<DT>(vec_elem_dyn<DT>(v[u], e), pres, rep));
+      if (bits[u]) {
+        if (slot < WHITV) {
+          wv[slot] = v[u];
+          wm[slot] = bits[u];
+        } else {  // beyond the wave's LDS slots: in place
+          uint32_t bu = bits[u];
+          while (bu) {
+            const int e = __ffs(bu) - 1;
+            bu &= bu - 1u;
+            vec_set_dyn<DT>(v[u], e, penalize<DT>(vec_elem_dyn<DT>(v[u], e), pres, rep));
+          }
+        }
+        ++slot;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nv = tot < WHITV ? tot : WHITV;
+    for (int i = lane; i < nv; i += WAVE) {
+      uint32_t m = wm[i];
+      while (m) {
+        const int e = __ffs(m) - 1;
+        m &= m - 1u;
+        if constexpr (DT == DSV_BF16) {
+          uint16_t* el = reinterpret_cast<uint16_t*>(&wv[i]) + e;
+          *el = (uint16_t)(__float_as_uint(penalize<DT>(bf16_bits_to_f32(*el), pres, rep)) >> 16);
+        } else {
+          float* el = reinterpret_cast<float*>(&wv[i]) + e;
+          *el = penalize<DT>(*el, pres, rep);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    slot = pre;
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      if (bits[u]) {
+        if (slot < WHITV) v[u] = wv[slot];
+        ++slot;
       }
     }
   }
@@ -959,16 +1047,19 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     reg_fence(v);
   }
 
-  if constexpr (DT == DSV_BF16) {
-    if (mode == M_HIST) {
-      // counts of the values in the window [wlo, kmax] that can reach the nucleus cut: wlo is
-      // the higher of kmax - (HWIN - 1) and the lowest key whose bound exp((x - m) / T) / s
-      // reaches half of the row floor (1 - top_p - 1e-5) / V (the nucleus section above)
+  if (DT == DSV_BF16 && mode == M_HIST) {
+    if constexpr (DT == DSV_BF16) {
+      // counts of the values in the window [wlo, kmax] where the row's cut is expected: wlo is
+      // the higher of kmax - (HWIN - 1) and the lowest key whose probability estimate
+      // exp((x - m) / T) / (s * C) (this chunk's sum standing for each of the row's C chunks)
+      // reaches 2 (1 - top_p) / V.  The row merge takes the cut from the counts when it lies
+      // in every chunk's window, and the full-histogram path otherwise.
       const int64_t tok = step_token(a, b, s);
+      const bool tok_here = tok >= lo && tok < hi;
+      uint32_t* cnt = reinterpret_cast<uint32_t*>(big);
       if (tid == 0) {
-        // the draft token's key: this chunk counts its ties ahead of it (ids below tok)
-        uint32_t ktok = 0xFFFFFFFFu;
-        if (tok >= 0 && tok < V && lo < tok) {
+        uint32_t ktok = 0xFFFFFFFFu;  // the draft token's key, in the chunk that holds it
+        if (tok_here) {
           float xt = load_elem<DT>(rowp, tok);
           if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
           ktok = key_of<DT>(xt);
@@ -978,14 +1069,13 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
         if (cbest) {
           const uint32_t kmax = unpack_key(cbest);
           uint32_t kb = 0x80u;  // the lowest finite key
-          const float eps = (0.99998f - a.top_ps[b]) / (float)V * 0.5f;
-          if (eps > 0.f && kmax > 0x80u) {
+          const float floor_e = 2.f * (1.f - a.top_ps[b]) / (float)V * (float)(out.s * (double)C);
+          if (floor_e > 0.f && kmax > 0x80u) {
             const float c2 = log2e_over(T);
-            const float inv_s = (float)(1.0 / out.s);
             uint32_t l0 = 0x80u, l1 = kmax;
             while (l0 < l1) {
               const uint32_t mid = (l0 + l1) >> 1;
-              if (__builtin_amdgcn_exp2f((value_of_key<DT>(mid) - out.m) * c2) * inv_s >= eps)
+              if (__builtin_amdgcn_exp2f((value_of_key<DT>(mid) - out.m) * c2) >= floor_e)
                 l1 = mid;
               else
                 l0 = mid + 1;
@@ -997,89 +1087,148 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
         }
         s_wlo = wlo;
       }
-      for (int i = tid; i < HWIN / 2; i += CT) hwin[i] = 0u;
+#pragma unroll
+      for (int i = tid; i < HWIN / 4; i += CT) big[i] = make_uint4(0u, 0u, 0u, 0u);
       __syncthreads();
-      const uint32_t wlo = s_wlo, ktok = s_ktok;
-      uint32_t kx = 0u;
-      int32_t tq = 0;
-      if (wlo != WIN_EMPTY) {
+      const uint32_t wlo = s_wlo;
+      int tq = 0;
+      if (tok_here) {  // values equal to the draft token's ahead of it
+        const uint32_t ktok = s_ktok;
+        const float xtv = value_of_key<DT>(ktok);
+        // element e of vector u is ahead of tok iff u * CT * n + e < rel
+        const int64_t rel64 = tok - (v0 + tid) * n;
+        const int rel = (int)(rel64 < 0 ? 0 : (rel64 > CV * CT * n ? CV * CT * n : rel64));
 #pragma unroll
         for (int u = 0; u < CV; ++u) {
-          reg_fence1(v[u]);
+          order_after(v[u], tq);
 #pragma unroll
-          for (int e = 0; e < n; ++e) {
-            const uint32_t k = key_of<DT>(vec_elem<DT>(v[u], e));
-            if (k >= wlo)
-              atomicAdd(&hwin[(k - wlo) >> 1], 1u << (((k - wlo) & 1u) * 16u));
-            else
-              kx = k > kx ? k : kx;
-            if (k == ktok) tq += (v0 + (int64_t)u * CT + tid) * n + e < tok;
+          for (int e = 0; e < n; ++e) tq += (vec_elem<DT>(v[u], e) == xtv) & (u * CT * n + e < rel);
+        }
+      }
+      uint32_t kx = 0u;
+      if (wlo != WIN_EMPTY) {
+        const uint32_t W = unpack_key(cbest) - wlo + 1u;
+        if (wlo > 0x8000u) {
+          // a window of positive values: position = raw bits - (wlo - 0x8000); zero, negative
+          // and lower values fall outside.  The largest value below the window is not
+          // tracked here (the merge takes the full-histogram path if it needs it).
+          const uint32_t cb = wlo - 0x8000u;
+          const uint32_t cb2 = cb | (cb << 16);
+#pragma unroll
+          for (int u = 0; u < CV; ++u) {
+            reg_fence1(v[u]);
+            const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t o2 = sub_u16x2(w4[q], cb2);
+              const uint32_t o0 = o2 & 0xffffu, o1 = o2 >> 16;
+              if (o0 < W) atomicAdd(&cnt[o0], 1u);
+              if (o1 < W) atomicAdd(&cnt[o1], 1u);
+            }
+          }
+          kx = KX_UNKNOWN;
+        } else {
+#pragma unroll
+          for (int u = 0; u < CV; ++u) {
+            reg_fence1(v[u]);
+#pragma unroll
+            for (int e = 0; e < n; ++e) {
+              const uint32_t k = key_of<DT>(vec_elem<DT>(v[u], e));
+              const uint32_t o = k - wlo;
+              if (o < W)
+                atomicAdd(&cnt[o], 1u);
+              else
+                kx = k > kx ? k : kx;
+            }
           }
         }
       }
       kx = (uint32_t)block_max_u64<CT / WAVE>((uint64_t)kx, su);  // (its barriers order the counts)
-      out.tieq = block_sum<CT / WAVE>(tq, reinterpret_cast<int32_t*>(sd));
+      out.tieq = tok_here ? block_sum<CT / WAVE>(tq, reinterpret_cast<int*>(sd)) : 0;
       if (wlo != WIN_EMPTY) {
+        // 16-bit counts (a chunk holds fewer than 65536 values), two keys a word
         const int nw = (int)((unpack_key(cbest) - wlo) >> 1) + 1;
         uint32_t* dst = P.hpart + (r * C + c) * (int64_t)(HWIN / 2);
-        for (int i = tid; i < nw; i += CT) dst[i] = hwin[i];
+        for (int i = tid; i < nw; i += CT) dst[i] = cnt[2 * i] | (cnt[2 * i + 1] << 16);
       }
       out.wlo = wlo;
       out.kx = kx;
     }
-  }
-
-  if (mode == M_LIST) {
+  } else if (mode == M_LIST) {
     int K = P.softmax ? a.top_ks[b] : P.kcand;
     K = K < 1 ? 1 : (K > P.kcand ? P.kcand : K);
-    // admission bound: min over the 4 waves of each wave's ceil(K/4)-th largest thread max,
+    // admission bound: min over the 4 waves of each wave's ceil(K/4)-th largest thread-max key,
     // so that at least K values of the chunk are at or above it
     const int J = (K + (CT / WAVE) - 1) / (CT / WAVE);
-    uint64_t tm = mine, w = 0ull;
-    for (int i = 0; i < J; ++i) {
-      w = wave_max_u64(tm);
-      if (tm == w) tm = 0ull;
+    const uint32_t kt = key_of<DT>(m_t);
+    const uint32_t wk = wave_kth_key<DT == DSV_BF16 ? 16 : 32>(kt, J);
+    __syncthreads();
+    if (lane == 0) su[wid] = wk;
+    if (tid == 0) {
+      s_cnt = 0;
+      s_nq = 0;
     }
     __syncthreads();
-    if (lane == 0) su[wid] = w;
-    if (tid == 0) s_cnt = 0;
-    __syncthreads();
-    uint64_t thr = ~0ull;
-    for (int i = 0; i < CT / WAVE; ++i) thr = su[i] < thr ? su[i] : thr;
-    if (thr == 0ull) thr = 1ull;
-    // values below thr_x cannot pass, nor can any value of a thread whose max is below it
-    const float thr_x = unpack_key(thr) ? value_of_key<DT>(unpack_key(thr)) : -INFINITY;
-    if (m_t >= thr_x) {
+    uint32_t thr = 0xFFFFFFFFu;
 #pragma unroll
-      for (int u = 0; u < CV; ++u) {
-        reg_fence1(v[u]);
+    for (int i = 0; i < CT / WAVE; ++i) thr = (uint32_t)su[i] < thr ? (uint32_t)su[i] : thr;
+    // only the threads whose max reaches the bound hold admitted values: they stage their
+    // vectors in LDS and the whole workgroup scans them
+    uint4* stage = reinterpret_cast<uint4*>(big);
+    if (kt >= thr) {
+      const int slot = atomicAdd(&s_nq, 1);
+      if (slot < STAGE_MAX) {
+        s_qtid[slot] = (int16_t)tid;
+#pragma unroll
+        for (int u = 0; u < CV; ++u) stage[slot * CV + u] = v[u];
+      }
+    }
+    __syncthreads();
+    const int nq = s_nq;
+    if (nq <= STAGE_MAX) {
+      for (int vi = tid; vi < nq * CV; vi += CT) {
+        const int slot = vi / CV, u = vi - slot * CV;
+        const uint4 w = stage[vi];
+        const int64_t j0 = (v0 + (int64_t)u * CT + s_qtid[slot]) * n;
 #pragma unroll
         for (int e = 0; e < n; ++e) {
-          const float x = vec_elem<DT>(v[u], e);
-          if (x >= thr_x) {
-            const int64_t j = (v0 + (int64_t)u * CT + tid) * n + e;
-            const uint64_t pk = pack(key_of<DT>(x), j);
-            if (j < hi && pk >= thr) {
-              const int slot = atomicAdd(&s_cnt, 1);
-              if (slot < CAND_CAP) cbuf[slot] = pk;
-            }
+          const uint32_t k = key_of<DT>(vec_elem<DT>(w, e));
+          if (k >= thr && j0 + e < hi) {
+            const int at = atomicAdd(&s_cnt, 1);
+            if (at < CAND_CAP) cbuf[at] = pack(k, j0 + e);
           }
         }
       }
     }
     __syncthreads();
     int nb = s_cnt;
-    if (nb > CAND_CAP)
+    if (nq > STAGE_MAX || nb > CAND_CAP) {
+      // too many threads to stage, or too many admitted values: re-read the chunk
       nb = refill_candidates<DT>(pen ? P.pbits + (int64_t)b * P.pwords : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
-                                 hist256, su, &s_cnt);
+                                 hist256, su, &s_cnt, nq > STAGE_MAX ? ((uint64_t)thr << 32) | 1ull : 0ull);
+    }
     // rank of each admitted value among them (values are distinct): the top K, in order
     const int kk = K < nb ? K : nb;
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;
-    for (int i = tid; i < nb; i += CT) {
-      const uint64_t v_i = cbuf[i];
-      int rank = 0;
-      for (int j = 0; j < nb; ++j) rank += cbuf[j] > v_i;
-      if (rank < kk) dst[rank] = v_i;
+    if (nb <= WAVE) {
+      if (wid == 0) {  // one value a lane, ranked against the others read from the lanes
+        const uint64_t v_i = lane < nb ? cbuf[lane] : 0ull;
+        const int hi_i = (int)(v_i >> 32), lo_i = (int)(uint32_t)v_i;
+        int rank = 0;
+        for (int j = 0; j < nb; ++j) {
+          const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi_i, j) << 32) |
+                             (uint32_t)__builtin_amdgcn_readlane(lo_i, j);
+          rank += o > v_i;
+        }
+        if (lane < nb && rank < kk) dst[rank] = v_i;
+      }
+    } else {
+      for (int i = tid; i < nb; i += CT) {
+        const uint64_t v_i = cbuf[i];
+        int rank = 0;
+        for (int j = 0; j < nb; ++j) rank += cbuf[j] > v_i;
+        if (rank < kk) dst[rank] = v_i;
+      }
     }
     out.ncand = kk;
   }
