@@ -264,6 +264,20 @@ __device__ __forceinline__ void vec_set_dyn(uint4& v, int e, float x) {
 }
 
 // Vector vi of a 16-byte-aligned row, no bounds check (the caller knows it is inside).
+// A raw buffer over [base, base + bytes): loads past the end return zeros, and each load takes
+// a 32-bit lane offset plus a scalar offset (no 64-bit address arithmetic per load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes at lane offset voff + scalar offset soff, streamed (non-temporal).
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  const auto t = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (int)soff, 2);
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0);
+}
+
 __device__ __forceinline__ uint4 load_vec_raw(const char* rowp, int64_t vi) {
   const v4u_t t = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(rowp) + vi);
   return make_uint4(t.x, t.y, t.z, t.w);

@@ -886,11 +886,10 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   uint4 v[CV];
   const int64_t nfull = hi / n;  // vectors wholly inside the row end before this one
   if constexpr (ALIGNED) {
+    // vectors past the row's end read as zeros here and are filled below
+    const auto rs = buf_rsrc(rowp + lo * (16 / n), (uint32_t)((hi - lo) * (16 / n)));
 #pragma unroll
-    for (int u = 0; u < CV; ++u) {
-      const int64_t vi = v0 + (int64_t)u * CT + tid;
-      v[u] = load_vec_raw(rowp, vi < nfull ? vi : nfull - 1);
-    }
+    for (int u = 0; u < CV; ++u) v[u] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)(u * CT * 16));
   } else {
 #pragma unroll
     for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, false);
@@ -907,7 +906,24 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       mode = M_LIST;  // top-k rows
     }
   }
-  const float T = P.softmax && mode != M_GREEDY ? a.temperatures[b] : 1.f;
+  // The row's parameters, loaded while the chunk's vector loads are in flight: the fence keeps
+  // the compiler from sinking them into the mode sections, where each would be a dependent
+  // load of its own behind the chunk's work.
+  const bool pen = P.softmax && P.pbits != nullptr;
+  float T = 1.f, top_p = 1.f, pres = 0.f, rep = 1.f;
+  int topk = P.kcand;
+  int64_t tok = -1;
+  if (P.softmax && !P.force_greedy) {
+    if (mode != M_GREEDY) T = a.temperatures[b];
+    topk = a.top_ks[b];
+    if (a.filter) top_p = a.top_ps[b];
+    if (pen) {
+      pres = a.presence ? a.presence[b] : 0.f;
+      rep = a.repetition ? a.repetition[b] : 1.f;
+    }
+    if (mode == M_HIST) tok = step_token(a, b, s);
+  }
+  asm volatile("" ::"s"(T), "s"(top_p), "s"(pres), "s"(rep), "s"(topk), "s"(tok));
   ChunkStat* st = P.cstat + r * C + c;
   if (ALIGNED && hi - lo < CHE) {
     // the row's last chunk: -inf past the row, and the partial last vector element by element
@@ -921,20 +937,20 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
   }
 
-  const bool pen = P.softmax && P.pbits != nullptr;
-  float pres = 0.f, rep = 1.f;
   if (pen) {
     // History hits (about 0.3% of the values).  Each lane copies its vectors that hold hits to
     // LDS, one lane per copied vector penalises the hit elements there, and the owners read
     // the vectors back: the registers end up penalised without a run-time register index.
-    pres = a.presence ? a.presence[b] : 0.f;
-    rep = a.repetition ? a.repetition[b] : 1.f;
+    // the n bits of vector u: word (lo + (u CT + tid) n) / 32 of the request's bitmap (lo is a
+    // multiple of 32); tokens >= vocab have no bit set, and words past the bitmap read as zeros
     uint32_t bits[CV];
+    {
+      const int64_t w0 = lo >> 5;
+      const auto rb = buf_rsrc(P.pbits + (int64_t)b * P.pwords + w0, (uint32_t)((P.pwords - w0) * 4));
+      const uint32_t voff = (uint32_t)((tid * n) >> 5) * 4u, sh = (uint32_t)(tid * n) & 31u;
 #pragma unroll
-    for (int u = 0; u < CV; ++u) {
-      const int64_t j = (v0 + (int64_t)u * CT + tid) * n;
-      const uint32_t w = pen_bits(P, b, j < hi ? j : lo, n);
-      bits[u] = j < hi ? w : 0u;
+      for (int u = 0; u < CV; ++u)
+        bits[u] = (buf_load4(rb, voff, (uint32_t)(u * CT * n / 8)) >> sh) & ((1u << n) - 1u);
     }
     int hv = 0;
 #pragma unroll
@@ -1054,22 +1070,26 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       // exp((x - m) / T) / (s * C) (this chunk's sum standing for each of the row's C chunks)
       // reaches 2 (1 - top_p) / V.  The row merge takes the cut from the counts when it lies
       // in every chunk's window, and the full-histogram path otherwise.
-      const int64_t tok = step_token(a, b, s);
       const bool tok_here = tok >= lo && tok < hi;
       uint32_t* cnt = reinterpret_cast<uint32_t*>(big);
-      if (tid == 0) {
-        uint32_t ktok = 0xFFFFFFFFu;  // the draft token's key, in the chunk that holds it
-        if (tok_here) {
-          float xt = load_elem<DT>(rowp, tok);
-          if (pen && pen_test(P, b, tok)) xt = penalize<DT>(xt, pres, rep);
-          ktok = key_of<DT>(xt);
+      if (tok_here) {
+        // the draft token's (penalised) value, from the registers of the thread that holds it
+        const int rel = (int)(tok - lo);
+        const int vi = rel / n, uu = vi / CT;
+        if (tid == vi - uu * CT) {
+          uint4 w = v[0];
+#pragma unroll
+          for (int u = 1; u < CV; ++u)
+            if (u == uu) w = v[u];
+          s_ktok = key_of<DT>(vec_elem_dyn<DT>(w, rel - vi * n));
         }
-        s_ktok = ktok;
+      }
+      if (tid == 0) {
         uint32_t wlo = WIN_EMPTY;
         if (cbest) {
           const uint32_t kmax = unpack_key(cbest);
           uint32_t kb = 0x80u;  // the lowest finite key
-          const float floor_e = 2.f * (1.f - a.top_ps[b]) / (float)V * (float)(out.s * (double)C);
+          const float floor_e = 2.f * (1.f - top_p) / (float)V * (float)(out.s * (double)C);
           if (floor_e > 0.f && kmax > 0x80u) {
             const float c2 = log2e_over(T);
             uint32_t l0 = 0x80u, l1 = kmax;
@@ -1155,14 +1175,14 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       out.kx = kx;
     }
   } else if (mode == M_LIST) {
-    int K = P.softmax ? a.top_ks[b] : P.kcand;
+    int K = topk;
     K = K < 1 ? 1 : (K > P.kcand ? P.kcand : K);
     // admission bound: min over the 4 waves of each wave's ceil(K/4)-th largest thread-max key,
     // so that at least K values of the chunk are at or above it
     const int J = (K + (CT / WAVE) - 1) / (CT / WAVE);
     const uint32_t kt = key_of<DT>(m_t);
     const uint32_t wk = wave_kth_key<DT == DSV_BF16 ? 16 : 32>(kt, J);
-    __syncthreads();
+    if (!P.softmax) __syncthreads();  // (softmax rows: the sum's barriers follow the last use of su)
     if (lane == 0) su[wid] = wk;
     if (tid == 0) {
       s_cnt = 0;
@@ -1186,43 +1206,76 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     __syncthreads();
     const int nq = s_nq;
     if (nq <= STAGE_MAX) {
-      for (int vi = tid; vi < nq * CV; vi += CT) {
-        const int slot = vi / CV, u = vi - slot * CV;
-        const uint4 w = stage[vi];
-        const int64_t j0 = (v0 + (int64_t)u * CT + s_qtid[slot]) * n;
+      for (int vb = 0; vb < nq * CV; vb += CT) {
+        const int vi = vb + tid;
+        uint4 w = make_uint4(0u, 0u, 0u, 0u);
+        int64_t j0 = hi;
+        if (vi < nq * CV) {
+          const int slot = vi / CV, u = vi - slot * CV;
+          w = stage[vi];
+          j0 = (v0 + (int64_t)u * CT + s_qtid[slot]) * n;
+        }
+        uint32_t am = 0u;  // the vector's admitted elements
 #pragma unroll
-        for (int e = 0; e < n; ++e) {
-          const uint32_t k = key_of<DT>(vec_elem<DT>(w, e));
-          if (k >= thr && j0 + e < hi) {
-            const int at = atomicAdd(&s_cnt, 1);
-            if (at < CAND_CAP) cbuf[at] = pack(k, j0 + e);
+        for (int e = 0; e < n; ++e)
+          am |= (uint32_t)(key_of<DT>(vec_elem<DT>(w, e)) >= thr && j0 + e < hi) << e;
+        // slots: a prefix over the wave and one LDS atomic a wave
+        const int na = __popc(am);
+        int pre = 0, tot = 0;
+        for (int k = 1;; ++k) {
+          const uint64_t bal = __ballot(na >= k);
+          if (!bal) break;
+          pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          tot += __popcll(bal);
+        }
+        if (tot) {
+          int base = 0;
+          if (lane == 0) base = atomicAdd(&s_cnt, tot);
+          int at = __shfl(base, 0, WAVE) + pre;
+#pragma unroll
+          for (int e = 0; e < n; ++e) {
+            if ((am >> e) & 1u) {
+              if (at < CAND_CAP) cbuf[at] = pack(key_of<DT>(vec_elem<DT>(w, e)), j0 + e);
+              ++at;
+            }
           }
         }
       }
     }
     __syncthreads();
-    int nb = s_cnt;
+    int nb = __builtin_amdgcn_readfirstlane(s_cnt);
     if (nq > STAGE_MAX || nb > CAND_CAP) {
       // too many threads to stage, or too many admitted values: re-read the chunk
       nb = refill_candidates<DT>(pen ? P.pbits + (int64_t)b * P.pwords : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
                                  hist256, su, &s_cnt, nq > STAGE_MAX ? ((uint64_t)thr << 32) | 1ull : 0ull);
     }
-    // rank of each admitted value among them (values are distinct): the top K, in order
     const int kk = K < nb ? K : nb;
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;
     if (nb <= WAVE) {
-      if (wid == 0) {  // one value a lane, ranked against the others read from the lanes
+      if (wid == 0) {
+        // the K largest of the admitted values, unordered (the row merge ranks them): one a
+        // lane, the K-th largest key by a radix select, then the lowest ids of its ties
         const uint64_t v_i = lane < nb ? cbuf[lane] : 0ull;
-        const int hi_i = (int)(v_i >> 32), lo_i = (int)(uint32_t)v_i;
-        int rank = 0;
-        for (int j = 0; j < nb; ++j) {
-          const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi_i, j) << 32) |
-                             (uint32_t)__builtin_amdgcn_readlane(lo_i, j);
-          rank += o > v_i;
+        bool take = lane < nb;
+        if (nb > K) {
+          const uint32_t key_i = lane < nb ? unpack_key(v_i) : 0u;
+          const uint32_t kth = wave_kth_key<DT == DSV_BF16 ? 16 : 32>(key_i, K);
+          const int need = K - __popcll(__ballot(lane < nb && key_i > kth));
+          const uint64_t ties = __ballot(lane < nb && key_i == kth);
+          int ahead = 0;  // ties with a lower id (a larger packed value)
+          for (uint64_t m = ties; m; m &= m - 1ull) {
+            const int j = __ffsll((long long)m) - 1;
+            const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v_i >> 32), j) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v_i, j);
+            ahead += o > v_i;
+          }
+          take = key_i > kth || (key_i == kth && lane < nb && ahead < need);
         }
-        if (lane < nb && rank < kk) dst[rank] = v_i;
+        const uint64_t tb = __ballot(take);
+        if (take)
+          dst[__builtin_amdgcn_mbcnt_hi((uint32_t)(tb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)tb, 0u))] = v_i;
       }
-    } else {
+    } else {  // more than a wave of values: each ranked against all (values are distinct)
       for (int i = tid; i < nb; i += CT) {
         const uint64_t v_i = cbuf[i];
         int rank = 0;
