@@ -42,14 +42,11 @@ struct ChunkStat {
   int32_t tieq;   // nucleus rows: values of the chunk with the draft token's key and a lower id
   uint32_t wlo;   // nucleus rows: lowest key of the chunk's value-count window (WIN_EMPTY: none)
   uint32_t kx;    // nucleus rows: largest key below the window (0: none; KX_UNKNOWN: not tracked)
-};
-static_assert(sizeof(ChunkStat) == 32, "ChunkStat layout");
-
-struct BonusChunk {
-  double mass;   // mass of kept ids (key > vcut for HIST, every id for UNF)
-  int32_t ties;  // ids with key == vcut (HIST)
+  float xtok;     // softmax rows: the draft token's adjusted value, in the chunk that holds it
   int32_t pad;
 };
+static_assert(sizeof(ChunkStat) == 40, "ChunkStat layout");
+
 
 constexpr int CT = 256;              // threads of a chunk workgroup
 constexpr int CV = 10;               // 16-byte vectors per thread per chunk
@@ -63,7 +60,7 @@ constexpr uint32_t WIN_EMPTY = 0x10000u;
 constexpr uint32_t KX_UNKNOWN = 0xFFFFFFFFu;  // ChunkStat::kx when the chunk did not track it
 constexpr int STAGE_MAX = 96;        // list rows: threads whose vectors fit the LDS stage
 constexpr int WHITV = 64;            // LDS slots of a wave for vectors holding history hits
-constexpr int NCH = 32;              // bonus-row chunks
+constexpr int NCHK = 16;             // most chunks a row may have (per-row chunk arrays)
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
 constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram
@@ -349,6 +346,13 @@ __device__ __forceinline__ float log2e_over(float T) { return 1.4426950408889634
 __device__ __forceinline__ float prob_of(float x, float T, float m_f, float invZ) {
   const float xf = x / T;
   return expf(xf - m_f) * invZ;
+}
+
+// P at one value of a dense row (unfiltered, or a nucleus row's kept value): p, renormalised
+// over the kept mass when the row is filtered.
+__device__ __forceinline__ double dense_P(const RowSum& rs, float T, float x) {
+  const float p = prob_of(x, T, rs.m_f, rs.invZ);
+  return (rs.mode == M_HIST || rs.norm) ? (double)(p / rs.S_f) : (double)p;
 }
 
 // ---------------------------------------------------------------------------------------

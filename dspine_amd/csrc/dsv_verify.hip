@@ -9,14 +9,14 @@
 //   k_merge  (rows)             per row: Z, the filtered top-k support (id, P), P at the draft
 //                               token and the step's accept/reject decision; nucleus rows (a
 //                               top-p / min-p cut with top-k > 64) find their cut from the chunk
-//                               pass's value counts
+//                               pass's value counts.  Then the bonus draw the row would give as
+//                               the accepted length: drawn for support-list rows, planned (the
+//                               chunk and threshold) for dense rows
 //   k_nuc    (<= 64 workgroups) nucleus rows those counts do not settle: the full 65536-key
 //                               value histogram of the row
-//   k_bonus  (chunks x requests) a dense bonus row (unfiltered / nucleus) summed per thread in one
-//                               vector pass
-//   k_final  (requests)         accepted length from the row decisions, the bonus draw (support
-//                               list, or the dense row's chunk -> thread -> element), outputs and
-//                               KV slots
+//   k_final  (requests)         accepted length from the row decisions, the bonus token of that
+//                               row (a dense row's planned chunk scanned here), outputs and KV
+//                               slots
 // Workgroups never wait on one another inside a kernel: on this multi-XCD part a device-scope
 // fence writes back and invalidates the whole L2, so every hand-off is a kernel boundary.
 //
@@ -29,7 +29,6 @@
 
 namespace dsv {
 
-constexpr int EPT_MAX = 40;  // bonus elements per thread: vocab <= NCH * BCT * 40 = 327680
 
 struct KParams {
   dsv_verify_args a;
@@ -37,17 +36,13 @@ struct KParams {
   ListEntry* lists;       // [rows, DSV_LIST_K]
   ChunkStat* cstat;       // [rows, C]
   uint64_t* cand;         // [rows, C, kcand]
-  BonusChunk* bchunks;    // [bs, NCH]
-  int32_t* qrank;         // [bs, QMAX]: ties at the cut key before the q id, within its chunk
-  double* tmass;          // [bs, NCH * BCT]: per-thread mass of the bonus row above the cut
-  int32_t* tties;         // [bs, NCH * BCT]: per-thread count of values at the cut key
+  int64_t* rbonus;        // [rows]: the bonus token each row gives as the accepted length
+  struct DrawPlan* plans; // [rows]: dense rows' planned bonus draw
   int32_t* step_ok;       // [rows]: 1 when the draft token verified by the row is accepted
   uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
   uint32_t* hpart;        // [rows, C, HWIN / 2]: nucleus rows' per-chunk window counts (16-bit pairs)
   uint32_t* nhist;        // [NUC_GRID, 65536]: full-histogram counts, one area per k_nuc workgroup
   int64_t pwords;
-  int64_t bchunk;         // elements per bonus chunk = BCT * ept
-  int32_t ept, nch;       // bonus elements per thread (multiple of 8), bonus chunks
   int32_t C;              // chunks per row
   int32_t kcand;          // candidate slots per chunk
   int32_t aligned;        // logits rows are 16-byte aligned
@@ -140,6 +135,350 @@ __device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char*
 }
 
 // ---------------------------------------------------------------------------------------
+// Bonus draw machinery (used by the row merge and k_final; see the bonus section below)
+// ---------------------------------------------------------------------------------------
+constexpr int FCT = 512;      // threads of k_final
+constexpr int DNW_MAX = FCT / WAVE;
+constexpr int64_t BONUS_LATER = -2;  // rbonus: the row is drawn in k_final
+constexpr int64_t BONUS_PLAN = -3;   // rbonus: k_final scans the row's planned chunk
+
+struct DrawShared {
+  double red_d[DNW_MAX];
+  int32_t red_i[DNW_MAX];
+  uint64_t red_u[DNW_MAX];
+  int64_t qid[QMAX];
+  float qv[QMAX];       // clamped q of the lane
+  int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
+  int32_t qrank[QMAX];  // q id at a split cut key: values at the cut key before it (id order), else -1
+  float qx[QMAX];       // adjusted value at the q id
+  double qd[QMAX];      // P - max(P - q, 0) at a q id (the residual's reduction), else 0
+  double cm[NCHK];      // chunk masses of P above the cut (every id of an unfiltered row)
+  int32_t ct[NCHK];     // chunk counts of values at the cut key
+  ListEntry lst[DSV_LIST_K];  // a support-list row's entries, sorted by id
+  int32_t nlist;
+  int64_t bonus;
+  double chunk_lo, thr, pick_lo;
+  int32_t acc, chunk, tieq, use_r, pick_thread, tb_pick;
+};
+
+// The draw's P at value x: exp2(x c2 - M c2) * scale, scale = 1/Z (over the kept mass S for a
+// filtered row).
+struct BonusP {
+  float c2, mc2, scale;
+  __device__ __forceinline__ float operator()(float x) const {
+    return __builtin_amdgcn_exp2f(fmaf(x, c2, -mc2)) * scale;
+  }
+};
+template <int DT>
+__device__ __forceinline__ BonusP bonus_p(const RowSum& rs, float T) {
+  BonusP q;
+  q.c2 = log2e_over(T);
+  q.mc2 = value_of_key<DT>(rs.kmax) * q.c2;
+  q.scale = rs.invZ * ((rs.mode == M_HIST || rs.norm) ? 1.f / rs.S_f : 1.f);
+  return q;
+}
+
+// Stage the sparse q of draft step `step` of request b (live = false: no q): ids, clamped
+// values, and which lane of a repeated id carries the residual's q (the last one).
+__device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, int step, bool live, DrawShared& sh) {
+  const int tid = threadIdx.x;
+  const int64_t qi = ((int64_t)b * (a.T - 1) + step) * a.K;
+  for (int l = tid; l < QMAX; l += blockDim.x) {
+    const bool on = live && l < a.K;
+    sh.qid[l] = on ? load_index(a.q_ids, a.q_ids_i64, qi + l) : -1;
+    sh.qv[l] = on ? clamp01(a.q_values[qi + l]) : 0.f;
+    sh.qd[l] = 0.0;
+    sh.qrank[l] = -1;
+  }
+  __syncthreads();
+  for (int l = tid; l < QMAX; l += blockDim.x) {
+    bool last = sh.qid[l] >= 0 && sh.qid[l] < a.vocab;
+    for (int l2 = l + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != sh.qid[l];
+    sh.qlast[l] = last;
+  }
+  __syncthreads();
+}
+
+// Thread t's span of chunk c in id order (NT threads tile the chunk: ids c*chunk + t*FE + [0,
+// FE)), penalised and handed to f(i, x) in id order; -inf past the row.
+template <int DT, bool ALIGNED, int NT, class F>
+__device__ __forceinline__ void for_span(const KParams& P, int b, const char* rowp, int c, float pres, float rep,
+                                         F&& f) {
+  constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
+  constexpr int SV = CT * CV / NT, FE = SV * n;  // vectors and ids a thread
+  static_assert(SV * NT == CT * CV && FE <= 96, "spans tile a chunk");
+  const int64_t V = P.a.vocab;
+  const int64_t clo = (int64_t)c * CHE, chi = clo + CHE < V ? clo + CHE : V;
+  const int64_t jlo = clo + (int64_t)threadIdx.x * FE;
+  uint4 v[SV];
+  if constexpr (ALIGNED) {
+    const auto rsr = buf_rsrc(rowp + clo * (16 / n), (uint32_t)((chi - clo) * (16 / n)));
+#pragma unroll
+    for (int u = 0; u < SV; ++u) v[u] = buf_load16(rsr, (uint32_t)threadIdx.x * (SV * 16u), (uint32_t)(u * 16));
+#pragma unroll
+    for (int u = 0; u < SV; ++u)  // past the row: the buffer reads zeros; -inf and the partial last vector
+      if (jlo + u * n + n > chi) v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
+  } else {
+#pragma unroll
+    for (int u = 0; u < SV; ++u) v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
+  }
+  uint64_t blo = 0, bhi = 0;  // the span's history bits (tokens >= vocab have none)
+  if (P.pbits) {
+    const auto rb = buf_rsrc(P.pbits + (int64_t)b * P.pwords, (uint32_t)(P.pwords * 4));
+    const uint32_t w0 = (uint32_t)(jlo >> 5) * 4u, sh = (uint32_t)(jlo & 31);
+    const uint64_t A = (uint64_t)buf_load4(rb, w0, 0) | ((uint64_t)buf_load4(rb, w0, 4) << 32);
+    const uint64_t B = (uint64_t)buf_load4(rb, w0, 8) | ((uint64_t)buf_load4(rb, w0, 12) << 32);
+    blo = (A >> sh) | (sh ? B << (64 - sh) : 0ull);
+    bhi = B >> sh;
+  }
+#pragma unroll
+  for (int u = 0; u < SV; ++u)
+#pragma unroll
+    for (int e = 0; e < n; ++e) {
+      const int i = u * n + e;
+      float x = vec_elem<DT>(v[u], e);
+      if (((i < 64 ? blo >> i : bhi >> (i - 64)) & 1ull)) x = penalize<DT>(x, pres, rep);
+      f(i, x);
+    }
+}
+
+// Support-list draw (wave 0): entries sh.lst[0, sh.nlist) sorted by id; q staged when resid.
+__device__ __forceinline__ int64_t list_draw(const dsv_verify_args& a, bool resid, float uf, const DrawShared& sh) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const bool live = lane < sh.nlist;
+  const ListEntry e = live ? sh.lst[lane] : ListEntry{INT_MAX, 0.f};
+  const double Pi = (double)e.P;
+  double w = Pi;
+  if (resid && live)
+    for (int l = 0; l < a.K; ++l)
+      if (sh.qlast[l] && sh.qid[l] == (int64_t)e.id) w = fmax(Pi - (double)sh.qv[l], 0.0);
+  double lo, hi;
+  double mass = wave_tiles(w, lo, hi);
+  if (!resid || !(mass > 0.0)) mass = wave_tiles(Pi, lo, hi);
+  const double thr = (double)uf * mass;
+  const uint64_t hit = __ballot(live && lo <= thr && thr < hi);
+  return hit ? __shfl((int64_t)e.id, __ffsll((long long)hit) - 1, WAVE) : a.vocab - 1;
+}
+
+// What a dense row's draw needs after the chunk is known (the row merge writes it; k_final
+// reads it for the accepted row).
+struct DrawPlan {
+  double thr, chunk_lo;  // the threshold u * mass and the mass before the chunk
+  int32_t chunk, tieq;   // the chunk (-1: no mass anywhere) and the cut-key values before it
+  int32_t use_r, pad;    // residual (1) or P (0)
+  double qd[QMAX];       // the residual's reduction at each q lane
+};
+
+// Dense draw, first part, over the NT threads of the workgroup: sh.cm / sh.ct hold the chunk
+// masses and cut counts, q is staged when resid.  Leaves the plan in sh (chunk, thr, chunk_lo,
+// tieq, use_r, qd).
+template <int DT, bool ALIGNED, int NT>
+__device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
+                                           bool resid, float uf, DrawShared& sh) {
+  constexpr int NW = NT / WAVE;
+  constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int64_t V = a.vocab;
+  const int C = P.C;
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const bool hist = rs.mode == M_HIST;
+  const BonusP bp = bonus_p<DT>(rs, T);
+  const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
+  const bool tie_cut = hist && rs.ktie > 0 && rs.ktie != INT_MAX;  // the cut splits a key's values
+  // the q ids' adjusted values; ids at a split cut key need their rank among its values
+  if (tid < WAVE) {
+    const bool qlive = resid && lane < a.K && sh.qlast[lane];
+    float xq = -INFINITY;
+    if (qlive) {
+      const int64_t qid = sh.qid[lane];
+      xq = load_elem<DT>(rowp, qid);
+      if (pen && pen_test(P, b, qid)) xq = penalize<DT>(xq, pres, rep);
+    }
+    if (lane < QMAX) {
+      sh.qx[lane] = xq;
+      sh.qrank[lane] = (qlive && tie_cut && key_of<DT>(xq) == rs.vcut) ? 0 : -1;
+    }
+  }
+  __syncthreads();
+  for (int l = 0; l < a.K; ++l) {  // (rare) rank of a q id among the cut key's values
+    if (sh.qrank[l] < 0) continue;
+    const int64_t qid = sh.qid[l];
+    const int cq = (int)(qid / CHE);
+    const int64_t jlo = (int64_t)cq * CHE + (int64_t)tid * FE;
+    int32_t before = 0;
+    for_span<DT, ALIGNED, NT>(P, b, rowp, cq, pres, rep,
+                              [&](int i, float x) { before += (key_of<DT>(x) == rs.vcut) & (jlo + i < qid); });
+    before = block_sum<NW>(before, sh.red_i);
+    if (tid == 0) {
+      for (int c = 0; c < cq; ++c) before += sh.ct[c];
+      sh.qrank[l] = before;
+    }
+    __syncthreads();
+  }
+  if (tid < WAVE) {
+    // the residual's reduction at each q id (lanes hold the q lanes)
+    if (resid && lane < a.K && sh.qlast[lane]) {
+      const float xq = sh.qx[lane];
+      const uint32_t k = key_of<DT>(xq);
+      const bool kept = !hist || k > rs.vcut ||
+                        (k == rs.vcut && (rs.ktie == INT_MAX || (sh.qrank[lane] >= 0 && sh.qrank[lane] < rs.ktie)));
+      const double Pq = kept ? (double)bp(xq) : 0.0;
+      sh.qd[lane] = Pq - fmax(Pq - (double)sh.qv[lane], 0.0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // lanes hold the chunks: masses with the kept values at the cut key, then the residual's
+    const int32_t ctl = lane < C ? sh.ct[lane] : 0;
+    int32_t tie_prefix = ctl;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int32_t t = __shfl_up(tie_prefix, o, WAVE);
+      if (lane >= o) tie_prefix += t;
+    }
+    tie_prefix -= ctl;
+    int32_t kt = 0;
+    if (hist) {
+      const int64_t room = (int64_t)rs.ktie - tie_prefix;
+      kt = room <= 0 ? 0 : (room < ctl ? (int32_t)room : ctl);
+    }
+    const double Mp = lane < C ? sh.cm[lane] + (kt > 0 ? (double)kt * P_cut : 0.0) : 0.0;
+    double Mr = Mp;
+    if (resid && lane < C)
+      for (int l = 0; l < a.K; ++l)
+        if (sh.qlast[l] && sh.qid[l] / CHE == lane) Mr -= sh.qd[l];
+    double lo_r, hi_r, lo_p, hi_p;
+    const double mr = wave_tiles(Mr, lo_r, hi_r);
+    const double mp = wave_tiles(Mp, lo_p, hi_p);
+    const bool use_r = resid && mr > 0.0;
+    const double thr = (double)uf * (use_r ? mr : mp);
+    const double clo = use_r ? lo_r : lo_p, chi = use_r ? hi_r : hi_p;
+    const double cmass = use_r ? Mr : Mp;
+    uint64_t hit = __ballot(lane < C && cmass > 0.0 && clo <= thr && thr < chi);
+    if (!hit) {  // rounding left the threshold at the end: the last chunk with mass
+      const uint64_t pos = __ballot(lane < C && cmass > 0.0);
+      hit = pos ? 1ull << (63 - __clzll((long long)pos)) : 0ull;
+    }
+    const int cstar = hit ? __ffsll((long long)hit) - 1 : -1;
+    if (tid == 0) {
+      sh.chunk = cstar;
+      sh.thr = thr;
+      sh.use_r = use_r ? 1 : 0;
+    }
+    if (cstar >= 0 && lane == cstar) {
+      sh.chunk_lo = clo;
+      sh.tieq = tie_prefix;
+    }
+  }
+  __syncthreads();
+}
+
+// Dense draw, second part: the planned chunk in id order -- per-thread masses, the thread whose
+// mass holds the threshold, then its ids.  Returns the token (every thread).
+template <int DT, bool ALIGNED, int NT>
+__device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
+                                              DrawShared& sh) {
+  constexpr int NW = NT / WAVE;
+  constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int64_t V = a.vocab;
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const bool hist = rs.mode == M_HIST;
+  const BonusP bp = bonus_p<DT>(rs, T);
+  const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
+  if (tid == 0) {
+    sh.bonus = V - 1;
+    sh.pick_thread = -1;
+  }
+  __syncthreads();
+  const int cstar = sh.chunk;
+  if (cstar < 0) return V - 1;
+  const bool use_r = sh.use_r != 0;
+  const int64_t jlo = (int64_t)cstar * CHE + (int64_t)tid * FE;
+  double mt = 0.0;
+  int32_t tt = 0;
+  for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, [&](int, float x) {
+    const uint32_t k = key_of<DT>(x);
+    if (!hist || k > rs.vcut)
+      mt += (double)bp(x);
+    else if (k == rs.vcut)
+      ++tt;
+  });
+  int32_t tie_tot = 0;
+  const int32_t tbefore = sh.tieq + block_excl_scan<NW>(tt, sh.red_i, &tie_tot);
+  int32_t kept_t = 0;
+  if (hist) {
+    const int64_t room = (int64_t)rs.ktie - tbefore;
+    kept_t = room <= 0 ? 0 : (room < tt ? (int32_t)room : tt);
+  }
+  double w_t = mt + (kept_t > 0 ? (double)kept_t * P_cut : 0.0);
+  if (use_r)
+    for (int l = 0; l < a.K; ++l)
+      if (sh.qlast[l] && sh.qid[l] >= jlo && sh.qid[l] < jlo + FE) w_t -= sh.qd[l];
+  double tlo, thi;
+  block_tiles<NW>(w_t, sh.red_d, tlo, thi);
+  const double base = sh.chunk_lo, thr = sh.thr;
+  if (w_t > 0.0 && base + tlo <= thr && thr < base + thi) sh.pick_thread = tid;
+  __syncthreads();
+  int pt = sh.pick_thread;
+  if (pt < 0) {
+    // rounding left the threshold past this chunk's recomputed mass: the last thread with mass
+    const uint64_t lp = block_max_u64<NW>(w_t > 0.0 ? (uint64_t)tid + 1 : 0ull, sh.red_u);
+    pt = lp ? (int)lp - 1 : -1;
+  }
+  if (tid == pt) {
+    sh.tb_pick = tbefore;
+    sh.pick_lo = base + tlo;
+  }
+  __syncthreads();
+  if (pt >= 0 && tid < WAVE) {
+    // thread pt's span, one id a lane (in passes of a wave): weights, then the running sum
+    const int64_t plo = (int64_t)cstar * CHE + (int64_t)pt * FE;
+    double start = sh.pick_lo;
+    int32_t seen_before = 0;
+    int64_t pick = -1, last_pos = -1;
+    for (int p0 = 0; p0 < FE && pick < 0; p0 += WAVE) {
+      const int64_t j = plo + p0 + lane;
+      const bool live = p0 + lane < FE && j < V;
+      float xj = live ? load_elem<DT>(rowp, j) : -INFINITY;
+      if (live && pen && pen_test(P, b, j)) xj = penalize<DT>(xj, pres, rep);
+      const uint32_t k = key_of<DT>(xj);
+      const bool tie = live && hist && k == rs.vcut;
+      const uint64_t tmask = __ballot(tie);
+      const int32_t seen = seen_before + __popcll(tmask & ((1ull << lane) - 1ull));
+      double Pj = 0.0;
+      if (live) {
+        if (!hist || k > rs.vcut)
+          Pj = (double)bp(xj);
+        else if (tie && (int64_t)sh.tb_pick + seen < (int64_t)rs.ktie)
+          Pj = P_cut;
+        if (use_r)
+          for (int l = 0; l < a.K; ++l)
+            if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
+      }
+      double wlo, whi;
+      const double tot = wave_tiles(Pj, wlo, whi);
+      const uint64_t hitj = __ballot(live && Pj > 0.0 && start + whi > thr);
+      const uint64_t pos = __ballot(live && Pj > 0.0);
+      if (hitj) pick = plo + p0 + (__ffsll((long long)hitj) - 1);
+      if (pos) last_pos = plo + p0 + (63 - __clzll((long long)pos));
+      start += tot;
+      seen_before += __popcll(tmask);
+    }
+    if (pick < 0) pick = last_pos;  // rounding: the last id with mass
+    if (lane == 0 && pick >= 0) sh.bonus = pick;
+  }
+  __syncthreads();
+  return sh.bonus;
+}
+
+// ---------------------------------------------------------------------------------------
 // Row merge (the last chunk workgroup of a row): chunk partials -> RowSum, support list and
 // the step decision.  Rank selection of the row's top-K uses the whole workgroup; the rest
 // runs on wave 0.
@@ -151,7 +490,8 @@ struct MergeShared {
 };
 
 template <int DT>
-__device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, int s, int mode, float T, MergeShared& ms) {
+__device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, int s, int mode, float T, MergeShared& ms,
+                                          DrawShared& ds, RowSum* srs) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int C = P.C;
@@ -226,6 +566,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     if (lane == 0) {
       list[0] = ListEntry{arg, 1.f};
       P.rowsum[r] = rs;
+      *srs = rs;
       P.step_ok[r] = ok;
     }
     return;
@@ -237,16 +578,8 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   rs.Z = Z;
   rs.m_f = m_f;
   rs.invZ = invZ;
-  // the draft token's adjusted logit
-  float xt = -INFINITY;
-  if (tok >= 0 && tok < a.vocab) {
-    xt = load_elem<DT>(row_ptr(a, r), tok);
-    if (P.pbits && pen_test(P, b, tok)) {
-      const float pres = a.presence ? a.presence[b] : 0.f;
-      const float rep = a.repetition ? a.repetition[b] : 1.f;
-      xt = penalize<DT>(xt, pres, rep);
-    }
-  }
+  // the draft token's adjusted logit (recorded by the chunk that holds it)
+  const float xt = (tok >= 0 && tok < a.vocab) ? cs[tok / Elems<DT>::chunk].xtok : -INFINITY;
   if (mode == M_UNF) {
     const float p = (tok >= 0 && tok < a.vocab) ? prob_of(xt, T, m_f, invZ) : 0.f;
     if (a.filter) {  // filtered request with nothing cut: P = p / sum(p)
@@ -256,6 +589,12 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
       rs.p_draft = p / rs.S_f;
     } else {
       rs.p_draft = p;
+    }
+    // each chunk's mass of P for the bonus draw: its softmax partial sum at the row's scale
+    if (lane < C) {
+      const double mc = m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0;
+      ds.cm[lane] = mc * (double)(invZ * (rs.norm ? 1.f / rs.S_f : 1.f));
+      ds.ct[lane] = 0;
     }
   } else {
     // LIST: lane j holds the j-th largest candidate
@@ -289,12 +628,17 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     const int32_t kid = keep ? id : INT_MAX;
     int rank = 0;
     for (int i = 0; i < kk; ++i) rank += __shfl(kid, i, WAVE) < kid;
-    if (keep) list[rank] = ListEntry{id, Pj};
+    if (keep) {
+      list[rank] = ListEntry{id, Pj};
+      ds.lst[rank] = ListEntry{id, Pj};
+    }
     rs.nlist = __popcll(__ballot(keep));
+    if (lane == 0) ds.nlist = rs.nlist;
   }
   const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
   if (lane == 0) {
     P.rowsum[r] = rs;
+    *srs = rs;
     P.step_ok[r] = ok;
   }
 }
@@ -328,18 +672,20 @@ struct NucMergeShared {
 // p of a nucleus row at its draft token and the step decision; RowSum out (wave 0).
 template <int DT>
 __device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int b, int s, RowSum rs, float T,
-                                               float xtok, int64_t tok, int64_t tie_tok) {
+                                               float xtok, int64_t tok, int64_t tie_tok, RowSum* srs) {
   const bool kept = key_of<DT>(xtok) > rs.vcut || (key_of<DT>(xtok) == rs.vcut && tie_tok < (int64_t)rs.ktie);
   rs.p_draft = (tok >= 0 && tok < P.a.vocab && kept) ? prob_of(xtok, T, rs.m_f, rs.invZ) / rs.S_f : 0.f;
   const int32_t ok = tok >= 0 ? step_accept_wave(P.a, b, s, tok, rs.p_draft) : 0;
   if (threadIdx.x == 0) {
     P.rowsum[r] = rs;
+    if (srs) *srs = rs;
     P.step_ok[r] = ok;
   }
 }
 
 template <int DT>
-__device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh) {
+__device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh,
+                                              DrawShared& ds, RowSum* srs) {
   constexpr int NW = CT / WAVE;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
@@ -392,16 +738,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       kb = lo;
     }
     sh.kb_row = kb;
-    float xt = -INFINITY;
-    if (tok >= 0 && tok < a.vocab) {
-      xt = load_elem<DT>(row_ptr(a, r), tok);
-      if (P.pbits && pen_test(P, b, tok)) {
-        const float pres = a.presence ? a.presence[b] : 0.f;
-        const float rep = a.repetition ? a.repetition[b] : 1.f;
-        xt = penalize<DT>(xt, pres, rep);
-      }
-    }
-    sh.xtok = xt;
+    sh.xtok = (tok >= 0 && tok < a.vocab) ? cs[tok / Elems<DT>::chunk].xtok : -INFINITY;
   }
   __syncthreads();
   RowSum rs;
@@ -423,6 +760,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     if (tid == 0) {
       rs.flags = FLAG_FULL_HIST;
       P.rowsum[r] = rs;
+      *srs = rs;
       P.step_ok[r] = 0;
     }
     return;
@@ -528,6 +866,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     if (tid == 0) {
       rs.flags = FLAG_FULL_HIST;
       P.rowsum[r] = rs;
+      *srs = rs;
       P.step_ok[r] = 0;
     }
     return;
@@ -556,6 +895,33 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     rs.S_kept = m_total;
   }
   rs.S_f = (float)rs.S_kept;
+  // For the bonus draw: each chunk's mass of P over the keys above the cut, and its count of
+  // values at the cut key.  Every key above the cut is in every window (the cut is at or above
+  // kcov, or below every counted value), so the window counts hold them all.
+  const BonusP bp = bonus_p<DT>(rs, T);
+  for (int c = wid; c < C; c += NW) {
+    const uint32_t wl = sh.cw[c], kh = sh.ck[c];
+    double mc = 0.0;
+    int32_t tc = 0;
+    if (wl != WIN_EMPTY) {
+      const uint32_t k0 = rs.vcut + 1u > wl ? rs.vcut + 1u : wl;
+      const uint32_t* hp = P.hpart + (r * C + c) * (int64_t)(HWIN / 2);
+      for (uint32_t k = k0 + (uint32_t)lane; k <= kh; k += WAVE) {
+        const uint32_t o = k - wl;
+        const uint32_t cnt = (hp[o >> 1] >> ((o & 1u) * 16u)) & 0xFFFFu;
+        if (cnt) mc += (double)cnt * (double)bp(value_of_key<DT>(k));
+      }
+      if (lane == 0 && rs.vcut >= wl && rs.vcut <= kh) {
+        const uint32_t o = rs.vcut - wl;
+        tc = (int32_t)((hp[o >> 1] >> ((o & 1u) * 16u)) & 0xFFFFu);
+      }
+    }
+    mc = wave_sum(mc);
+    if (lane == 0) {
+      ds.cm[c] = mc;
+      ds.ct[c] = tc;
+    }
+  }
   const float xt = sh.xtok;
   if (tid < WAVE) {
     // values of the draft token's key ahead of it: the whole counts of the chunks before its
@@ -577,7 +943,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       }
     }
     tie_tok = wave_sum(tie_tok);
-    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok);
+    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok, srs);
   }
 }
 
@@ -810,7 +1176,7 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
       rs.S_kept = fS;
     }
     rs.S_f = (float)rs.S_kept;
-    nucleus_finish<DT>(P, r, b, s, rs, T, sh.xtok, tok, tie_tok);
+    nucleus_finish<DT>(P, r, b, s, rs, T, sh.xtok, tok, tie_tok, nullptr);
   }
   __syncthreads();
 }
@@ -870,7 +1236,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   __shared__ uint4 s_hv[CT / WAVE * WHITV];  // history-hit vectors of each wave
   __shared__ uint32_t s_hm[CT / WAVE * WHITV];
   __shared__ int32_t s_cnt, s_nq;
-  __shared__ uint32_t s_wlo, s_ktok;
+  __shared__ uint32_t s_wlo;
+  __shared__ float s_xtok;
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
@@ -921,7 +1288,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       pres = a.presence ? a.presence[b] : 0.f;
       rep = a.repetition ? a.repetition[b] : 1.f;
     }
-    if (mode == M_HIST) tok = step_token(a, b, s);
+    if (mode != M_GREEDY) tok = step_token(a, b, s);
   }
   asm volatile("" ::"s"(T), "s"(top_p), "s"(pres), "s"(rep), "s"(topk), "s"(tok));
   ChunkStat* st = P.cstat + r * C + c;
@@ -1013,6 +1380,21 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
   }
 
+  // the draft token's adjusted value, from the registers of the thread that holds it (read by
+  // thread 0 and the nucleus pass after the softmax sum's barriers)
+  const bool tok_here = tok >= lo && tok < hi;
+  if (tok_here) {
+    const int rel = (int)(tok - lo);
+    const int vi = rel / n, uu = vi / CT;
+    if (tid == vi - uu * CT) {
+      uint4 w = v[0];
+#pragma unroll
+      for (int u = 1; u < CV; ++u)
+        if (u == uu) w = v[u];
+      s_xtok = vec_elem_dyn<DT>(w, rel - vi * n);
+    }
+  }
+
   // max and the first index attaining it
   float m_t = -INFINITY;
   int bu = -1;
@@ -1048,6 +1430,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   out.tieq = 0;
   out.wlo = WIN_EMPTY;
   out.kx = 0u;
+  out.xtok = 0.f;
+  out.pad = 0;
 
   if (P.softmax && mode != M_GREEDY && cbest) {
     const float c2 = log2e_over(T);
@@ -1070,20 +1454,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       // exp((x - m) / T) / (s * C) (this chunk's sum standing for each of the row's C chunks)
       // reaches 2 (1 - top_p) / V.  The row merge takes the cut from the counts when it lies
       // in every chunk's window, and the full-histogram path otherwise.
-      const bool tok_here = tok >= lo && tok < hi;
       uint32_t* cnt = reinterpret_cast<uint32_t*>(big);
-      if (tok_here) {
-        // the draft token's (penalised) value, from the registers of the thread that holds it
-        const int rel = (int)(tok - lo);
-        const int vi = rel / n, uu = vi / CT;
-        if (tid == vi - uu * CT) {
-          uint4 w = v[0];
-#pragma unroll
-          for (int u = 1; u < CV; ++u)
-            if (u == uu) w = v[u];
-          s_ktok = key_of<DT>(vec_elem_dyn<DT>(w, rel - vi * n));
-        }
-      }
       if (tid == 0) {
         uint32_t wlo = WIN_EMPTY;
         if (cbest) {
@@ -1113,8 +1484,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       const uint32_t wlo = s_wlo;
       int tq = 0;
       if (tok_here) {  // values equal to the draft token's ahead of it
-        const uint32_t ktok = s_ktok;
-        const float xtv = value_of_key<DT>(ktok);
+        const float xtv = s_xtok;
         // element e of vector u is ahead of tok iff u * CT * n + e < rel
         const int64_t rel64 = tok - (v0 + tid) * n;
         const int rel = (int)(rel64 < 0 ? 0 : (rel64 > CV * CT * n ? CV * CT * n : rel64));
@@ -1285,16 +1655,22 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
     out.ncand = kk;
   }
-  if (tid == 0) *st = out;
+  if (tok_here) __syncthreads();  // (orders the owner's s_xtok before thread 0 in every mode)
+  if (tid == 0) {
+    if (tok_here) out.xtok = s_xtok;
+    *st = out;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
 // k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0)
 // ---------------------------------------------------------------------------------------
-template <int DT>
+template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(CT) void k_merge(KParams P) {
   __shared__ MergeShared ms;
   __shared__ NucMergeShared ns;
+  __shared__ DrawShared ds;
+  __shared__ RowSum srs;
   const dsv_verify_args& a = P.a;
   const int64_t r = blockIdx.x;
   int b, s;
@@ -1306,23 +1682,57 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
     return;
   }
   const int mode = row_mode(a, b, 0);
+  const float T = a.temperatures[b];
   if (mode == M_HIST) {
-    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, a.temperatures[b], ns);
-    return;
+    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, T, ns, ds, &srs);
+  } else {
+    merge_row<DT>(P, r, b, s, mode, T, ms, ds, &srs);
   }
-  merge_row<DT>(P, r, b, s, mode, a.temperatures[b], ms);
+  __syncthreads();
+  // the bonus token this row gives when it is the request's accepted length (k_final picks it)
+  const RowSum rs = srs;
+  const int cap = req_cap(a, b);
+  const bool resid = s < cap - 1;  // row s ends the prefix when draft s+1 is rejected
+  int64_t bonus;
+  if (rs.mode == M_GREEDY) {
+    bonus = rs.argmax;
+  } else if (rs.mode == M_LIST) {
+    stage_q(a, b, s, resid, ds);
+    bonus = threadIdx.x < WAVE ? list_draw(a, resid, a.uniform_final[b], ds) : 0;
+  } else if (rs.flags & FLAG_FULL_HIST) {
+    bonus = BONUS_LATER;
+  } else {
+    // the chunk and threshold; k_final scans the chunk when this row is the accepted one
+    stage_q(a, b, s, resid, ds);
+    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, resid, a.uniform_final[b], ds);
+    DrawPlan* pl = P.plans + r;
+    if (threadIdx.x < QMAX) pl->qd[threadIdx.x] = ds.qd[threadIdx.x];
+    if (threadIdx.x == 0) {
+      pl->thr = ds.thr;
+      pl->chunk_lo = ds.chunk_lo;
+      pl->chunk = ds.chunk;
+      pl->tieq = ds.tieq;
+      pl->use_r = ds.use_r;
+      pl->pad = 0;
+    }
+    bonus = BONUS_PLAN;
+  }
+  if (threadIdx.x == 0) P.rbonus[r] = bonus;
 }
 
 // ---------------------------------------------------------------------------------------
-// Bonus draw helpers
+// Bonus draw (sampling/sparse/accept.py:249-307 and :179-204; runtime/worker.py:1048-1089)
+//
+// The bonus of a request is drawn from its row at the accepted length a: max(P - q_a, 0) when
+// draft a+1 was rejected (P when that residual has no mass), P when every draft was accepted,
+// by inverse CDF in id order.  Which draw a row would make is fixed before a is known, so the
+// row merge draws every row's token (k_final picks row a's): support-list rows over their list,
+// dense rows (unfiltered, nucleus) by locating the chunk from chunk masses -- softmax partial
+// sums at the row scale, or the nucleus window counts above the cut -- less the residual's
+// reduction at the q ids, then scanning that one chunk in id order.  Rows whose cut the full
+// histogram settles (k_nuc) are drawn in k_final the same way.  The draw's P is computed with
+// exp2 (within a few float ulps of the reference's p / S); the accept test uses the exact P.
 // ---------------------------------------------------------------------------------------
-// P at one element of a dense-support bonus row.
-__device__ __forceinline__ double dense_P(const RowSum& rs, float T, float x) {
-  const float p = prob_of(x, T, rs.m_f, rs.invZ);
-  return (rs.mode == M_HIST || rs.norm) ? (double)(p / rs.S_f) : (double)p;
-}
-
-
 __device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, int acc, int64_t bonus) {
   const int T = a.T;
   for (int i = threadIdx.x; i < T; i += blockDim.x) {
@@ -1349,373 +1759,93 @@ __device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, i
   }
 }
 
-// The elements [lo_t, lo_t + cnt) of a thread's bonus range, penalised, as floats.
+// ---------------------------------------------------------------------------------------
+// k_final: outputs, one workgroup per request -- the accepted length a, and the bonus token of
+// row a (drawn by the row merge, or here for rows the full histogram settled)
+// ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__device__ __forceinline__ void load_range(const KParams& P, int b, const char* rowp, int64_t lo_t, int64_t hi_t,
-                                           float pres, float rep, float (&x)[EPT_MAX]) {
-  constexpr int n = Elems<DT>::n;
-  constexpr int NV = EPT_MAX / n;
-  uint4 v[NV];
-  const int nv = (P.ept + n - 1) / n;
-  if constexpr (ALIGNED) {
-    // whole vectors inside the row: clamped, unconditional loads; the rest filled below
-    const int64_t nfull = P.a.vocab / n;
-    const uint32_t fill = DT == DSV_BF16 ? FILL_BF16 : FILL_F32;
-#pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      const int64_t vi = lo_t / n + u;
-      v[u] = load_vec_raw(rowp, vi < nfull ? vi : nfull - 1);
-    }
-#pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      const int64_t vi = lo_t / n + u;
-      if (u >= nv || vi * n >= hi_t) v[u] = make_uint4(fill, fill, fill, fill);
-      else if (vi >= nfull) v[u] = load_vec<DT>(rowp, vi, hi_t, false);  // the row's partial last vector
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < NV; ++u)
-      v[u] = u < nv ? load_vec<DT>(rowp, lo_t / n + u, hi_t, false) : make_uint4(0, 0, 0, 0);
-  }
-  uint64_t bits = 0;
-  if (P.pbits && lo_t < hi_t) {
-    const int64_t w0 = lo_t >> 5;
-    bits = pen_word(P, b, w0);
-    if (w0 + 1 < P.pwords) bits |= (uint64_t)pen_word(P, b, w0 + 1) << 32;
-    bits >>= (lo_t & 31);
-  }
-#pragma unroll
-  for (int u = 0; u < NV; ++u)
-#pragma unroll
-    for (int e = 0; e < n; ++e) {
-      const int i = u * n + e;
-      float xv = vec_elem<DT>(v[u], e);
-      if ((bits >> i) & 1ull) xv = penalize<DT>(xv, pres, rep);
-      x[i] = xv;
-    }
-}
-
-// Accepted length of request b: the first rejected step (all threads get it; uses sh.acc).
-struct BonusShared {
-  double red_d[BCT / WAVE];
-  int32_t red_i[BCT / WAVE];
-  uint64_t red_u[BCT / WAVE];
-  int64_t qid[QMAX];
-  float qv[QMAX];       // clamped q of the lane
-  int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
-  double qd[QMAX];      // P - max(P - q, 0) of a kept q id (the residual's reduction), else 0
-  int64_t bonus;
-  double chunk_lo, thr, pick_lo;
-  int32_t acc, chunk, tieq, use_r, pick_thread, tb_pick;
-};
-
-struct ReqView {
-  int64_t row0;
-  int cap, acc;
-  bool rows_ok, all;
-};
-
-__device__ __forceinline__ ReqView request_view(const KParams& P, int b, BonusShared& sh) {
+__global__ __launch_bounds__(FCT) void k_final(KParams P) {
+  constexpr int CHE = Elems<DT>::chunk;
+  __shared__ DrawShared sh;
   const dsv_verify_args& a = P.a;
+  const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-  ReqView q;
-  q.row0 = request_row0(a, b);
-  q.cap = req_cap(a, b);
-  q.rows_ok = q.row0 >= 0 && q.row0 < a.rows;
-  if (q.rows_ok && q.row0 + q.cap > a.rows) q.cap = (int)(a.rows - q.row0);
-  if (tid < WAVE) {
-    int acc = q.rows_ok ? q.cap - 1 : 0;
-    for (int s0 = 0; s0 < acc; s0 += WAVE) {
+  const int64_t V = a.vocab;
+  int64_t row0 = request_row0(a, b);
+  int cap = req_cap(a, b);
+  const bool rows_ok = row0 >= 0 && row0 < a.rows;
+  if (!rows_ok) {  // inconsistent row offsets: no row of this request can be read
+    write_outputs(a, b, 0, V - 1);
+    return;
+  }
+  if (row0 + cap > a.rows) cap = (int)(a.rows - row0);
+  if (tid < WAVE) {  // the first rejected step
+    int acc = cap - 1;
+    for (int s0 = 0; s0 < cap - 1; s0 += WAVE) {
       const int s = s0 + lane;
-      const uint64_t rej = __ballot(s < q.cap - 1 && P.step_ok[q.row0 + s] == 0);
+      const uint64_t rej = __ballot(s < cap - 1 && P.step_ok[row0 + s] == 0);
       if (rej) {
         acc = s0 + __ffsll((long long)rej) - 1;
         break;
       }
     }
-    if (tid == 0) sh.acc = acc;
-  }
-  __syncthreads();
-  q.acc = sh.acc;
-  q.all = q.acc == q.cap - 1;
-  return q;
-}
-
-// Stage the sparse q of the rejected step: ids, clamped values, and which lane of a repeated
-// id carries the residual's q (the last one).
-__device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, const ReqView& q, BonusShared& sh) {
-  const int tid = threadIdx.x;
-  const int64_t qi = ((int64_t)b * (a.T - 1) + q.acc) * a.K;
-  for (int l = tid; l < QMAX; l += blockDim.x) {
-    const bool live = !q.all && l < a.K;
-    sh.qid[l] = live ? load_index(a.q_ids, a.q_ids_i64, qi + l) : -1;
-    sh.qv[l] = live ? clamp01(a.q_values[qi + l]) : 0.f;
-    sh.qd[l] = 0.0;
-  }
-  __syncthreads();
-  for (int l = tid; l < QMAX; l += blockDim.x) {
-    bool last = sh.qid[l] >= 0 && sh.qid[l] < a.vocab;
-    for (int l2 = l + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != sh.qid[l];
-    sh.qlast[l] = last;
-  }
-  __syncthreads();
-}
-
-// ---------------------------------------------------------------------------------------
-// k_bonus: per-thread masses of each dense bonus row (one vector pass; chunks x requests)
-// ---------------------------------------------------------------------------------------
-template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(BCT) void k_bonus(KParams P) {
-  __shared__ BonusShared sh;
-  const dsv_verify_args& a = P.a;
-  const int b = blockIdx.y, c = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int64_t V = a.vocab;
-  const ReqView q = request_view(P, b, sh);
-  if (!q.rows_ok) return;
-  const int64_t rstar = q.row0 + q.acc;
-  const RowSum rs = P.rowsum[rstar];
-  if (rs.mode != M_UNF && rs.mode != M_HIST) return;  // support list: drawn by k_final
-  const bool hist_mode = rs.mode == M_HIST;
-  if (hist_mode && !q.all) stage_q(a, b, q, sh);
-  const bool pen = P.pbits != nullptr;
-  const float pres = pen && a.presence ? a.presence[b] : 0.f;
-  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
-  const float T = a.temperatures[b];
-  const char* rowp = row_ptr(a, rstar);
-  const int ept = P.ept;
-  const int64_t lo_t = (int64_t)c * P.bchunk + (int64_t)tid * ept;
-  const int64_t hi_t = lo_t + ept < V ? lo_t + ept : V;
-  const int cnt = hi_t > lo_t ? (int)(hi_t - lo_t) : 0;
-  float x[EPT_MAX];
-  load_range<DT, ALIGNED>(P, b, rowp, lo_t, hi_t, pres, rep, x);
-  double mgt = 0.0;
-  int32_t ties = 0;
-#pragma unroll
-  for (int i = 0; i < EPT_MAX; ++i) {
-    if (i < cnt) {
-      const uint32_t k = key_of<DT>(x[i]);
-      if (!hist_mode || k > rs.vcut)
-        mgt += dense_P(rs, T, x[i]);
-      else if (k == rs.vcut)
-        ++ties;
+    if (tid == 0) {
+      sh.acc = acc;
+      sh.bonus = P.rbonus[row0 + acc];
     }
   }
-  int32_t tie_tot = 0;
-  const int32_t tie_before = block_excl_scan<BCT / WAVE>(ties, sh.red_i, &tie_tot);
-  const double msum = block_sum<BCT / WAVE>(mgt, sh.red_d);
-  const int64_t slot = (int64_t)b * NCH * BCT + (int64_t)c * BCT + tid;
-  P.tmass[slot] = mgt;
-  P.tties[slot] = ties;
-  if (tid == 0) P.bchunks[(int64_t)b * NCH + c] = BonusChunk{msum, tie_tot, 0};
-  // chunk-relative tie rank of each q id that sits at the cut key in this thread's range
-  if (hist_mode && !q.all && ties)
-    for (int l = 0; l < a.K; ++l) {
-      const int64_t id = sh.qid[l];
-      if (id < lo_t || id >= hi_t) continue;
-      int32_t before = 0;
-      bool at_cut = false;
-#pragma unroll
-      for (int i = 0; i < EPT_MAX; ++i)
-        if (i < cnt && key_of<DT>(x[i]) == rs.vcut) {
-          if (lo_t + i < id) ++before;
-          if (lo_t + i == id) at_cut = true;
-        }
-      if (at_cut) P.qrank[(int64_t)b * QMAX + l] = tie_before + before;
+  __syncthreads();
+  const int acc = sh.acc;
+  int64_t bonus = sh.bonus;
+  if (bonus == BONUS_PLAN) {  // the row merge planned the draw: scan the chunk
+    const int64_t rstar = row0 + acc;
+    const RowSum rs = P.rowsum[rstar];
+    const bool resid = acc < cap - 1;
+    stage_q(a, b, acc, resid, sh);
+    const DrawPlan* pl = P.plans + rstar;
+    if (tid < QMAX) sh.qd[tid] = pl->qd[tid];
+    if (tid == 0) {
+      sh.thr = pl->thr;
+      sh.chunk_lo = pl->chunk_lo;
+      sh.chunk = pl->chunk;
+      sh.tieq = pl->tieq;
+      sh.use_r = pl->use_r;
     }
-}
-
-// ---------------------------------------------------------------------------------------
-// k_final: bonus draw and outputs, one workgroup per request
-// (sampling/sparse/accept.py:249-307 and :179-204; runtime/worker.py:1048-1089)
-// ---------------------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(BCT) void k_final(KParams P) {
-  __shared__ BonusShared sh;
-  const dsv_verify_args& a = P.a;
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-  const int64_t V = a.vocab;
-  const ReqView q = request_view(P, b, sh);
-  if (!q.rows_ok) {  // inconsistent row offsets: no row of this request can be read
-    write_outputs(a, b, 0, V - 1);
-    return;
-  }
-  const int acc = q.acc;
-  const bool all = q.all;
-  const int64_t rstar = q.row0 + acc;
-  const RowSum rs = P.rowsum[rstar];
-  const bool dense = rs.mode == M_UNF || rs.mode == M_HIST;
-  stage_q(a, b, q, sh);
-  const float uf = a.uniform_final[b];
-  const float T = a.temperatures[b];
-  const char* rowp = row_ptr(a, rstar);
-
-  if (!dense) {
-    // support list (GREEDY / LIST rows): lanes hold the entries, sorted by id
-    if (tid < WAVE) {
-      const bool live = lane < rs.nlist;
-      const ListEntry e = live ? P.lists[rstar * DSV_LIST_K + lane] : ListEntry{INT_MAX, 0.f};
-      const double Pi = (double)e.P;
-      double w = Pi;
-      if (!all && live)
-        for (int l = 0; l < a.K; ++l)
-          if (sh.qlast[l] && sh.qid[l] == (int64_t)e.id) w = fmax(Pi - (double)sh.qv[l], 0.0);
-      double lo, hi;
-      double mass = wave_tiles(w, lo, hi);
-      if (all || !(mass > 0.0)) mass = wave_tiles(Pi, lo, hi);
-      const double thr = (double)uf * mass;
-      const uint64_t hit = __ballot(live && lo <= thr && thr < hi);
-      int64_t bonus = V - 1;
-      if (hit) bonus = __shfl((int64_t)e.id, __ffsll((long long)hit) - 1, WAVE);
-      if (tid == 0) sh.bonus = bonus;
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, a.temperatures[b], sh);
+  } else if (bonus == BONUS_LATER) {
+    const int64_t rstar = row0 + acc;
+    const RowSum rs = P.rowsum[rstar];
+    const float T = a.temperatures[b];
+    const bool resid = acc < cap - 1;
+    stage_q(a, b, acc, resid, sh);
+    const char* rowp = row_ptr(a, rstar);
+    const bool pen = P.pbits != nullptr;
+    const float pres = pen && a.presence ? a.presence[b] : 0.f;
+    const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+    const BonusP bp = bonus_p<DT>(rs, T);
+    for (int c = 0; c < P.C; ++c) {  // chunk masses: a scan of every chunk
+      double m = 0.0;
+      int32_t t = 0;
+      for_span<DT, ALIGNED, FCT>(P, b, rowp, c, pres, rep, [&](int, float x) {
+        const uint32_t k = key_of<DT>(x);
+        if (rs.mode != M_HIST || k > rs.vcut)
+          m += (double)bp(x);
+        else if (k == rs.vcut)
+          ++t;
+      });
+      m = block_sum<FCT / WAVE>(m, sh.red_d);
+      t = block_sum<FCT / WAVE>(t, sh.red_i);
+      if (tid == 0) {
+        sh.cm[c] = m;
+        sh.ct[c] = t;
+      }
     }
     __syncthreads();
-    write_outputs(a, b, acc, sh.bonus);
-    return;
+    dense_plan<DT, ALIGNED, FCT>(P, b, rowp, rs, T, resid, a.uniform_final[b], sh);
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, sh);
+    (void)CHE;
   }
-
-  // ---- dense support: chunk masses from k_bonus ---------------------------------------------
-  const bool pen = P.pbits != nullptr;
-  const float pres = pen && a.presence ? a.presence[b] : 0.f;
-  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
-  const bool hist_mode = rs.mode == M_HIST;
-  const int ept = P.ept;
-  const int nch = P.nch;
-  const double P_cut = hist_mode ? dense_P(rs, T, value_of_key<DT>(rs.vcut)) : 0.0;
-  if (tid < WAVE) {
-    // lanes hold the chunks
-    BonusChunk bc = BonusChunk{0.0, 0, 0};
-    if (lane < nch) bc = P.bchunks[(int64_t)b * NCH + lane];
-    int32_t tie_prefix = bc.ties;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int32_t t = __shfl_up(tie_prefix, o, WAVE);
-      if (lane >= o) tie_prefix += t;
-    }
-    tie_prefix -= bc.ties;
-    // the residual's reduction at each q id (lanes hold the q lanes)
-    const bool qlive = !all && lane < a.K && sh.qlast[lane];
-    const int64_t qid = qlive ? sh.qid[lane] : 0;
-    const int32_t tp = __shfl(tie_prefix, (int)(qid / P.bchunk), WAVE);
-    if (qlive) {
-      float xq = load_elem<DT>(rowp, qid);
-      if (pen && pen_test(P, b, qid)) xq = penalize<DT>(xq, pres, rep);
-      const uint32_t k = key_of<DT>(xq);
-      const bool kept =
-          !hist_mode || k > rs.vcut ||
-          (k == rs.vcut && (int64_t)tp + P.qrank[(int64_t)b * QMAX + lane] < (int64_t)rs.ktie);
-      const double Pq = kept ? dense_P(rs, T, xq) : 0.0;
-      sh.qd[lane] = Pq - fmax(Pq - (double)sh.qv[lane], 0.0);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    int32_t kt = 0;
-    if (hist_mode) {
-      const int64_t room = (int64_t)rs.ktie - tie_prefix;
-      kt = room <= 0 ? 0 : (room < bc.ties ? (int32_t)room : bc.ties);
-    }
-    const double Mp = bc.mass + (kt > 0 ? (double)kt * P_cut : 0.0);
-    double Mr = Mp;
-    if (!all && lane < nch)
-      for (int l = 0; l < a.K; ++l)
-        if (sh.qlast[l] && sh.qid[l] / P.bchunk == lane) Mr -= sh.qd[l];
-    double lo_r, hi_r, lo_p, hi_p;
-    const double mr = wave_tiles(lane < nch ? Mr : 0.0, lo_r, hi_r);
-    const double mp = wave_tiles(lane < nch ? Mp : 0.0, lo_p, hi_p);
-    const bool use_r = !all && mr > 0.0;
-    const double thr = (double)uf * (use_r ? mr : mp);
-    const double clo = use_r ? lo_r : lo_p, chi = use_r ? hi_r : hi_p;
-    const uint64_t hit = __ballot(lane < nch && clo <= thr && thr < chi);
-    const int cstar = hit ? __ffsll((long long)hit) - 1 : -1;
-    if (tid == 0) {
-      sh.chunk = cstar;
-      sh.thr = thr;
-      sh.use_r = use_r ? 1 : 0;
-      sh.bonus = V - 1;
-      sh.pick_thread = -1;
-    }
-    if (cstar >= 0 && lane == cstar) {
-      sh.chunk_lo = clo;
-      sh.tieq = tie_prefix;
-    }
-  }
-  __syncthreads();
-  const int cstar = sh.chunk;
-  if (cstar < 0) {
-    write_outputs(a, b, acc, sh.bonus);
-    return;
-  }
-  // the thread of chunk cstar whose mass holds the threshold
-  const bool use_r = sh.use_r != 0;
-  const int64_t slot = (int64_t)b * NCH * BCT + (int64_t)cstar * BCT + tid;
-  const int32_t tt = P.tties[slot];
-  int32_t tie_tot = 0;
-  const int32_t tbefore = sh.tieq + block_excl_scan<BCT / WAVE>(tt, sh.red_i, &tie_tot);
-  int32_t kept_t = 0;
-  if (hist_mode) {
-    const int64_t room = (int64_t)rs.ktie - tbefore;
-    kept_t = room <= 0 ? 0 : (room < tt ? (int32_t)room : tt);
-  }
-  const int64_t lo_t = (int64_t)cstar * P.bchunk + (int64_t)tid * ept;
-  const int64_t hi_t = lo_t + ept < V ? lo_t + ept : V;
-  double w_t = P.tmass[slot] + (kept_t > 0 ? (double)kept_t * P_cut : 0.0);
-  if (use_r)
-    for (int l = 0; l < a.K; ++l)
-      if (sh.qlast[l] && sh.qid[l] >= lo_t && sh.qid[l] < hi_t) w_t -= sh.qd[l];
-  double tlo, thi;
-  block_tiles<BCT / WAVE>(w_t, sh.red_d, tlo, thi);
-  const double base = sh.chunk_lo, thr = sh.thr;
-  if (base + tlo <= thr && thr < base + thi) sh.pick_thread = tid;
-  __syncthreads();
-  int pt = sh.pick_thread;
-  if (pt < 0) {
-    // rounding left the threshold past this chunk's recomputed mass: the last thread with mass
-    const uint64_t lp = block_max_u64<BCT / WAVE>(w_t > 0.0 ? (uint64_t)tid + 1 : 0ull, sh.red_u);
-    pt = lp ? (int)lp - 1 : -1;
-  }
-  if (tid == pt) {
-    sh.tb_pick = tbefore;
-    sh.pick_lo = base + tlo;
-  }
-  __syncthreads();
-  if (pt >= 0 && tid < WAVE) {
-    // thread pt's elements in id order, one per lane: weights, then the running sum
-    const int64_t plo = (int64_t)cstar * P.bchunk + (int64_t)pt * ept;
-    const int64_t phi = plo + ept < V ? plo + ept : V;
-    const int64_t j = plo + lane;
-    const bool live = j < phi;
-    float xj = live ? load_elem<DT>(rowp, j) : -INFINITY;
-    if (live && pen && pen_test(P, b, j)) xj = penalize<DT>(xj, pres, rep);
-    const uint32_t k = key_of<DT>(xj);
-    const bool tie = live && hist_mode && k == rs.vcut;
-    const uint64_t tmask = __ballot(tie);
-    const int32_t seen = __popcll(tmask & ((1ull << lane) - 1ull));
-    double Pj = 0.0;
-    if (live) {
-      if (!hist_mode || k > rs.vcut)
-        Pj = dense_P(rs, T, xj);
-      else if (tie && (int64_t)sh.tb_pick + seen < (int64_t)rs.ktie)
-        Pj = P_cut;
-      if (use_r)
-        for (int l = 0; l < a.K; ++l)
-          if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
-    }
-    double wlo, whi;
-    wave_tiles(Pj, wlo, whi);
-    const double start = sh.pick_lo;
-    const uint64_t hit = __ballot(live && start + whi > thr);
-    const uint64_t pos = __ballot(live && Pj > 0.0);
-    int64_t pick = -1;
-    if (hit)
-      pick = plo + (__ffsll((long long)hit) - 1);
-    else if (pos)
-      pick = plo + (63 - __clzll((long long)pos));  // rounding: the last element with mass
-    if (lane == 0 && pick >= 0) sh.bonus = pick;
-  }
-  __syncthreads();
-  write_outputs(a, b, acc, sh.bonus);
+  write_outputs(a, b, acc, bonus);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1809,7 +1939,7 @@ using namespace dsv;
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, hpart, nhist, bchunks, qrank, tmass, tties, step_ok, pbits, total;
+  int64_t rowsum, lists, cstat, cand, hpart, nhist, rbonus, plans, step_ok, pbits, total;
 };
 static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
   if (dtype == DSV_BF16) {
@@ -1844,10 +1974,8 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.cand, rows * C * (int64_t)kcand * 8);
   take(w.hpart, kcand ? rows * C * (int64_t)(HWIN / 2) * 4 : 0);
   take(w.nhist, kcand ? (int64_t)NUC_GRID * 65536 * 4 : 0);
-  take(w.bchunks, (int64_t)bs * NCH * (int64_t)sizeof(BonusChunk));
-  take(w.qrank, (int64_t)bs * QMAX * 4);
-  take(w.tmass, (int64_t)bs * NCH * BCT * 8);
-  take(w.tties, (int64_t)bs * NCH * BCT * 4);
+  take(w.rbonus, rows * 8);
+  take(w.plans, rows * (int64_t)sizeof(DrawPlan));
   take(w.step_ok, rows * 4);
   take(w.pbits, history ? (int64_t)bs * pen_words(vocab) * 4 : 0);
   w.total = o;
@@ -1923,18 +2051,11 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.cand = reinterpret_cast<uint64_t*>(ws + w.cand);
   P.hpart = reinterpret_cast<uint32_t*>(ws + w.hpart);
   P.nhist = reinterpret_cast<uint32_t*>(ws + w.nhist);
-  P.bchunks = reinterpret_cast<BonusChunk*>(ws + w.bchunks);
-  P.qrank = reinterpret_cast<int32_t*>(ws + w.qrank);
-  P.tmass = reinterpret_cast<double*>(ws + w.tmass);
-  P.tties = reinterpret_cast<int32_t*>(ws + w.tties);
+  P.rbonus = reinterpret_cast<int64_t*>(ws + w.rbonus);
+  P.plans = reinterpret_cast<DrawPlan*>(ws + w.plans);
   P.step_ok = reinterpret_cast<int32_t*>(ws + w.step_ok);
   P.pbits = history ? reinterpret_cast<uint32_t*>(ws + w.pbits) : nullptr;
   P.pwords = pen_words(a.vocab);
-  int64_t ept = align_up((a.vocab + (int64_t)NCH * BCT - 1) / ((int64_t)NCH * BCT), 8);
-  if (ept > EPT_MAX) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab %lld is too large", (long long)a.vocab);
-  P.ept = (int32_t)ept;
-  P.bchunk = (int64_t)BCT * ept;
-  P.nch = (int32_t)((a.vocab + P.bchunk - 1) / P.bchunk);
   P.C = C;
   P.kcand = DSV_LIST_K;
   P.aligned = ((uintptr_t)a.logits % 16 == 0) && ((a.row_stride * (int64_t)esize) % 16 == 0) &&
@@ -1956,10 +2077,17 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
     launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * C), stream);
     if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_stop, stream) != hipSuccess)
       DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling stop event");
-    if (a.logits_dtype == DSV_BF16)
-      hipLaunchKernelGGL(k_merge<DSV_BF16>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-    else
-      hipLaunchKernelGGL(k_merge<DSV_F32>, dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+    if (a.logits_dtype == DSV_BF16) {
+      if (P.aligned)
+        hipLaunchKernelGGL((k_merge<DSV_BF16, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+      else
+        hipLaunchKernelGGL((k_merge<DSV_BF16, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+    } else {
+      if (P.aligned)
+        hipLaunchKernelGGL((k_merge<DSV_F32, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+      else
+        hipLaunchKernelGGL((k_merge<DSV_F32, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+    }
     DSV_CHECK_LAUNCH("k_chunk / k_merge");
     if (hist_possible) {  // nucleus rows whose chunk windows fall short of the row floor
       const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
@@ -1975,26 +2103,18 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
       DSV_CHECK_LAUNCH("k_nuc");
     }
   }
-  if (stages & 2) {
-    const dim3 grid(P.nch, a.bs);
+  if (stages & 4) {
     if (a.logits_dtype == DSV_BF16) {
       if (P.aligned)
-        hipLaunchKernelGGL((k_bonus<DSV_BF16, true>), grid, dim3(BCT), 0, stream, P);
+        hipLaunchKernelGGL((k_final<DSV_BF16, true>), dim3(a.bs), dim3(FCT), 0, stream, P);
       else
-        hipLaunchKernelGGL((k_bonus<DSV_BF16, false>), grid, dim3(BCT), 0, stream, P);
+        hipLaunchKernelGGL((k_final<DSV_BF16, false>), dim3(a.bs), dim3(FCT), 0, stream, P);
     } else {
       if (P.aligned)
-        hipLaunchKernelGGL((k_bonus<DSV_F32, true>), grid, dim3(BCT), 0, stream, P);
+        hipLaunchKernelGGL((k_final<DSV_F32, true>), dim3(a.bs), dim3(FCT), 0, stream, P);
       else
-        hipLaunchKernelGGL((k_bonus<DSV_F32, false>), grid, dim3(BCT), 0, stream, P);
+        hipLaunchKernelGGL((k_final<DSV_F32, false>), dim3(a.bs), dim3(FCT), 0, stream, P);
     }
-    DSV_CHECK_LAUNCH("k_bonus");
-  }
-  if (stages & 4) {
-    if (a.logits_dtype == DSV_BF16)
-      hipLaunchKernelGGL(k_final<DSV_BF16>, dim3(a.bs), dim3(BCT), 0, stream, P);
-    else
-      hipLaunchKernelGGL(k_final<DSV_F32>, dim3(a.bs), dim3(BCT), 0, stream, P);
     DSV_CHECK_LAUNCH("k_final");
   }
   return DSV_OK;
