@@ -23,8 +23,11 @@ LIST_K = 64
 EXPORTS = (
     "dsv_last_error", "dsv_device_count", "dsv_verify_workspace_bytes", "dsv_verify",
     "dsv_greedy_verify", "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_topk_workspace_bytes",
-    "dsv_uniforms", "dsv_profile_events",
+    "dsv_uniforms", "dsv_profile_events", "dsv_adjust_logits", "dsv_adjust_history",
+    "dsv_logits_padding", "dsv_window_index", "dsv_target_probs", "dsv_compress",
+    "dsv_accept_chain", "dsv_sample_chain", "dsv_pack_joint",
 )
+DSV_ADJ_ADD, DSV_ADJ_SCALE = 0, 1
 
 _c = ctypes
 vp, i32, i64 = _c.c_void_p, _c.c_int32, _c.c_int64
@@ -48,6 +51,24 @@ class VerifyArgs(ctypes.Structure):
         ("accept", vp), ("commit", vp), ("bonus", vp), ("output", vp), ("new_seq", vp),
         ("kv_slots", vp),
         ("workspace", vp), ("workspace_bytes", i64),
+    ]
+
+
+class ChainArgs(ctypes.Structure):
+    """Mirror of ``dsv_chain_args``."""
+
+    _fields_ = [
+        ("bs", i32), ("T", i32), ("K", i32), ("pad0", i32),
+        ("vocab", i64),
+        ("candidates", vp), ("verify_lens", vp), ("uniforms", vp), ("uniform_final", vp),
+        ("prefix_lens", vp),
+        ("row_offsets", vp), ("row_offsets_i64", i32), ("pad1", i32),
+        ("dense_p", vp), ("p_stride", i64), ("denominator", vp),
+        ("p_ids", vp), ("p_values", vp), ("p_lengths", vp), ("p_overflow", vp),
+        ("p_cap", i32), ("pad2", i32),
+        ("dense_q", vp), ("q_stride", i64),
+        ("q_ids", vp), ("q_ids_i64", i32), ("pad3", i32), ("q_values", vp),
+        ("accept", vp), ("commit", vp), ("bonus", vp), ("output", vp), ("new_seq", vp),
     ]
 
 
@@ -91,6 +112,24 @@ def load():
         lib.dsv_uniforms.argtypes = [vp, vp, i32, i64, i32, i32, vp, vp]
         lib.dsv_profile_events.restype = i32
         lib.dsv_profile_events.argtypes = [vp, vp]
+        lib.dsv_adjust_logits.restype = i32
+        lib.dsv_adjust_logits.argtypes = [vp, i32, i64, i64, i64, vp, i32, i64, i32, vp, i64, vp]
+        lib.dsv_adjust_history.restype = i32
+        lib.dsv_adjust_history.argtypes = [vp, i32, i64, i64, i64, vp, i32, i64, vp, i32, vp, vp, vp]
+        lib.dsv_logits_padding.restype = i32
+        lib.dsv_logits_padding.argtypes = [vp, i32, i64, i64, i64, vp]
+        lib.dsv_window_index.restype = i32
+        lib.dsv_window_index.argtypes = [vp, i32, i32, i32, vp, i64, vp]
+        lib.dsv_target_probs.restype = i32
+        lib.dsv_target_probs.argtypes = [ctypes.POINTER(VerifyArgs), vp, i64, i32, vp]
+        lib.dsv_compress.restype = i32
+        lib.dsv_compress.argtypes = [vp, i64, i64, i64, i32, vp, vp, vp, vp, vp]
+        lib.dsv_accept_chain.restype = i32
+        lib.dsv_accept_chain.argtypes = [ctypes.POINTER(ChainArgs), vp]
+        lib.dsv_pack_joint.restype = i32
+        lib.dsv_pack_joint.argtypes = [vp, vp, i64, i32, vp, vp, i32, vp, vp, vp, vp, vp, i64, i64, vp]
+        lib.dsv_sample_chain.restype = i32
+        lib.dsv_sample_chain.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         _lib = lib
     return _lib
 

@@ -37,6 +37,7 @@ struct KParams {
   ChunkStat* cstat;       // [rows, C]
   uint64_t* cand;         // [rows, C, kcand]
   int64_t* rbonus;        // [rows]: the bonus token each row gives as the accepted length
+  int32_t* rties;         // [rows, NCHK]: nucleus rows' chunk counts of values at the cut key
   struct DrawPlan* plans; // [rows]: dense rows' planned bonus draw
   int32_t* step_ok;       // [rows]: 1 when the draft token verified by the row is accepted
   uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
@@ -48,7 +49,7 @@ struct KParams {
   int32_t aligned;        // logits rows are 16-byte aligned
   int32_t force_greedy;   // greedy-verify entry: every row is GREEDY
   int32_t softmax;        // chunk pass computes softmax partial sums (the verify entry)
-  int32_t pad;
+  int32_t raw_p;          // dense target writer: the filtered p, not renormalised
 };
 
 __device__ __forceinline__ const char* row_ptr(const dsv_verify_args& a, int64_t r) {
@@ -58,6 +59,7 @@ __device__ __forceinline__ const char* row_ptr(const dsv_verify_args& a, int64_t
 
 // The draft token verified by row (b, s), or -1 when the row verifies no step.
 __device__ __forceinline__ int64_t step_token(const dsv_verify_args& a, int b, int s) {
+  if (!a.candidates) return -1;  // target-distribution entry: no drafts
   const int cap = req_cap(a, b);
   return (s < cap - 1 && s + 1 < a.T) ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
 }
@@ -279,7 +281,6 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-  const int64_t V = a.vocab;
   const int C = P.C;
   const bool pen = P.pbits != nullptr;
   const float pres = pen && a.presence ? a.presence[b] : 0.f;
@@ -920,6 +921,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     if (lane == 0) {
       ds.cm[c] = mc;
       ds.ct[c] = tc;
+      P.rties[r * NCHK + c] = tc;
     }
   }
   const float xt = sh.xtok;
@@ -1688,6 +1690,7 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
   } else {
     merge_row<DT>(P, r, b, s, mode, T, ms, ds, &srs);
   }
+  if (!a.candidates) return;  // target-distribution entry: no draw
   __syncthreads();
   // the bonus token this row gives when it is the request's accepted length (k_final picks it)
   const RowSum rs = srs;
@@ -1849,6 +1852,120 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
 }
 
 // ---------------------------------------------------------------------------------------
+// k_dense_p: the target distribution written out densely (runtime/worker.py:440-508), one
+// workgroup per (row, chunk), each thread a span of consecutive ids.
+// ---------------------------------------------------------------------------------------
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
+  constexpr int CHE = Elems<DT>::chunk, FE = CV * Elems<DT>::n;
+  constexpr int NW = CT / WAVE;
+  __shared__ int32_t red_i[NW];
+  __shared__ ListEntry lst[DSV_LIST_K];
+  __shared__ int32_t s_before;
+  const dsv_verify_args& a = P.a;
+  const int C = P.C;
+  const int64_t r = blockIdx.x / C;
+  const int c = (int)(blockIdx.x - r * C);
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  const int64_t jlo = (int64_t)c * CHE + (int64_t)tid * FE;
+  float* orow = out + r * out_stride;
+  int b = 0, s = 0;
+  const bool live_row = row_request(a, r, b, s);
+  const RowSum rs = P.rowsum[r];
+  const int mode = live_row ? rs.mode : M_SKIP;
+  // the span's values, four at a time
+  float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto put = [&](int i, float v) {
+    const int k = i & 3;
+    if (k == 0) acc4.x = v; else if (k == 1) acc4.y = v; else if (k == 2) acc4.z = v; else acc4.w = v;
+    if (k == 3) {
+      const int64_t j = jlo + i - 3;
+      if (j + 3 < V) {
+        *reinterpret_cast<float4*>(orow + j) = acc4;
+      } else {
+        if (j < V) orow[j] = acc4.x;
+        if (j + 1 < V) orow[j + 1] = acc4.y;
+        if (j + 2 < V) orow[j + 2] = acc4.z;
+      }
+    }
+  };
+  const bool vec_ok = (out_stride % 4 == 0) && ((uintptr_t)out % 16 == 0);
+  auto put1 = [&](int i, float v) {  // unaligned output: element stores
+    const int64_t j = jlo + i;
+    if (j < V) orow[j] = v;
+  };
+  if (mode == M_SKIP || mode == M_GREEDY || mode == M_LIST) {
+    int n = 0;
+    if (mode == M_LIST) {
+      n = rs.nlist;
+      for (int i = tid; i < n; i += CT) lst[i] = P.lists[r * DSV_LIST_K + i];
+      __syncthreads();
+    }
+    for (int i = 0; i < FE; ++i) {
+      const int64_t j = jlo + i;
+      float v = 0.f;
+      if (mode == M_GREEDY)
+        v = j == (int64_t)rs.argmax ? 1.f : 0.f;
+      else if (mode == M_LIST)
+        for (int e = 0; e < n; ++e)
+          if ((int64_t)lst[e].id == j) {
+            v = lst[e].P;
+            if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
+              float x = load_elem<DT>(row_ptr(a, r), j);
+              if (P.pbits && pen_test(P, b, j))
+                x = penalize<DT>(x, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
+              v = prob_of(x, a.temperatures[b], rs.m_f, rs.invZ);
+            }
+          }
+      if (vec_ok) put(i, v); else put1(i, v);
+    }
+    return;
+  }
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const float T = a.temperatures[b];
+  const char* rowp = row_ptr(a, r);
+  const bool hist = mode == M_HIST;
+  int32_t tbefore = 0;
+  if (hist && rs.ktie > 0 && rs.ktie != INT_MAX) {
+    // the cut key's values before this thread's span, in id order
+    int32_t t = 0;
+    for_span<DT, ALIGNED, CT>(P, b, rowp, c, pres, rep, [&](int, float x) { t += key_of<DT>(x) == rs.vcut; });
+    int32_t tot = 0;
+    tbefore = block_excl_scan<NW>(t, red_i, &tot);
+    if (tid == 0) {
+      int32_t before = 0;
+      if (!(rs.flags & FLAG_FULL_HIST)) {
+        for (int c2 = 0; c2 < c; ++c2) before += P.rties[r * NCHK + c2];
+      } else {
+        s_before = 0;
+      }
+      if (!(rs.flags & FLAG_FULL_HIST)) s_before = before;
+    }
+    if (rs.flags & FLAG_FULL_HIST) {  // (rare) the earlier chunks' counts by scanning them
+      int32_t e = 0;
+      for (int c2 = 0; c2 < c; ++c2)
+        for_span<DT, ALIGNED, CT>(P, b, rowp, c2, pres, rep, [&](int, float x) { e += key_of<DT>(x) == rs.vcut; });
+      e = block_sum<NW>(e, red_i);
+      if (tid == 0) s_before = e;
+    }
+    __syncthreads();
+    tbefore += s_before;
+  }
+  int32_t seen = 0;
+  for_span<DT, ALIGNED, CT>(P, b, rowp, c, pres, rep, [&](int i, float x) {
+    float v = 0.f;
+    const uint32_t k = key_of<DT>(x);
+    const bool kept = !hist || k > rs.vcut || (k == rs.vcut && (int64_t)tbefore + seen < (int64_t)rs.ktie);
+    if (kept) v = P.raw_p ? prob_of(x, T, rs.m_f, rs.invZ) : (float)dense_P(rs, T, x);
+    seen += hist && k == rs.vcut;
+    if (vec_ok) put(i, v); else put1(i, v);
+  });
+}
+
+// ---------------------------------------------------------------------------------------
 // Greedy verify (verification/caps.py:32-59, verification/ragged.py:51-76)
 // ---------------------------------------------------------------------------------------
 __device__ inline int64_t chunk_argmax(const ChunkStat* cs, int C) {
@@ -1939,7 +2056,7 @@ using namespace dsv;
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, hpart, nhist, rbonus, plans, step_ok, pbits, total;
+  int64_t rowsum, lists, cstat, cand, hpart, nhist, rbonus, rties, plans, step_ok, pbits, total;
 };
 static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
   if (dtype == DSV_BF16) {
@@ -1975,6 +2092,7 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.hpart, kcand ? rows * C * (int64_t)(HWIN / 2) * 4 : 0);
   take(w.nhist, kcand ? (int64_t)NUC_GRID * 65536 * 4 : 0);
   take(w.rbonus, rows * 8);
+  take(w.rties, rows * NCHK * 4);
   take(w.plans, rows * (int64_t)sizeof(DrawPlan));
   take(w.step_ok, rows * 4);
   take(w.pbits, history ? (int64_t)bs * pen_words(vocab) * 4 : 0);
@@ -2000,47 +2118,49 @@ extern "C" int dsv_profile_events(void* start, void* stop) {
   return DSV_OK;
 }
 
-extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: null arguments");
-  const dsv_verify_args& a = *args;
+// Validation and kernel parameters shared by the verify step and the target-distribution
+// entry (drafts = false: candidates, q, uniforms and outputs may be absent).
+static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* what, KParams& P, bool& hist_possible) {
   if (a.logits_dtype != DSV_BF16 && a.logits_dtype != DSV_F32)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: logits must be float32 or bfloat16");
+    DSV_FAIL(DSV_ERR_INVALID, "%s: logits must be float32 or bfloat16", what);
   if (a.bs <= 0 || a.T < 1 || a.vocab < 1 || a.rows < 0 || a.row_stride < a.vocab)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: invalid shape (bs %d, T %d, vocab %lld, rows %lld)", a.bs, a.T,
+    DSV_FAIL(DSV_ERR_INVALID, "%s: invalid shape (bs %d, T %d, vocab %lld, rows %lld)", what, a.bs, a.T,
              (long long)a.vocab, (long long)a.rows);
   if (a.vocab >= (1ll << 31) || a.rows >= (1ll << 31))
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: vocab and rows must be < 2^31");
-  if (a.bs > 65535) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: at most 65535 requests per call");
+    DSV_FAIL(DSV_ERR_INVALID, "%s: vocab and rows must be < 2^31", what);
+  if (a.bs > 65535) DSV_FAIL(DSV_ERR_INVALID, "%s: at most 65535 requests per call", what);
   if (!a.row_offsets && a.rows != (int64_t)a.bs * a.T)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: dense layout needs rows == bs*T (%lld != %d*%d)", (long long)a.rows,
-             a.bs, a.T);
-  if (!a.logits || !a.temperatures || !a.top_ks || !a.top_ps || !a.candidates || !a.q_ids || !a.q_values ||
-      !a.uniforms || !a.uniform_final || !a.prefix_lens || !a.accept || !a.commit || !a.bonus || !a.output ||
-      !a.new_seq || !a.workspace)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: required pointer is null");
-  if (a.K < 1 || a.K > QMAX) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: q width K=%d outside [1, %d]", a.K, QMAX);
-  if (a.hist_ids && a.hist_len < 0) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: negative hist_len");
-  if (a.kv_slots && a.page_table && a.page_cols < 1) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: empty page table");
+    DSV_FAIL(DSV_ERR_INVALID, "%s: dense layout needs rows == bs*T (%lld != %d*%d)", what, (long long)a.rows, a.bs,
+             a.T);
+  if (!a.logits || !a.temperatures || !a.top_ks || (a.filter && !a.top_ps) || !a.workspace)
+    DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
+  if (drafts) {
+    if (!a.top_ps || !a.candidates || !a.q_ids || !a.q_values || !a.uniforms || !a.uniform_final || !a.prefix_lens ||
+        !a.accept || !a.commit || !a.bonus || !a.output || !a.new_seq)
+      DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
+    if (a.K < 1 || a.K > QMAX) DSV_FAIL(DSV_ERR_INVALID, "%s: q width K=%d outside [1, %d]", what, a.K, QMAX);
+  }
+  if (a.hist_ids && a.hist_len < 0) DSV_FAIL(DSV_ERR_INVALID, "%s: negative hist_len", what);
+  if (a.kv_slots && a.page_table && a.page_cols < 1) DSV_FAIL(DSV_ERR_INVALID, "%s: empty page table", what);
   if (a.backend != DSV_BACKEND_PYTORCH && a.backend != DSV_BACKEND_FLASHINFER)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: unknown backend %d", a.backend);
-  const bool hist_possible = a.filter && a.max_top_k > DSV_LIST_K;
+    DSV_FAIL(DSV_ERR_INVALID, "%s: unknown backend %d", what, a.backend);
+  hist_possible = a.filter && a.max_top_k > DSV_LIST_K;
   if (hist_possible && a.logits_dtype != DSV_BF16)
     DSV_FAIL(DSV_ERR_UNSUPPORTED,
-             "dsv_verify: float32 logits with top_k > %d and a top-p / min-p cut are not implemented; use bfloat16",
+             "%s: float32 logits with top_k > %d and a top-p / min-p cut are not implemented; use bfloat16", what,
              DSV_LIST_K);
   if (hist_possible && a.backend == DSV_BACKEND_FLASHINFER && a.need_min_p)
-    DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: flashinfer min-p branch with top_k > %d is not implemented",
-             DSV_LIST_K);
+    DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: flashinfer min-p branch with top_k > %d is not implemented", what, DSV_LIST_K);
   const int C = chunks_per_row(a.vocab, a.logits_dtype);
-  if (C > 16) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab %lld needs %d chunks (> 16)", (long long)a.vocab, C);
+  if (C > 16) DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab %lld needs %d chunks (> 16)", what, (long long)a.vocab, C);
   const bool history = a.hist_ids && a.hist_len > 0;
   const WsLayout w = ws_layout(a.rows, a.bs, a.vocab, a.logits_dtype, DSV_LIST_K, history);
   if (a.workspace_bytes < w.total)
-    DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_verify: workspace %lld < %lld bytes", (long long)a.workspace_bytes,
+    DSV_FAIL(DSV_ERR_WORKSPACE, "%s: workspace %lld < %lld bytes", what, (long long)a.workspace_bytes,
              (long long)w.total);
+  if (history && (size_t)pen_words(a.vocab) * 4 > 64 * 1024)
+    DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab too large for the history bitmap", what);
   const size_t esize = a.logits_dtype == DSV_BF16 ? 2 : 4;
-  KParams P;
   memset(&P, 0, sizeof(P));
   P.a = a;
   if (!history) P.a.hist_ids = nullptr;
@@ -2052,6 +2172,7 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.hpart = reinterpret_cast<uint32_t*>(ws + w.hpart);
   P.nhist = reinterpret_cast<uint32_t*>(ws + w.nhist);
   P.rbonus = reinterpret_cast<int64_t*>(ws + w.rbonus);
+  P.rties = reinterpret_cast<int32_t*>(ws + w.rties);
   P.plans = reinterpret_cast<DrawPlan*>(ws + w.plans);
   P.step_ok = reinterpret_cast<int32_t*>(ws + w.step_ok);
   P.pbits = history ? reinterpret_cast<uint32_t*>(ws + w.pbits) : nullptr;
@@ -2061,47 +2182,65 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   P.aligned = ((uintptr_t)a.logits % 16 == 0) && ((a.row_stride * (int64_t)esize) % 16 == 0) &&
               a.vocab * (int64_t)esize >= 16;
   P.softmax = 1;
+  return DSV_OK;
+}
+
+// The row stage: history bitmaps, the chunk pass, the row merge, and the full-histogram rows.
+static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipStream_t stream) {
+  const dsv_verify_args& a = P.a;
+  if (P.pbits) {
+    const size_t prep_lds = (size_t)P.pwords * 4;
+    (void)hipFuncSetAttribute((const void*)k_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)prep_lds);
+    hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
+    DSV_CHECK_LAUNCH("k_prep");
+  }
+  if (profile && g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling start event");
+  launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * P.C), stream);
+  if (profile && g_prof_start && g_prof_stop && hipEventRecord(g_prof_stop, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling stop event");
+  if (a.logits_dtype == DSV_BF16) {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_merge<DSV_BF16, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+    else
+      hipLaunchKernelGGL((k_merge<DSV_BF16, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+  } else {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_merge<DSV_F32, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+    else
+      hipLaunchKernelGGL((k_merge<DSV_F32, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
+  }
+  DSV_CHECK_LAUNCH("k_chunk / k_merge");
+  if (hist_possible) {  // nucleus rows whose chunk windows fall short of the row floor
+    const size_t nuc_lds = (size_t)HIST_WORDS * 4;
+    const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
+    if (P.aligned) {
+      (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)nuc_lds);
+      hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+    } else {
+      (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)nuc_lds);
+      hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+    }
+    DSV_CHECK_LAUNCH("k_nuc");
+  }
+  return DSV_OK;
+}
+
+extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_verify: null arguments");
+  const dsv_verify_args& a = *args;
+  KParams P;
+  bool hist_possible = false;
+  const int rc = verify_prepare(a, true, "dsv_verify", P, hist_possible);
+  if (rc != DSV_OK) return rc;
   if (a.rows == 0) return DSV_OK;
   const int stages = a.stages ? a.stages : 7;
-  const size_t prep_lds = history ? (size_t)P.pwords * 4 : 0;
-  const size_t nuc_lds = (size_t)HIST_WORDS * 4;
-  if (prep_lds > 64 * 1024) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_verify: vocab too large for the history bitmap");
   if (stages & 1) {
-    if (history) {
-      (void)hipFuncSetAttribute((const void*)k_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)prep_lds);
-      hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
-      DSV_CHECK_LAUNCH("k_prep");
-    }
-    if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
-      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling start event");
-    launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * C), stream);
-    if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_stop, stream) != hipSuccess)
-      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling stop event");
-    if (a.logits_dtype == DSV_BF16) {
-      if (P.aligned)
-        hipLaunchKernelGGL((k_merge<DSV_BF16, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-      else
-        hipLaunchKernelGGL((k_merge<DSV_BF16, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-    } else {
-      if (P.aligned)
-        hipLaunchKernelGGL((k_merge<DSV_F32, true>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-      else
-        hipLaunchKernelGGL((k_merge<DSV_F32, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
-    }
-    DSV_CHECK_LAUNCH("k_chunk / k_merge");
-    if (hist_possible) {  // nucleus rows whose chunk windows fall short of the row floor
-      const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
-      if (P.aligned) {
-        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)nuc_lds);
-        hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
-      } else {
-        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)nuc_lds);
-        hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
-      }
-      DSV_CHECK_LAUNCH("k_nuc");
-    }
+    const int rc2 = launch_rows(P, hist_possible, true, stream);
+    if (rc2 != DSV_OK) return rc2;
   }
   if (stages & 4) {
     if (a.logits_dtype == DSV_BF16) {
@@ -2117,6 +2256,37 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
     }
     DSV_CHECK_LAUNCH("k_final");
   }
+  return DSV_OK;
+}
+
+extern "C" int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t out_stride, int32_t normalize,
+                                dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: null arguments");
+  dsv_verify_args a = *args;
+  a.candidates = nullptr;  // no drafts: no accept decisions, no bonus draw
+  if (!out || out_stride < a.vocab) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: output [rows, vocab] required");
+  KParams P;
+  bool hist_possible = false;
+  const int rc = verify_prepare(a, false, "dsv_target_probs", P, hist_possible);
+  if (rc != DSV_OK) return rc;
+  P.raw_p = normalize ? 0 : 1;
+  if (a.rows == 0) return DSV_OK;
+  const int rc2 = launch_rows(P, hist_possible, false, stream);
+  if (rc2 != DSV_OK) return rc2;
+  const dim3 grid((unsigned)(a.rows * P.C));
+  if (a.logits_dtype == DSV_BF16) {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_dense_p<DSV_BF16, true>), grid, dim3(CT), 0, stream, P, out, out_stride);
+    else
+      hipLaunchKernelGGL((k_dense_p<DSV_BF16, false>), grid, dim3(CT), 0, stream, P, out, out_stride);
+  } else {
+    if (P.aligned)
+      hipLaunchKernelGGL((k_dense_p<DSV_F32, true>), grid, dim3(CT), 0, stream, P, out, out_stride);
+    else
+      hipLaunchKernelGGL((k_dense_p<DSV_F32, false>), grid, dim3(CT), 0, stream, P, out, out_stride);
+  }
+  DSV_CHECK_LAUNCH("k_dense_p");
   return DSV_OK;
 }
 

@@ -69,3 +69,55 @@ def topk_ids(logits: torch.Tensor, k: int, out: torch.Tensor = None) -> torch.Te
                             logits.stride(0), k, None, out.data_ptr(), 1,
                             ws.data_ptr(), ws.numel(), _lib.stream_of(logits.device)), "dsv_topk")
     return out
+
+
+def serial_sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, greedy_tok, out_tok, out_q,
+                        block_size: int, *, confidence_out=None):
+    """Sample every request's draft chain over its K candidate lanes (kernels/dspine.py:677-772);
+    fills out_tok[:n] / out_q[:n] in place and returns (out_tok, out_q).
+
+    table float32 [n, K, K] (n = bs*(block_size-1)); inv_temp float32 [>=bs]; top_k int32
+    [>=bs] (>= 1; >= K disables it); top_p float32 [>=bs] in (0, 1]; min_p float32 [>=bs] in
+    [0, 1]; greedy int32 [>=bs]; u float32 [>=n] in [0, 1); cand int64 [n, K]; greedy_tok int64
+    [>=n]; out_tok int64 [>=n]; out_q float32 [>=n, K].  Row i of request b reads row ``sender``
+    of its table (the lane drawn at row i-1, lane 0 first): p = softmax(table * inv_t); keep
+    rank < top_k, mass ahead <= top_p, p >= min_p * max p (ties: lower lane first);
+    q = w / sum w; the drawn lane is #(cdf <= u * total) clamped to the last kept lane.  Greedy
+    requests emit greedy_tok with a one-hot q.  ``confidence_out`` float32 [>=n] receives max p
+    (before filtering) of each row of a non-greedy request; other entries are left as they are.
+    One wavefront per request walks its chain; K <= 64."""
+    t = int(block_size)
+    n, k = cand.shape
+    if t < 2 or n % (t - 1) or tuple(table.shape) != (n, k, k) or not table.is_contiguous():
+        raise ValueError("serial_sample_chain table layout mismatch")
+    bs = n // (t - 1)
+    staged = (inv_temp, top_k, top_p, min_p, greedy)
+    if any(x.numel() < bs for x in staged) or u.numel() < n or greedy_tok.numel() < n:
+        raise ValueError("serial_sample_chain staging buffers too small")
+    if out_tok.numel() < n or out_q.shape[0] < n or out_q.shape[1] != k:
+        raise ValueError("serial_sample_chain output buffers too small")
+    if not (cand.is_contiguous() and out_q.is_contiguous()):
+        raise ValueError("serial_sample_chain expects contiguous candidates and q")
+    if confidence_out is not None and (confidence_out.dtype != torch.float32 or confidence_out.numel() < n
+                                       or not confidence_out.is_contiguous()
+                                       or confidence_out.device != table.device):
+        raise ValueError("serial_sample_chain confidence needs contiguous float32 storage on the table device")
+    dtypes = (table.dtype, inv_temp.dtype, top_k.dtype, top_p.dtype, min_p.dtype, greedy.dtype, u.dtype,
+              cand.dtype, greedy_tok.dtype, out_tok.dtype, out_q.dtype)
+    expected = (torch.float32, torch.float32, torch.int32, torch.float32, torch.float32, torch.int32,
+                torch.float32, torch.int64, torch.int64, torch.int64, torch.float32)
+    if dtypes != expected:
+        raise ValueError(f"serial_sample_chain dtype contract violated: {dtypes}")
+    if k > 64:
+        raise ValueError("serial_sample_chain supports at most 64 candidate lanes")
+    staged_c = [x.contiguous() for x in (inv_temp, top_k, top_p, min_p, greedy, u, greedy_tok)]
+    if not out_tok.is_contiguous():
+        raise ValueError("serial_sample_chain expects contiguous out_tok")
+    if bs:
+        dev = _lib.require_cuda(table, cand, out_tok, out_q, confidence_out, *staged_c)
+        it, tk, tp, mp, gr, uu, gt = staged_c
+        _lib.check(_lib.load().dsv_sample_chain(
+            table.data_ptr(), n, k, t, it.data_ptr(), tk.data_ptr(), tp.data_ptr(), mp.data_ptr(), gr.data_ptr(),
+            uu.data_ptr(), cand.data_ptr(), gt.data_ptr(), out_tok.data_ptr(), out_q.data_ptr(),
+            _lib.ptr(confidence_out), _lib.stream_of(dev)), "dsv_sample_chain")
+    return (out_tok, out_q)

@@ -1,0 +1,246 @@
+"""The verify-side runtime of the DSpine worker (runtime/worker.py of the reference, the parts
+on the draft-verification path).
+
+Target distributions come from the HIP row kernels (``dsv_target_probs``); chain rejection on
+an explicit target runs ``dsv_accept_chain`` with the draft's sparse q lanes, so the
+reference's dense-q scatter (and its [bs, T-1, V] buffer traffic) does not exist here; the
+sampled-verify seam routes to the fused single-pass verify (``dsv_verify``) through
+``TargetDistribution.sample_prefix``.  The SGLang scheduler integration around these
+functions (model forward, KV pools, plugin hooks) is not part of this package: the worker
+below holds only the state the verify path reads.
+"""
+
+from __future__ import annotations
+
+import threading
+from types import SimpleNamespace
+
+import torch
+
+from dspine_amd import _lib
+from dspine_amd.sampling.random import verification_uniforms
+from dspine_amd.sampling.sparse.accept import fill_chain_args, fill_sparse_q
+from dspine_amd.verify import Workspace, target_probs
+
+_active_worker = None
+
+
+class SoftmaxTemp:
+    """softmax(logits.float() / temperature) per row, the temperature of row r being that of
+    request r // rows_per_request (SGLang's SoftmaxTemp, called at runtime/worker.py:455-459)."""
+
+    @staticmethod
+    def execute(*, logits, temperatures, rows_per_request=1):
+        rows = logits.shape[0]
+        t = int(rows_per_request)
+        if t < 1 or rows % t:
+            raise ValueError("rows must be whole requests of rows_per_request rows")
+        info = SimpleNamespace(temperatures=temperatures, top_ks=_full_i32(rows // t, logits.device),
+                               top_ps=torch.ones(rows // t, device=logits.device))
+        return target_probs(logits, info, bs=rows // t, T=t)
+
+
+def _full_i32(n, device):
+    return torch.full((n,), 1 << 30, device=device, dtype=torch.int32)
+
+
+def build_dspine_target_probs(*, next_token_logits, sampling_info, block_size: int, bs: int,
+                              sampling_backend: str) -> torch.Tensor:
+    """[bs, T, V] float32 (runtime/worker.py:440-470): softmax(logits / temperature), the
+    configured backend's top-k / top-p / min-p filter, renormalised; rows of requests with
+    top_k <= 1 one-hot at argmax(logits) (lowest id) when ``is_any_greedy``; a batch with no
+    filter flag is the plain softmax."""
+    t = int(block_size)
+    probs = target_probs(next_token_logits, sampling_info, bs=bs, T=t, sampling_backend=sampling_backend)
+    return probs.view(bs, t, -1)
+
+
+def filter_target_probs(probs, sampling_info, t, bs, sampling_backend, normalize=True):
+    """runtime/worker.py:473-508 on given probabilities [bs*t, V]: the backend filter, then
+    (``normalize``) renormalised; without a filter flag the input is returned as a view.
+
+    The HIP row kernels take logits: log(p) at temperature 1 has softmax p / sum(p), which
+    selects the same support as p (the filter's cumulative masses see p / sum(p), equal to p
+    for a softmax row) and renormalises to the same distribution.  With ``normalize`` False the
+    kept entries are the input values themselves."""
+    need = any(bool(getattr(sampling_info, n, False))
+               for n in ("need_top_k_sampling", "need_top_p_sampling", "need_min_p_sampling"))
+    if not need:
+        return probs.view(bs, t, -1)
+    if sampling_backend not in ("pytorch", "flashinfer"):
+        raise ValueError(f"DSPINE sampled verify: unsupported sampling backend {sampling_backend!r}")
+    flat = probs.reshape(bs * t, -1)
+    if flat.dtype != torch.float32:
+        raise ValueError("filter_target_probs expects float32 probabilities")
+    info = SimpleNamespace(**{k: getattr(sampling_info, k) for k in (
+        "top_ks", "top_ps", "min_ps", "need_top_k_sampling", "need_top_p_sampling",
+        "need_min_p_sampling", "max_top_k") if hasattr(sampling_info, k)})
+    info.temperatures = torch.ones(bs, device=flat.device)
+    info.is_any_greedy = False
+    out = target_probs(torch.log(flat), info, bs=bs, T=t, sampling_backend=sampling_backend)
+    if not normalize:
+        out = torch.where(out > 0, flat, torch.zeros((), device=flat.device))
+    return out.view(bs, t, -1)
+
+
+def dspine_accept_sampling(*, target_probs=None, candidates, target_logits, candidate_ids, q_rows,
+                           sampling_info, sampling_backend, dense_q=None, random_state=None):
+    """Chain rejection sampling of a drafted block (runtime/worker.py:511-581).
+
+    candidates [bs, T] = [anchor, T-1 drafts]; candidate_ids / q_rows [bs, T-1, K] hold the
+    sparse q each draft was drawn from (lanes with distinct ids).  With ``target_probs``
+    [bs, T, V] the rejection runs against it; otherwise the fused verify reads target_logits
+    once.  ``dense_q`` is accepted for the reference's signature and left untouched (all
+    zero): the q lanes are read directly.  Returns (accept_len int32 [bs], bonus int64 [bs])."""
+    bs, block = candidates.shape
+    gamma = block - 1
+    if tuple(candidate_ids.shape[:2]) != (bs, gamma) or candidate_ids.shape != q_rows.shape:
+        raise RuntimeError("DSPINE verify: candidate / q layout mismatch")
+    device = candidates.device
+    uniforms, final = verification_uniforms(bs, block, device, random_state)
+    prefix = torch.zeros(bs, device=device, dtype=torch.int32)
+    q_vals = q_rows.to(torch.float32).contiguous()
+    q_ids = candidate_ids.contiguous()
+    if target_probs is None:
+        from dspine_amd.verify import verify_step
+
+        outputs, _ = verify_step(logits=target_logits, sampling_info=sampling_info, candidates=candidates,
+                                 q_ids=q_ids, q_values=q_vals, uniforms=uniforms, uniform_final=final,
+                                 prefix_lens=prefix, sampling_backend=sampling_backend)
+        return outputs[0], outputs[2]
+    outputs = _new_outputs(bs, block, device)
+    chain_on_probs(candidates=candidates, probs=target_probs.reshape(bs * block, -1), q_ids=q_ids,
+                   q_values=q_vals, verify_lens=None, uniforms=uniforms, uniform_final=final,
+                   prefix_lens=prefix, outputs=outputs)
+    return outputs[0], outputs[2]
+
+
+def chain_on_probs(*, candidates, probs, q_ids, q_values, verify_lens, uniforms, uniform_final, prefix_lens,
+                   outputs, row_offsets=None):
+    """Sparse-q chain rejection against dense P [rows, V] float32 (dsv_accept_chain)."""
+    dev = _lib.require_cuda(candidates, probs, q_ids, q_values, uniforms, uniform_final, prefix_lens)
+    if probs.ndim != 2 or probs.dtype != torch.float32 or probs.stride(1) != 1:
+        raise ValueError("target probabilities must be row-contiguous float32 [rows, V]")
+    bs, t = candidates.shape
+    a = _lib.ChainArgs()
+    keep = fill_chain_args(a, candidates=candidates, verify_lens=verify_lens, uniforms=uniforms,
+                           uniform_final=uniform_final, prefix_lens=prefix_lens, outputs=outputs,
+                           row_offsets=row_offsets)
+    fill_sparse_q(a, q_ids, q_values, bs, t)
+    a.vocab = probs.shape[1]
+    a.dense_p, a.p_stride = probs.data_ptr(), probs.stride(0)
+    if bs:
+        _lib.check(_lib.load().dsv_accept_chain(a, _lib.stream_of(dev)), "dsv_accept_chain")
+    del keep
+    return outputs
+
+
+def _new_outputs(bs, t, device):
+    return (torch.empty(bs, device=device, dtype=torch.int32),
+            torch.empty(bs, device=device, dtype=torch.int32),
+            torch.empty(bs, device=device, dtype=torch.int64),
+            torch.empty((bs, t), device=device, dtype=torch.int64),
+            torch.empty(bs, device=device, dtype=torch.int32))
+
+
+class DraftRound:
+    """This round's sampled draft chain as the verifier consumes it (the fields of the
+    reference's DSpineDraftSampler that verification reads, runtime/worker.py:70-438):
+    candidate_out int64 [>=bs, T-1, K] and q_out float32 [>=bs, T-1, K] from
+    ``serial_sample_chain``, the round's batch size, whether it ran, K and the request RNG."""
+
+    def __init__(self, k: int = 16, random=None):
+        self.k = int(k)
+        self.random = random
+        self.round_sampled = False
+        self.round_bs = 0
+        self.candidate_out = None
+        self.q_out = None
+
+    def stage(self, candidate_out, q_out):
+        if candidate_out.shape != q_out.shape or candidate_out.shape[-1] != self.k:
+            raise ValueError("draft round storage must be [bs, T-1, K] ids and q")
+        self.candidate_out, self.q_out = candidate_out, q_out
+        self.round_bs = int(candidate_out.shape[0])
+        self.round_sampled = True
+
+    def finish(self):
+        self.round_sampled = False
+
+
+class VerifyWorker:
+    """Verify-path state of DSpineWorkerV2 (runtime/worker.py:584-1089): the block size, the
+    draft round, double-buffered caller-owned output buffers, the target distribution and the
+    sampling backend."""
+
+    def __init__(self, block_size: int, device, *, k: int = 16, sampling_backend: str = "pytorch",
+                 random=None, use_target_distribution: bool = True):
+        from dspine_amd.sampling.target import TargetDistribution
+
+        self.block_size = int(block_size)
+        self.device = torch.device(device)
+        self.sampling_backend = sampling_backend
+        self._dspine_sampler = DraftRound(k, random)
+        self.target_distribution = TargetDistribution(self) if use_target_distribution else None
+        self._buffers = [None, None]
+        self._flip = 0
+        self._lock = threading.Lock()
+
+    def _next_accept_bonus_buffers(self, bs: int):
+        """Two alternating sets of (accept, commit, bonus, output, new_seq), grown on demand, so
+        the outputs of one round stay valid while the next is verified."""
+        with self._lock:
+            self._flip ^= 1
+            buf = self._buffers[self._flip]
+            if buf is None or buf[0].numel() < bs:
+                buf = _new_outputs(max(bs, 2 * (buf[0].numel() if buf else 0)), self.block_size, self.device)
+                self._buffers[self._flip] = buf
+        return tuple(x[:bs] for x in buf)
+
+    def _accept_sampled_round(self, *, candidates, next_token_logits, sampling_info, max_top_k=None,
+                              uniform_top_k_value=None):
+        """runtime/worker.py:1016-1046: refuse a round whose sampled chain did not run."""
+        sampler = self._dspine_sampler
+        bs = int(candidates.shape[0])
+        if not sampler.round_sampled:
+            raise RuntimeError("DSPINE sampled verify reached without this round's sampled draft chain")
+        if bs != sampler.round_bs:
+            raise RuntimeError(
+                f"DSPINE sampled verify for batch {bs} while the staged round has batch {sampler.round_bs}")
+        return self._dspine_verify(candidates=candidates, next_token_logits=next_token_logits,
+                                   candidate_ids=sampler.candidate_out[:bs], q_rows=sampler.q_out[:bs],
+                                   sampling_info=sampling_info)
+
+    def _dspine_verify(self, *, candidates, next_token_logits, candidate_ids, q_rows, sampling_info, **_):
+        """runtime/worker.py:1048-1089."""
+        bs = candidates.shape[0]
+        target = None
+        if self.target_distribution is not None:
+            outputs = self.target_distribution.sample_prefix(
+                candidates=candidates, next_token_logits=next_token_logits, sampling_info=sampling_info,
+                prefix_lens=torch.zeros(bs, device=candidates.device, dtype=torch.int32), bs=bs,
+                verify_lens=torch.full((bs,), self.block_size, device=candidates.device, dtype=torch.int32))
+            if outputs is not None:
+                return outputs[0], outputs[2]
+            target = self.target_distribution.dense(next_token_logits, sampling_info, bs)
+        return dspine_accept_sampling(target_probs=target, candidates=candidates, target_logits=next_token_logits,
+                                      candidate_ids=candidate_ids, q_rows=q_rows, sampling_info=sampling_info,
+                                      sampling_backend=self.sampling_backend,
+                                      random_state=self._dspine_sampler.random)
+
+
+def set_active_worker(worker) -> None:
+    global _active_worker
+    _active_worker = worker
+
+
+def accept_dspine_sampled_round(*, candidates, next_token_logits, sampling_info, max_top_k=None,
+                                uniform_top_k_value=None, **_dflash_only_arguments):
+    """Seam C (runtime/worker.py:1092-1115): (accept_len int32 [bs], bonus int64 [bs]) of this
+    round's drafts under the request's ordinary target distribution."""
+    worker = _active_worker
+    if worker is None:
+        raise RuntimeError("DSPINE sampled verify reached before the DSpine worker exists")
+    return worker._accept_sampled_round(candidates=candidates, next_token_logits=next_token_logits,
+                                        sampling_info=sampling_info, max_top_k=max_top_k,
+                                        uniform_top_k_value=uniform_top_k_value)

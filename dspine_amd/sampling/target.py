@@ -1,0 +1,64 @@
+"""Target distributions with sparse-q chain rejection (sampling/target.py of the reference).
+
+``sample_prefix`` verifies a round in one fused HIP pass (``dsv_verify``): the target
+distribution of each verified row is computed and consumed in registers/LDS, never written to
+HBM.  ``dense`` materialises P for callers that need it.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import torch
+
+from dspine_amd.sampling.random import verification_uniforms
+from dspine_amd.verify import Workspace, verify_step
+
+
+class TargetDistribution:
+    def __init__(self, worker):
+        self.worker = worker
+        self.scratch = Workspace()  # grow-only (sampling/target.py:94-104)
+
+    def dense(self, logits, info, bs, row_to_request=None):
+        """P [bs, T, V] float32 of full blocks, or [rows, 1, V] of compact rows mapped to their
+        requests by ``row_to_request`` (sampling/target.py:15-32)."""
+        from dspine_amd.runtime.worker import build_dspine_target_probs
+
+        width = int(self.worker.block_size)
+        if row_to_request is not None:
+            info = copy.copy(info)
+            for name in ("temperatures", "top_ks", "top_ps", "min_ps"):
+                value = getattr(info, name, None)
+                if value is not None:
+                    setattr(info, name, value.reshape(-1).index_select(0, row_to_request))
+            bs, width = logits.shape[0], 1
+        return build_dspine_target_probs(next_token_logits=logits, sampling_info=info, block_size=width, bs=bs,
+                                         sampling_backend=self.worker.sampling_backend)
+
+    def sample_prefix(self, *, candidates, next_token_logits, sampling_info, prefix_lens, bs, verify_lens,
+                      row_offsets=None, row_to_request=None):
+        """Verify one (possibly shortened) target call against this round's sampled q
+        (sampling/target.py:34-122).  Rows are ``b*T + s`` or compact ``row_offsets[b] + s``.
+        Returns the worker's next output buffers, or None when compact rows come without
+        ``row_offsets`` (the caller then builds P densely)."""
+        sampler = self.worker._dspine_sampler
+        if not sampler.round_sampled or sampler.round_bs != bs:
+            raise RuntimeError("Sparse rejection must consume this round's actual proposal q")
+        width = int(self.worker.block_size)
+        if candidates.shape != (bs, width):
+            raise ValueError("Proposal storage does not match this decode batch")
+        if row_to_request is not None and row_offsets is None:
+            return None
+        outputs = self.worker._next_accept_bonus_buffers(bs)
+        uniforms, final = verification_uniforms(bs, width, candidates.device, sampler.random)
+        q_ids = sampler.candidate_out[:bs]
+        q_values = sampler.q_out[:bs]
+        if q_values.dtype != torch.float32:
+            q_values = q_values.float()
+        verify_step(logits=next_token_logits, sampling_info=sampling_info, candidates=candidates,
+                    q_ids=q_ids.contiguous(), q_values=q_values.contiguous(), uniforms=uniforms,
+                    uniform_final=final, prefix_lens=prefix_lens.to(torch.int32), verify_lens=verify_lens,
+                    row_offsets=row_offsets, outputs=outputs, sampling_backend=self.worker.sampling_backend,
+                    workspace=self.scratch)
+        return outputs

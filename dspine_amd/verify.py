@@ -140,20 +140,8 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
                     ("uniforms", uniforms), ("uniform_final", uniform_final),
                     ("prefix_lens", prefix_lens)):
         _contig(t, name)
-    if sampling_backend not in ("pytorch", "flashinfer"):
-        raise ValueError(f"unsupported sampling backend {sampling_backend!r}")
-    info = sampling_info
-    temps = _f32(info.temperatures, "temperatures", bs, dev)
-    top_ks = _i32(info.top_ks, "top_ks", bs, dev)
-    top_ps = _f32(info.top_ps, "top_ps", bs, dev)
-    min_ps = _f32(getattr(info, "min_ps", None), "min_ps", bs, dev)
-    need_k = bool(getattr(info, "need_top_k_sampling", False))
-    need_p = bool(getattr(info, "need_top_p_sampling", False))
-    need_min_p = bool(getattr(info, "need_min_p_sampling", False))
-    any_greedy = bool(getattr(info, "is_any_greedy", False))
-    max_top_k = getattr(info, "max_top_k", None)
-    if not isinstance(max_top_k, int):
-        max_top_k = TOP_K_ALL  # unknown on the host: nucleus rows may occur
+    a = _lib.VerifyArgs()
+    keep = sampling_fields(a, sampling_info, bs, dev, sampling_backend)
     if outputs is None:
         outputs, kv_new = new_outputs(bs, T, dev, kv_slots=page_table is not None)
         if kv_slots is None:
@@ -183,7 +171,6 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
     ws = workspace if workspace is not None else _default_ws.setdefault(dev, Workspace())
     nbytes = int(lib.dsv_verify_workspace_bytes(rows, bs, T, V))
     wbuf = ws.get(nbytes, dev)
-    a = _lib.VerifyArgs()
     a.logits = logits.data_ptr()
     a.logits_dtype = _lib.dtype_code(logits)
     a.rows, a.vocab, a.row_stride = rows, V, logits.stride(0)
@@ -191,13 +178,6 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
     a.verify_lens = _lib.ptr(verify_lens)
     a.row_offsets = _lib.ptr(row_offsets)
     a.row_offsets_i64 = int(row_offsets is not None and row_offsets.dtype == torch.int64)
-    a.backend = _lib.DSV_BACKEND_PYTORCH if sampling_backend == "pytorch" else _lib.DSV_BACKEND_FLASHINFER
-    a.temperatures, a.top_ks, a.top_ps = temps.data_ptr(), top_ks.data_ptr(), top_ps.data_ptr()
-    a.min_ps = _lib.ptr(min_ps)
-    a.filter = int(need_k or need_p or need_min_p)
-    a.need_min_p = int(need_min_p)
-    a.any_greedy = int(any_greedy)
-    a.max_top_k = int(min(max_top_k, 2**31 - 1))
     a.hist_ids, a.hist_len = _lib.ptr(hist), hist_len
     a.presence, a.repetition = _lib.ptr(pres), _lib.ptr(rep)
     a.candidates = candidates.data_ptr()
@@ -213,4 +193,64 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
     a.workspace, a.workspace_bytes = wbuf.data_ptr(), wbuf.numel()
     a.stages = int(_stages)
     _lib.check(lib.dsv_verify(a, _lib.stream_of(dev)), "dsv_verify")
+    del keep
     return outputs, kv_slots
+
+
+def sampling_fields(a, info, bs: int, dev, sampling_backend: str):
+    """Fill the sampling-parameter fields of ``dsv_verify_args`` from a duck-typed
+    SamplingBatchInfo (temperatures [bs] or [bs, 1], top_ks, top_ps, min_ps, the need_* and
+    is_any_greedy flags, max_top_k).  Returns the converted tensors (they must outlive the
+    launch)."""
+    if sampling_backend not in ("pytorch", "flashinfer"):
+        raise ValueError(f"unsupported sampling backend {sampling_backend!r}")
+    temps = _f32(info.temperatures, "temperatures", bs, dev)
+    top_ks = _i32(info.top_ks, "top_ks", bs, dev)
+    top_ps = _f32(info.top_ps, "top_ps", bs, dev)
+    min_ps = _f32(getattr(info, "min_ps", None), "min_ps", bs, dev)
+    need_k = bool(getattr(info, "need_top_k_sampling", False))
+    need_p = bool(getattr(info, "need_top_p_sampling", False))
+    need_min_p = bool(getattr(info, "need_min_p_sampling", False))
+    max_top_k = getattr(info, "max_top_k", None)
+    if not isinstance(max_top_k, int):
+        max_top_k = TOP_K_ALL  # unknown on the host: nucleus rows may occur
+    a.backend = _lib.DSV_BACKEND_PYTORCH if sampling_backend == "pytorch" else _lib.DSV_BACKEND_FLASHINFER
+    a.temperatures, a.top_ks, a.top_ps = temps.data_ptr(), top_ks.data_ptr(), top_ps.data_ptr()
+    a.min_ps = _lib.ptr(min_ps)
+    a.filter = int(need_k or need_p or need_min_p)
+    a.need_min_p = int(need_min_p)
+    a.any_greedy = int(bool(getattr(info, "is_any_greedy", False)))
+    a.max_top_k = int(min(max_top_k, 2**31 - 1))
+    return (temps, top_ks, top_ps, min_ps)
+
+
+def target_probs(logits: torch.Tensor, info, *, bs: int, T: int, sampling_backend: str = "pytorch",
+                 normalize: bool = True, out: torch.Tensor | None = None,
+                 workspace: Workspace | None = None) -> torch.Tensor:
+    """Dense target P [rows, V] float32 of logits [rows = bs*T, V] (request b owns rows b*T ..
+    b*T+T-1): softmax(logits / temperature), the backend filter, renormalised (``normalize``
+    False: the filtered softmax p as is); rows of greedy requests one-hot at the argmax; an
+    unfiltered batch is the plain softmax (runtime/worker.py:440-508)."""
+    lib = _lib.load()
+    dev = _lib.require_cuda(logits, out)
+    if logits.ndim != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a row-contiguous [rows, V] tensor")
+    rows, V = logits.shape
+    if bs < 1 or T < 1 or rows != bs * T:
+        raise ValueError(f"logits rows {rows} != bs*T ({bs}*{T})")
+    if out is None:
+        out = torch.empty((rows, V), device=dev, dtype=torch.float32)
+    if out.shape != (rows, V) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be a row-contiguous float32 [rows, V] tensor")
+    a = _lib.VerifyArgs()
+    keep = sampling_fields(a, info, bs, dev, sampling_backend)
+    ws = workspace if workspace is not None else _default_ws.setdefault(dev, Workspace())
+    wbuf = ws.get(int(lib.dsv_verify_workspace_bytes(rows, bs, T, V)), dev)
+    a.logits, a.logits_dtype = logits.data_ptr(), _lib.dtype_code(logits)
+    a.rows, a.vocab, a.row_stride = rows, V, logits.stride(0)
+    a.bs, a.T = bs, T
+    a.workspace, a.workspace_bytes = wbuf.data_ptr(), wbuf.numel()
+    _lib.check(lib.dsv_target_probs(a, out.data_ptr(), out.stride(0), int(bool(normalize)),
+                                    _lib.stream_of(dev)), "dsv_target_probs")
+    del keep
+    return out

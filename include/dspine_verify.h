@@ -18,16 +18,20 @@
  *   dsv_topk              kernels/dspine.py:165-207 (topk_ids) and the tie rule of
  *                         layers/fp8/coarse.py:19-34 / sampling/tp_head.py:9-14
  *   dsv_uniforms          sampling/random.py:71-91 (seeded_uniforms / _uniforms :46-68)
- *   dsv_adjust_logits     sampling/compact.py:14-79 (adjust_logits)
- *   dsv_adjust_history    sampling/compact.py:14-79 with SGLang's presence/repetition buffers
+ *   dsv_adjust_logits     sampling/compact.py:14-79 (adjust_logits: the additive and the scaling
+ *                         operation, compact.py:32-45)
+ *   dsv_adjust_history    sampling/compact.py:47-63 with SGLang's presence/repetition penalizers
  *                         given as a per-request token history
- *   dsv_target_probs      runtime/worker.py:440-470 (build_dspine_target_probs)
- *   dsv_accept_dense      sampling/rejection.py:101-153 (sample_capped_chain_from_probs)
- *   dsv_accept_sparse     sampling/sparse/accept.py:463-543 (accept_sparse)
- *   dsv_compress          sampling/sparse/accept.py:422-460 (compress_probs)
- *   dsv_sample_chain      kernels/dspine.py:677-772 (serial_sample_chain)
- *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices) and the out_cache_loc
- *                         gather of verification/ragged.py:192-200
+ *   dsv_logits_padding    sampling/padding.py:4-12 (logits_padding)
+ *   dsv_target_probs      runtime/worker.py:440-508 (build_dspine_target_probs, filter_target_probs)
+ *   dsv_accept_chain      sampling/rejection.py:12-153 (_sample_capped_chain,
+ *                         sample_capped_chain_from_probs) and sampling/sparse/accept.py:81-543
+ *                         (accept_sparse with dense, RAW or packed P)
+ *   dsv_compress          sampling/sparse/accept.py:7-78,422-460 (compress_probs)
+ *   dsv_pack_joint        sampling/sparse/target.py:22-66,95-178 (_pack_joint, _overflow_dense,
+ *                         build_sparse_target)
+ *   dsv_sample_chain      kernels/dspine.py:616-772 (serial_sample_chain)
+ *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices)
  */
 #ifndef DSPINE_VERIFY_H
 #define DSPINE_VERIFY_H
@@ -145,6 +149,100 @@ int64_t dsv_topk_workspace_bytes(int64_t rows, int64_t vocab, int32_t k);
 /* (seed, position, column).                                                                */
 int dsv_uniforms(const int64_t* seeds, const void* positions, int32_t positions_i64, int64_t n,
                  int32_t width, int32_t stream_id, float* out, dsv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------- */
+/* In-place logit adjustments (one operation a call, in the caller's order, each rounded to  */
+/* the logits dtype like the reference's in-place tensor ops).  Row r belongs to request     */
+/* row_to_request[r] (int64) when given, else r / rows_per_request.                          */
+/* ---------------------------------------------------------------------------------------- */
+enum {
+  DSV_ADJ_ADD = 0,  /* x += v[req, j]                      (compact.py:38-42, :56-63, :77-79) */
+  DSV_ADJ_SCALE = 1 /* x = x < 0 ? x * v[req, j] : x / v   (compact.py:32-34, :43-45)        */
+};
+int dsv_adjust_logits(void* logits, int32_t logits_dtype, int64_t rows, int64_t vocab, int64_t row_stride,
+                      const int64_t* row_to_request, int32_t rows_per_request, int64_t requests, int32_t op,
+                      const float* values, int64_t values_stride, dsv_stream_t stream);
+/* Presence (x -= presence[req]) then repetition (x < 0 ? x*r : x/r) on each token of the    */
+/* request's history [requests, hist_len] (int32, each token once), in place.                */
+int dsv_adjust_history(void* logits, int32_t logits_dtype, int64_t rows, int64_t vocab, int64_t row_stride,
+                       const int64_t* row_to_request, int32_t rows_per_request, int64_t requests,
+                       const int32_t* hist_ids, int32_t hist_len, const float* presence,
+                       const float* repetition, dsv_stream_t stream);
+
+/* Every row of out [rows, vocab] becomes the one-point distribution [0, -inf, -inf, ...].   */
+int dsv_logits_padding(void* out, int32_t dtype, int64_t rows, int64_t vocab, int64_t row_stride,
+                       dsv_stream_t stream);
+
+/* Compact window index: out[qo[b] + d] = b*T + d for d < qo[b+1] - qo[b] (qo int32/int64,   */
+/* [bs + 1]); out holds `total` entries (qo[bs]); writes outside it are dropped.              */
+int dsv_window_index(const void* qo_indptr, int32_t qo_i64, int32_t bs, int32_t T, int64_t* out, int64_t total,
+                     dsv_stream_t stream);
+
+/* Dense target distribution P [rows, vocab] float32 (out row stride out_stride): softmax of  */
+/* the temperature-scaled logits, the backend filter, renormalised (normalize = 0: the       */
+/* filtered p as is); greedy rows one-hot at the argmax; unfiltered batches unnormalised.    */
+/* Uses the fields of dsv_verify_args up to the history and the workspace; candidates, q,    */
+/* uniforms and outputs are ignored.                                                          */
+int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t out_stride, int32_t normalize,
+                     dsv_stream_t stream);
+
+/* Per row, the ids with p > 0 in id order up to `capacity` ([rows, capacity] int32 ids /   */
+/* float32 values, unused slots -1 / 0), lengths = min(n, capacity), overflow = n > capacity  */
+/* or any negative / NaN / infinite p.                                                        */
+int dsv_compress(const float* p, int64_t rows, int64_t vocab, int64_t row_stride, int32_t capacity, int32_t* ids,
+                 float* values, int32_t* lengths, int32_t* overflow, dsv_stream_t stream);
+
+/* Sparse joint target (sampling/sparse/target.py:22-66, CPU form :156-178): from each row's  */
+/* top-W of P (top_vals [rows, W] float32 descending, top_ids [rows, W] int64; W <= 64 and    */
+/* W <= capacity + 1), keep p > 0, p >= p[top_k - 1] and the nucleus (mass of strictly larger */
+/* p < top_p, or top_p >= 1); ids ascending with p / sum(kept) into [rows, capacity] (then    */
+/* -1 / 0), lengths = min(count, capacity), overflow = count > capacity.  When P is given,    */
+/* overflow rows of P [rows, vocab] become p * (p >= p[top_k - 1]) / sum in place.           */
+int dsv_pack_joint(const float* top_vals, const int64_t* top_ids, int64_t rows, int32_t W, const int32_t* top_ks,
+                   const float* top_ps, int32_t capacity, int32_t* ids, float* values, int32_t* lengths,
+                   int32_t* overflow, float* P, int64_t vocab, int64_t p_stride, dsv_stream_t stream);
+
+/* Chain rejection on given distributions.  P row of draft step s of request b: row_offsets  */
+/* [b] + s, else b*T + s.  Packed P (p_ids != NULL) is used on rows whose overflow flag is 0  */
+/* (capacity <= 64); other rows read dense_p (divided by denominator[row] when given).  q is  */
+/* dense [bs, T-1, vocab] (dense_q) or sparse lanes [bs, T-1, K] (q_ids / q_values).          */
+typedef struct dsv_chain_args {
+  int32_t bs, T, K, pad0;
+  int64_t vocab;
+  const int64_t* candidates;  /* [bs, T] */
+  const int32_t* verify_lens; /* [bs] in [1, T], NULL = T */
+  const float* uniforms;      /* [bs, T-1] */
+  const float* uniform_final; /* [bs] */
+  const int32_t* prefix_lens; /* [bs] */
+  const void* row_offsets;    /* [bs] int32 / int64, NULL = b*T */
+  int32_t row_offsets_i64, pad1;
+  const float* dense_p;       /* [rows, vocab] (row stride p_stride), or NULL */
+  int64_t p_stride;
+  const float* denominator;   /* [rows] or NULL */
+  const int32_t* p_ids;       /* packed [rows, p_cap], or NULL */
+  const float* p_values;
+  const int32_t* p_lengths;
+  const int32_t* p_overflow;  /* [rows] or NULL (no overflow) */
+  int32_t p_cap, pad2;
+  const float* dense_q;       /* [bs, T-1, vocab] (row stride q_stride), or NULL */
+  int64_t q_stride;
+  const void* q_ids;          /* [bs, T-1, K] int32 / int64 */
+  int32_t q_ids_i64, pad3;
+  const float* q_values;      /* [bs, T-1, K] */
+  int32_t* accept;            /* [bs] */
+  int32_t* commit;            /* [bs] */
+  int64_t* bonus;             /* [bs] */
+  int64_t* output;            /* [bs, T] */
+  int32_t* new_seq;           /* [bs] */
+} dsv_chain_args;
+int dsv_accept_chain(const dsv_chain_args* args, dsv_stream_t stream);
+
+/* Draft-side K-lane chain over n = bs*(block_size-1) rows of table [n, K, K] (K <= 64):      */
+/* out_tok [n] int64, out_q [n, K] float32, confidence [n] float32 (may be NULL).            */
+int dsv_sample_chain(const float* table, int64_t n, int32_t K, int32_t block_size, const float* inv_temp,
+                     const int32_t* top_k, const float* top_p, const float* min_p, const int32_t* greedy,
+                     const float* u, const int64_t* cand, const int64_t* greedy_tok, int64_t* out_tok,
+                     float* out_q, float* confidence, dsv_stream_t stream);
 
 #ifdef __cplusplus
 }

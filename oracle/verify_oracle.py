@@ -48,7 +48,12 @@ PINNED = {
     "compress": "invariants of tests/test_p_distribution_reference.py:156-175",
     "window_index": "closed form tests/test_sps.py:446-448",
     "logits_padding": "tests/test_release.py:45-67",
-    "sample_chain": "ties-to-lower-lane known answer tests/test_cuda.py:213-232, brute force",
+    "sample_chain": "ties-to-lower-lane known answer tests/test_cuda.py:213-232, brute force; "
+    "confidence known answers tests/test_sampled_confidence.py:124-196",
+    "packed_bonus": "packed == dense identity on the same P and coins "
+    "(tests/test_sparse_accept_compact.py:58-105, whose pure-Python reference :22-53 is the spec)",
+    "sparse_target": "equals the full-vocabulary joint filter (flashinfer restatement) on unique "
+    "scores, closed-form overflow densification; tie order at the k-th place unpinned",
 }
 
 
@@ -310,7 +315,7 @@ def _clamp01(v: float) -> float:
 
 
 def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, uniform_final,
-                 prefix_lens, row_offsets=None, dense_q=None):
+                 prefix_lens, row_offsets=None, dense_q=None, packed=None, vocab=None):
     """Chain rejection for every request.
 
     prob_row(r) returns target row r as a float32 numpy vector; rows are ``b*T + s`` or
@@ -320,6 +325,11 @@ def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, u
     Accept iff q > 0, q <= 1 and float32(u*q) < p.  The residual max(p - q, 0) (or p when every
     draft was accepted or the residual has no mass) is summed in float64 in id order; bonus =
     first id with cdf > u_final*mass, default V-1.
+
+    ``packed`` = (ids, values, lengths, overflow) [rows, cap] is packed P
+    (sampling/sparse/accept.py:239-304): a row whose overflow flag is 0 (every row when
+    ``prob_row`` is None, then ``vocab`` gives V) takes p at a token as the sum of its entries
+    with that id, and draws its bonus by ``packed_bonus``.
 
     Returns (accept, commit, bonus, output [bs, T], new_seq, margins) where margins[b] holds
     the smallest relative decision margin of request b (accept tests and the bonus draw)."""
@@ -338,6 +348,10 @@ def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, u
     output = np.zeros((bs, T), np.int64)
     new_seq = np.zeros(bs, np.int32)
     margins = np.full(bs, np.inf)
+
+    def is_packed(r):
+        return packed is not None and (prob_row is None or int(np.asarray(packed[3])[r]) == 0)
+
     for b in range(bs):
         cap = int(caps[b])
         base = int(offs[b]) if offs is not None else b * T
@@ -345,9 +359,13 @@ def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, u
         margin = math.inf
         while a < cap - 1:
             token = int(cand[b, a + 1])
-            row = prob_row(base + a)
-            V = row.shape[0]
-            p = np.float32(row[token]) if 0 <= token < V else np.float32(0.0)
+            if is_packed(base + a):
+                p = packed_p_at(packed, base + a, token)
+                V = int(vocab) if prob_row is None else prob_row(base + a).shape[0]
+            else:
+                row = prob_row(base + a)
+                V = row.shape[0]
+                p = np.float32(row[token]) if 0 <= token < V else np.float32(0.0)
             if dense_q is not None:
                 qrow = dense_q(b, a)
                 q = np.float32(qrow[token]) if 0 <= token < V else np.float32(0.0)
@@ -366,6 +384,17 @@ def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, u
             else:
                 break
         all_acc = a == cap - 1
+        if is_packed(base + a):
+            V = int(vocab) if prob_row is None else prob_row(base + a).shape[0]
+            qrow = None if (all_acc or qi is None) else (qi[b, a], qv[b, a])
+            bonus, m = packed_bonus(packed, base + a, qrow, float(uf[b]), V)
+            margin = min(margin, m)
+            accept[b], commit[b], bonus_out[b] = a, a + 1, bonus
+            for i in range(T):
+                output[b, i] = cand[b, i + 1] if i < a else (bonus if i == a else 0)
+            new_seq[b] = prefix[b] + a + 1
+            margins[b] = margin
+            continue
         prow = prob_row(base + a).astype(np.float64)
         V = prow.shape[0]
         w = prow
@@ -399,6 +428,58 @@ def chain_accept(prob_row, candidates, q_ids, q_values, verify_lens, uniforms, u
         new_seq[b] = prefix[b] + a + 1
         margins[b] = margin
     return accept, commit, bonus_out, output, new_seq, margins
+
+
+def packed_p_at(packed, row: int, token: int) -> np.float32:
+    """p of a packed row at a token: the float32 sum of its entries with that id
+    (sampling/sparse/accept.py:270-274)."""
+    ids, vals, lens = (np.asarray(x) for x in packed[:3])
+    p = np.float32(0.0)
+    for i in range(int(lens[row])):
+        if int(ids[row, i]) == token:
+            p = np.float32(p + np.float32(vals[row, i]))
+    return p
+
+
+def packed_bonus(packed, row: int, q, coin: float, V: int):
+    """sampling/sparse/accept.py:179-204: the packed entries in ascending id order; the
+    residual subtracts, at each id, the clamped q summed over the draft lanes with that id (q
+    None: every draft accepted, the residual is p); zero residual mass falls back to p; bonus =
+    first id with cdf > coin*mass (float64, id order), default V-1.  Returns (bonus, margin)."""
+    ids, vals, lens = (np.asarray(x) for x in packed[:3])
+    n = int(lens[row])
+    entries = sorted(int(ids[row, i]) for i in range(n))
+    p = [float(packed_p_at(packed, row, t)) for t in entries]
+    w = list(p)
+    if q is not None:
+        qids, qvals = q
+        at = []
+        for t in entries:
+            acc = 0.0
+            for lane in range(len(qids)):
+                if int(qids[lane]) == t:
+                    acc += _clamp01(float(qvals[lane]))
+            at.append(acc)
+        w = [max(pv - av, 0.0) for pv, av in zip(p, at)]
+        if sum(w) <= 0.0:
+            w = list(p)
+    cdf = np.cumsum(np.asarray(w, dtype=np.float64)) if w else np.zeros(0)
+    mass = float(cdf[-1]) if cdf.size else 0.0
+    thr = coin * mass
+    for i, t in enumerate(entries):
+        if cdf[i] > thr and t < V:
+            lo = float(cdf[i - 1]) if i > 0 else 0.0
+            m = min((float(cdf[i]) - thr) / mass, (thr - lo) / mass) if mass > 0 else math.inf
+            return t, m
+    return V - 1, math.inf
+
+
+def raw_prob_row(dense_p, denominator):
+    """RAW target rows (sampling/sparse/accept.py:119-128,153-160,259-268): p / denominator[row]
+    in IEEE float32."""
+    P = torch.as_tensor(dense_p, dtype=torch.float32)
+    den = torch.as_tensor(denominator, dtype=torch.float32).view(-1)
+    return lambda r: (P[r] / den[r]).numpy()
 
 
 # ---------------------------------------------------------------------------------------
@@ -497,15 +578,58 @@ def kv_slots(page_table, prefix_lens, accept, T: int) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------------------
+# S7. Sparse joint target (sampling/sparse/target.py:95-178, CPU form :156-178)
+# ---------------------------------------------------------------------------------------
+
+def sparse_target(p: torch.Tensor, top_ks_rows, top_ps_rows, capacity: int):
+    """From softmax rows p [rows, V] float32: the top-(capacity+1) prefix (lower id first among
+    equal p); keep p > 0, p >= p[k-1] and the nucleus (mass of strictly larger prefix p <
+    top_p, or top_p >= 1); pack ids ascending with p / sum(kept) into [rows, capacity] (-1 / 0
+    padding); lengths = min(count, capacity); overflow = count > capacity.  Overflow rows of the
+    returned dense copy are p * (p >= p[k-1]) / sum; other rows are p unchanged.
+    Returns (ids, values, lengths, overflow, dense)."""
+    rows, vocab = p.shape
+    width = min(capacity + 1, vocab)
+    order = torch.argsort(p, dim=-1, descending=True, stable=True)[:, :width]
+    top = p.gather(1, order)
+    ks = torch.as_tensor(top_ks_rows).long().view(-1).clamp(1, width)
+    tps = torch.as_tensor(top_ps_rows, dtype=torch.float32).view(-1)
+    threshold = top.gather(1, (ks - 1)[:, None])
+    higher = (top[:, None, :] * (top[:, None, :] > top[:, :, None])).sum(-1)
+    keep = (top > 0) & (top >= threshold) & ((higher < tps[:, None]) | (tps[:, None] >= 1))
+    count = keep.sum(-1)
+    kept = top.masked_fill(~keep, 0)
+    kept = kept / kept.sum(-1, keepdim=True)
+    key = order.masked_fill(~keep, 2147483647)
+    sorted_ids, perm = key.sort(-1)
+    kept = kept.gather(1, perm)
+    ids = torch.full((rows, capacity), -1, dtype=torch.int32)
+    vals = torch.zeros((rows, capacity), dtype=torch.float32)
+    n = min(width, capacity)
+    ids[:, :n] = sorted_ids[:, :n].masked_fill(sorted_ids[:, :n] == 2147483647, -1).int()
+    vals[:, :n] = kept[:, :n]
+    overflow = (count > capacity).int()
+    dense = p.clone()
+    for r in range(rows):
+        if overflow[r]:
+            dense[r] = dense[r].masked_fill(dense[r] < threshold[r], 0)
+            dense[r] /= dense[r].sum()
+    return ids, vals, count.clamp_max(capacity).int(), overflow, dense
+
+
+# ---------------------------------------------------------------------------------------
 # a19. Draft-side K-lane chain (kernels/dspine.py:616-674)
 # ---------------------------------------------------------------------------------------
 
-def sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, greedy_tok, block_size):
+def sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, greedy_tok, block_size,
+                 confidence=None):
     """Per request, walk T-1 rows of the [K, K] table: p = softmax(table[row, sender] * inv_t);
     rank/mass-ahead with lower lanes first among ties; keep rank < top_k, mass-ahead <= top_p,
     p >= min_p * max p; q = w / sum w; choice = #(cdf <= u * cdf[K-1]) clamped to the last kept
     lane.  Greedy requests emit greedy_tok with a one-hot q.  The sender of the next row is the
-    sampled lane.  fp32 arithmetic, sums in lane order."""
+    sampled lane.  fp32 arithmetic, sums in lane order.  ``confidence`` (float32 [>= n], kernels/
+    dspine.py:645-648) receives max p of each row of a non-greedy request (before filtering);
+    rows of greedy requests are left as they are."""
     table = np.asarray(table, dtype=np.float32)
     n, K, _ = table.shape
     tm1 = int(block_size) - 1
@@ -524,6 +648,8 @@ def sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, greedy_t
                 tot = np.float32(tot + mass[c])
             p = (mass / tot).astype(np.float32)
             pmax = p.max()
+            if confidence is not None and not int(greedy[b]):
+                confidence[r] = pmax
             keep = np.zeros(K, bool)
             for c in range(K):
                 ahead = [d for d in range(K) if p[d] > p[c] or (p[d] == p[c] and d < c)]

@@ -21,7 +21,10 @@ def test_header_declares_the_entry_points():
     names = declared_functions()
     for required in ("dsv_verify", "dsv_verify_workspace_bytes", "dsv_greedy_verify",
                      "dsv_greedy_workspace_bytes", "dsv_topk", "dsv_topk_workspace_bytes",
-                     "dsv_uniforms", "dsv_last_error", "dsv_device_count", "dsv_profile_events"):
+                     "dsv_uniforms", "dsv_last_error", "dsv_device_count", "dsv_profile_events",
+                     "dsv_adjust_logits", "dsv_adjust_history", "dsv_logits_padding", "dsv_window_index",
+                     "dsv_target_probs", "dsv_compress", "dsv_accept_chain", "dsv_sample_chain",
+                     "dsv_pack_joint"):
         assert required in names
 
 
@@ -36,19 +39,21 @@ def test_library_exports_every_declared_symbol():
     assert set(_lib.EXPORTS) == set(declared_functions())
 
 
-def test_args_struct_layout_matches_c(tmp_path):
-    """ctypes VerifyArgs field offsets == offsetof() of struct dsv_verify_args compiled by gcc."""
-    from dspine_amd._lib import VerifyArgs
+@pytest.mark.parametrize("cls_name, c_name", [("VerifyArgs", "dsv_verify_args"), ("ChainArgs", "dsv_chain_args")])
+def test_args_struct_layout_matches_c(tmp_path, cls_name, c_name):
+    """ctypes field offsets == offsetof() of the C struct compiled by gcc."""
+    from dspine_amd import _lib
 
-    names = [f[0] for f in VerifyArgs._fields_]
+    cls = getattr(_lib, cls_name)
+    names = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dspine_verify.h"', "int main(void) {",
-             '  printf("%zu\\n", sizeof(dsv_verify_args));']
-    lines += [f'  printf("%zu\\n", offsetof(dsv_verify_args, {n}));' for n in names]
+             f'  printf("%zu\\n", sizeof({c_name}));']
+    lines += [f'  printf("%zu\\n", offsetof({c_name}, {n}));' for n in names]
     lines += ["  return 0;", "}"]
     src.write_text("\n".join(lines))
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     out = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
-    assert out[0] == ctypes.sizeof(VerifyArgs)
-    assert out[1:] == [getattr(VerifyArgs, n).offset for n in names]
+    assert out[0] == ctypes.sizeof(cls)
+    assert out[1:] == [getattr(cls, n).offset for n in names]

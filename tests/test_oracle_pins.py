@@ -5,6 +5,7 @@ tie rule) fails it."""
 
 import math
 import random
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -400,3 +401,131 @@ def test_exact_softmax_is_rounded_float64():
     # closed form on the flat row: p(0) = 1 / (V - 20 + 20 e^0.5)
     p0 = 1.0 / (151936 - 20 + 20 * np.exp(0.5))
     assert abs(ex[0, 1].item() / p0 - 1) < 1e-7
+
+
+# ---------------------------------------------------------------------------------------
+# packed P (sampling/sparse/accept.py:179-204,239-304), RAW rows, sparse joint target (S7),
+# draft-chain confidence
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("bs", [1, 9, 32])
+@pytest.mark.parametrize("kind", ["compact", "pure_packed", "overflow"])
+def test_packed_chain_matches_pure_python(bs, kind):
+    """tests/test_sparse_accept_compact.py:56-105: packed rows (support 7, stored in reverse id
+    order) give exactly the dense pure-Python reference's outputs."""
+    rng = torch.Generator().manual_seed(713)
+    vocab, T, K = 257, 16, 16
+    caps = (torch.arange(bs) % T + 1).tolist()
+    caps[0] = T
+    rows = sum(caps)
+    p = torch.zeros(rows, vocab)
+    support = torch.tensor([0, 2, 3, 7, 11, 13, 15])
+    p[:, support] = torch.softmax(torch.randn(rows, len(support), generator=rng), -1)
+    qids = torch.arange(16).expand(bs, T - 1, K).contiguous()
+    qvals = torch.softmax(torch.randn(bs, T - 1, K, generator=rng), -1)
+    cand = torch.zeros(bs, T, dtype=torch.int64)
+    cand[:, 1:] = torch.multinomial(qvals.reshape(-1, K), 1, generator=rng).view(bs, T - 1)
+    u = torch.full((bs, T - 1), .371)
+    uf = torch.linspace(.071, .917, bs)
+    prefix = torch.arange(bs) + 8191
+    cand[0, 1:] = 0
+    u[0] = 0
+    offsets = np.concatenate(([0], np.cumsum(caps)))[:-1]
+    if bs > 1:
+        lo, hi = int(offsets[1]), int(offsets[1]) + caps[1]
+        same = torch.softmax(torch.arange(16, dtype=torch.float32), 0)
+        p[lo:hi] = 0
+        p[lo:hi, :16] = same
+        qvals[1] = same
+        u[1] = 1
+    if kind == "overflow":
+        p[::11] = torch.softmax(torch.randn((len(p[::11]), vocab), generator=rng), -1)
+    ids, vals, lens, ovf = O.compress(p, 32)
+    lane = torch.arange(32)[None, :]
+    perm = (lens[:, None].long() - 1 - lane).clamp_min(0)
+    packed = (ids.gather(1, perm).where(lane < lens[:, None], -1), vals.gather(1, perm).where(lane < lens[:, None], 0),
+              lens, ovf)
+    pn = p.numpy()
+    expected = _pure_python_reference(pn.tolist(), cand.tolist(), qids.tolist(), qvals.tolist(), caps,
+                                      u.tolist(), uf.tolist(), prefix.tolist())
+    prob_row = None if kind == "pure_packed" else (lambda r: pn[r])
+    got = O.chain_accept(prob_row, cand.numpy(), qids.numpy(), qvals.numpy(), caps, u.numpy(), uf.numpy(),
+                         prefix.numpy(), row_offsets=offsets, packed=packed, vocab=vocab)
+    for b, (a, c, bonus, emitted, ns) in enumerate(expected):
+        assert (int(got[0][b]), int(got[1][b]), int(got[2][b]), got[3][b].tolist(), int(got[4][b])) == \
+            (a, c, bonus, emitted, ns), b
+
+
+def test_packed_bonus_sums_repeated_q_lanes():
+    """Packed residual subtracts the clamped q summed over the lanes with an id
+    (accept.py:186-193); lanes outside [0, 1] count as 0."""
+    packed = (np.array([[7, 3, 9]]), np.array([[0.2, 0.5, 0.3]], np.float32), np.array([3]), np.array([0]))
+    qids = np.array([3, 3, 9, 7])
+    qvals = np.array([0.2, 0.25, 1.5, 0.05], np.float32)
+    # residual in id order (3, 7, 9): (0.5 - 0.45, 0.2 - 0.05, 0.3 - 0) = (0.05, 0.15, 0.3)
+    # cdf (0.05, 0.2, 0.5): coins away from the boundaries
+    for coin, want in ((0.0, 3), (0.05, 3), (0.2, 7), (0.3, 7), (0.5, 9), (0.99, 9)):
+        assert O.packed_bonus(packed, 0, (qids, qvals), coin, 100)[0] == want, coin
+    # zero residual mass falls back to p; all-accepted draws from p directly
+    full = (np.array([3, 7, 9]), np.array([1.0, 1.0, 1.0], np.float32))
+    assert O.packed_bonus(packed, 0, full, 0.5, 100)[0] == 7  # p in id order: 0.5 | 0.2 | 0.3
+    assert O.packed_bonus(packed, 0, None, 0.45, 100)[0] == 3
+
+
+def test_raw_rows_are_ieee_quotients():
+    P = torch.tensor([[3.0, 1.0, 0.5]])
+    den = torch.tensor([3.0])
+    row = O.raw_prob_row(P, den)(0)
+    assert row.dtype == np.float32 and row.tolist() == [1.0, np.float32(1.0) / np.float32(3.0), np.float32(0.5 / 3.0)]
+
+
+def test_sparse_target_equals_full_vocabulary_joint_filter():
+    """On unique scores the top-(cap+1) joint support equals the full-vocabulary flashinfer
+    joint filter (tests/ref_utils.py:79-108 restated); packed values are the renormalised p."""
+    g = torch.Generator().manual_seed(4)
+    rows, V, cap = 16, 3001, 32
+    p = torch.softmax(torch.randn(rows, V, generator=g) * 3, -1)
+    ks = torch.tensor([1, 5, 20, 32] * 4)
+    ps = torch.tensor([1.0, 0.9, 0.5, 0.95] * 4)
+    ids, vals, lens, ovf, dense = O.sparse_target(p, ks, ps, cap)
+    info = SimpleNamespace(top_ks=ks, top_ps=ps, min_ps=torch.zeros(rows), need_top_k_sampling=True,
+                           need_top_p_sampling=True, need_min_p_sampling=False)
+    full = O.filter_target_probs(p.clone(), info, 1, rows, "flashinfer").view(rows, V)
+    assert int(ovf.sum()) == 0 and torch.equal(dense, p)
+    for r in range(rows):
+        support = torch.nonzero(full[r] > 0).view(-1)
+        n = int(lens[r])
+        assert torch.equal(ids[r, :n].long(), support) and bool((ids[r, n:] == -1).all())
+        torch.testing.assert_close(vals[r, :n], full[r, support], rtol=2e-6, atol=0)
+
+
+def test_sparse_target_overflow_rows_are_densified():
+    """A tie group at the k-th place larger than the capacity overflows; the dense row keeps
+    every p >= p[k-1], renormalised (sparse/target.py:60-66,174-177)."""
+    p = torch.zeros(1, 100)
+    p[0, 10:50] = 0.02
+    p[0, 60] = 0.2
+    ids, vals, lens, ovf, dense = O.sparse_target(p, torch.tensor([4]), torch.tensor([1.0]), 8)
+    assert int(ovf[0]) == 1 and int(lens[0]) == 8
+    assert ids[0].tolist() == list(range(10, 18))
+    expect = torch.zeros(100)
+    expect[10:50] = 0.02 / 1.0
+    expect[60] = 0.2
+    torch.testing.assert_close(dense[0], expect / expect.sum(), rtol=1e-6, atol=0)
+
+
+def test_sample_chain_confidence_known_answers():
+    """tests/test_sampled_confidence.py:169-196: confidence is max p before filtering, also when
+    the filter leaves q one-hot; greedy requests leave it untouched."""
+    p = np.array([[0.85, 0.14, 0.009, 0.001], [0.99, 0.008, 0.001, 0.001]], np.float32)
+    k, width, temperature = 4, 2, 0.7
+    table = np.repeat((np.log(p) * temperature)[:, None, :], k, 1).astype(np.float32)
+    conf = np.full(2, -1.0, np.float32)
+    tok, q = O.sample_chain(table, [1 / temperature] * 2, [5, 5], [0.8, 0.8], [0.05, 0.05], [0, 0],
+                            np.array([0.2, 0.8]), np.arange(k)[None].repeat(2, 0), np.zeros(2, np.int64), width,
+                            confidence=conf)
+    np.testing.assert_allclose(q.max(-1), 1.0)
+    np.testing.assert_allclose(conf, p.max(-1), rtol=1e-5)
+    conf2 = np.full(2, -1.0, np.float32)
+    O.sample_chain(table, [1 / temperature] * 2, [5, 5], [0.8, 0.8], [0.05, 0.05], [0, 1], np.array([0.2, 0.8]),
+                   np.arange(k)[None].repeat(2, 0), np.zeros(2, np.int64), width, confidence=conf2)
+    assert conf2[1] == -1.0 and conf2[0] == conf[0]
