@@ -87,8 +87,10 @@ def time_graph(step, steps, warmup, torch):
     return start.elapsed_time(end) / steps, g
 
 
-def cpu_baseline(batch, max_seconds=30.0):
-    """The CPU oracle (torch on the host) on a bounded sample of the same workload."""
+def cpu_baseline(batch, min_seconds=10.0, max_seconds=30.0):
+    """The CPU oracle (torch on the host) on a bounded sample of the same workload: passes over
+    the requests, one request per call, until at least ``min_seconds`` of work (capped at
+    ``max_seconds``)."""
     import numpy as np
     import torch
 
@@ -97,23 +99,28 @@ def cpu_baseline(batch, max_seconds=30.0):
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     bs, T = batch["candidates"].shape
-    reqs, rows, t0 = [], 0, time.perf_counter()
-    for b in range(bs):
-        O.verify_step(
-            batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
-            q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(),
-            verify_lens=np.full(bs, T), uniforms=batch["uniforms"].numpy(),
-            uniform_final=batch["uniform_final"].numpy(), prefix_lens=batch["prefix_lens"].numpy(),
-            hist_ids=batch["hist_ids"], presence=batch["presence"], repetition=batch["repetition"],
-            page_table=batch["page_table"], requests=[b])
-        reqs.append(b)
-        rows += T
-        if time.perf_counter() - t0 > max_seconds:
-            break
+    calls, rows, t0 = 0, 0, time.perf_counter()
+    done = False
+    while not done:
+        for b in range(bs):
+            O.verify_step(
+                batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
+                q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(),
+                verify_lens=np.full(bs, T), uniforms=batch["uniforms"].numpy(),
+                uniform_final=batch["uniform_final"].numpy(), prefix_lens=batch["prefix_lens"].numpy(),
+                hist_ids=batch["hist_ids"], presence=batch["presence"], repetition=batch["repetition"],
+                page_table=batch["page_table"], requests=[b])
+            calls += 1
+            rows += T
+            if time.perf_counter() - t0 > max_seconds:
+                done = True
+                break
+        if time.perf_counter() - t0 >= min_seconds:
+            done = True
     dt = time.perf_counter() - t0
     return {"value": rows / dt, "unit": "rows/s", "cores": n, "kind": "port",
-            "sample": f"{len(reqs)} of {bs} requests ({rows} rows x 151936) of the same workload, "
-                      f"one request per oracle call, {dt:.1f} s"}
+            "sample": f"{calls} request verifications ({calls / bs:.2f} passes over the {bs} requests, "
+                      f"{rows} rows x 151936) of the same workload, one request per oracle call, {dt:.1f} s"}
 
 
 def main():
