@@ -150,6 +150,7 @@ struct DrawShared {
   uint64_t red_u[DNW_MAX];
   int64_t qid[QMAX];
   float qv[QMAX];       // clamped q of the lane
+  float qraw[QMAX];     // q of the lane as given (the draft test sums these)
   int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
   int32_t qrank[QMAX];  // q id at a split cut key: values at the cut key before it (id order), else -1
   float qx[QMAX];       // adjusted value at the q id
@@ -160,7 +161,9 @@ struct DrawShared {
   int32_t nlist;
   int64_t bonus;
   double chunk_lo, thr, pick_lo;
-  int32_t acc, chunk, tieq, use_r, pick_thread, tb_pick;
+  int32_t acc, chunk, tieq, use_r, pick_thread, ptb;
+  uint64_t ptmask;   // the picked thread's span positions at the cut key
+  float pw[64];      // the picked thread's span weights
 };
 
 // The draw's P at value x: exp2(x c2 - M c2) * scale, scale = 1/Z (over the kept mass S for a
@@ -200,6 +203,61 @@ __device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, int ste
   }
   __syncthreads();
 }
+
+// The q lanes of draft step+1 for one wave (lanes are the q lanes): ids, given and clamped
+// values, whether the lane is the last with its id, and -- want_x -- the adjusted logit at each
+// such id.  Leaves them in sh for the wave (fenced), the workgroup sees them after a barrier.
+template <int DT>
+__device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, bool live, const char* rowp,
+                                             bool want_x, DrawShared& sh) {
+  const dsv_verify_args& a = P.a;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int64_t qi = ((int64_t)b * (a.T - 1) + step) * a.K;
+  const bool on = live && lane < a.K;
+  const int64_t qid = on ? load_index(a.q_ids, a.q_ids_i64, qi + lane) : -1;
+  const float qr = on ? a.q_values[qi + lane] : 0.f;
+  sh.qid[lane] = qid;
+  sh.qraw[lane] = qr;
+  sh.qv[lane] = clamp01(qr);
+  sh.qd[lane] = 0.0;
+  sh.qrank[lane] = -1;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  bool last = qid >= 0 && qid < a.vocab;
+  for (int l2 = lane + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != qid;
+  sh.qlast[lane] = last;
+  float xq = -INFINITY;
+  if (want_x && last) {
+    xq = load_elem<DT>(rowp, qid);
+    if (P.pbits && pen_test(P, b, qid))
+      xq = penalize<DT>(xq, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
+  }
+  sh.qx[lane] = xq;
+}
+
+// The draft test from the fetched q lanes (wave-level): q = the sum of the lanes holding tok.
+__device__ __forceinline__ int32_t step_accept_lds(const DrawShared& sh, int K, int64_t tok, float p, float coin) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  uint64_t bal = __ballot(lane < K && sh.qid[lane] == tok);
+  float q = 0.f;
+  while (bal) {
+    const int l = __ffsll((long long)bal) - 1;
+    bal &= bal - 1ull;
+    q += sh.qraw[l];
+  }
+  return (q > 0.f && q <= 1.f && coin * q < p) ? 1 : 0;
+}
+
+// The row's chunk statistics, draft token and coin, read at the start of the row merge.
+struct RowPre {
+  ChunkStat cs[NCHK];
+  int64_t tok;  // draft token the row tests, -1 for none
+  float u;      // its coin
+  float uf;     // the request's bonus coin
+  float top_p, min_p;
+  int32_t top_k;
+};
 
 // Thread t's span of chunk c in id order (NT threads tile the chunk: ids c*chunk + t*FE + [0,
 // FE)), penalised and handed to f(i, x) in id order; -inf past the row.
@@ -276,7 +334,7 @@ struct DrawPlan {
 // tieq, use_r, qd).
 template <int DT, bool ALIGNED, int NT>
 __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
-                                           bool resid, float uf, DrawShared& sh) {
+                                           bool resid, float uf, DrawShared& sh, bool have_qx = false) {
   constexpr int NW = NT / WAVE;
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
   const dsv_verify_args& a = P.a;
@@ -293,7 +351,9 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
   if (tid < WAVE) {
     const bool qlive = resid && lane < a.K && sh.qlast[lane];
     float xq = -INFINITY;
-    if (qlive) {
+    if (have_qx) {  // fetched with the q lanes
+      xq = qlive ? sh.qx[lane] : -INFINITY;
+    } else if (qlive) {
       const int64_t qid = sh.qid[lane];
       xq = load_elem<DT>(rowp, qid);
       if (pen && pen_test(P, b, qid)) xq = penalize<DT>(xq, pres, rep);
@@ -384,8 +444,9 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
                                               DrawShared& sh) {
   constexpr int NW = NT / WAVE;
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
+  static_assert(FE <= 64, "a thread's span fits a 64-bit mask");
   const dsv_verify_args& a = P.a;
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int tid = threadIdx.x;
   const int64_t V = a.vocab;
   const bool pen = P.pbits != nullptr;
   const float pres = pen && a.presence ? a.presence[b] : 0.f;
@@ -402,14 +463,22 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
   if (cstar < 0) return V - 1;
   const bool use_r = sh.use_r != 0;
   const int64_t jlo = (int64_t)cstar * CHE + (int64_t)tid * FE;
+  // the span's weights stay in registers for the thread that holds the threshold
+  float w[FE];
+  uint64_t tmask = 0;  // span positions holding the cut key
   double mt = 0.0;
   int32_t tt = 0;
-  for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, [&](int, float x) {
+  for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, [&](int i, float x) {
     const uint32_t k = key_of<DT>(x);
-    if (!hist || k > rs.vcut)
-      mt += (double)bp(x);
-    else if (k == rs.vcut)
+    float wi = 0.f;
+    if (!hist || k > rs.vcut) {
+      wi = bp(x);
+    } else if (k == rs.vcut) {
+      tmask |= 1ull << i;
       ++tt;
+    }
+    w[i] = wi;
+    mt += (double)wi;
   });
   int32_t tie_tot = 0;
   const int32_t tbefore = sh.tieq + block_excl_scan<NW>(tt, sh.red_i, &tie_tot);
@@ -433,46 +502,39 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
     const uint64_t lp = block_max_u64<NW>(w_t > 0.0 ? (uint64_t)tid + 1 : 0ull, sh.red_u);
     pt = lp ? (int)lp - 1 : -1;
   }
-  if (tid == pt) {
-    sh.tb_pick = tbefore;
+  if (tid == pt) {  // the span's weights, from registers, for the wave that walks it
+#pragma unroll
+    for (int e = 0; e < FE; ++e) sh.pw[e] = w[e];
+    sh.ptmask = tmask;
+    sh.ptb = tbefore;
     sh.pick_lo = base + tlo;
   }
   __syncthreads();
   if (pt >= 0 && tid < WAVE) {
-    // thread pt's span, one id a lane (in passes of a wave): weights, then the running sum
+    // one id a lane in id order: kept cut-key values in rank order, the residual at the q ids,
+    // then the running sum
+    const int lane = tid;
     const int64_t plo = (int64_t)cstar * CHE + (int64_t)pt * FE;
-    double start = sh.pick_lo;
-    int32_t seen_before = 0;
-    int64_t pick = -1, last_pos = -1;
-    for (int p0 = 0; p0 < FE && pick < 0; p0 += WAVE) {
-      const int64_t j = plo + p0 + lane;
-      const bool live = p0 + lane < FE && j < V;
-      float xj = live ? load_elem<DT>(rowp, j) : -INFINITY;
-      if (live && pen && pen_test(P, b, j)) xj = penalize<DT>(xj, pres, rep);
-      const uint32_t k = key_of<DT>(xj);
-      const bool tie = live && hist && k == rs.vcut;
-      const uint64_t tmask = __ballot(tie);
-      const int32_t seen = seen_before + __popcll(tmask & ((1ull << lane) - 1ull));
-      double Pj = 0.0;
-      if (live) {
-        if (!hist || k > rs.vcut)
-          Pj = (double)bp(xj);
-        else if (tie && (int64_t)sh.tb_pick + seen < (int64_t)rs.ktie)
-          Pj = P_cut;
-        if (use_r)
-          for (int l = 0; l < a.K; ++l)
-            if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
-      }
-      double wlo, whi;
-      const double tot = wave_tiles(Pj, wlo, whi);
-      const uint64_t hitj = __ballot(live && Pj > 0.0 && start + whi > thr);
-      const uint64_t pos = __ballot(live && Pj > 0.0);
-      if (hitj) pick = plo + p0 + (__ffsll((long long)hitj) - 1);
-      if (pos) last_pos = plo + p0 + (63 - __clzll((long long)pos));
-      start += tot;
-      seen_before += __popcll(tmask);
+    const int64_t j = plo + lane;
+    const bool live = lane < FE;
+    const uint64_t pm = sh.ptmask;
+    double Pj = live ? (double)sh.pw[lane] : 0.0;
+    if (live && ((pm >> lane) & 1ull)) {
+      const int32_t seen = __popcll(pm & ((1ull << lane) - 1ull));
+      Pj = (int64_t)sh.ptb + seen < (int64_t)rs.ktie ? P_cut : 0.0;
     }
-    if (pick < 0) pick = last_pos;  // rounding: the last id with mass
+    if (live && use_r)
+      for (int l = 0; l < a.K; ++l)
+        if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
+    double wlo, whi;
+    wave_tiles(Pj, wlo, whi);
+    const uint64_t hitj = __ballot(live && Pj > 0.0 && sh.pick_lo + whi > thr);
+    const uint64_t pos = __ballot(live && Pj > 0.0);
+    int64_t pick = -1;
+    if (hitj)
+      pick = plo + (__ffsll((long long)hitj) - 1);
+    else if (pos)
+      pick = plo + (63 - __clzll((long long)pos));  // rounding: the last id with mass
     if (lane == 0 && pick >= 0) sh.bonus = pick;
   }
   __syncthreads();
@@ -492,14 +554,14 @@ struct MergeShared {
 
 template <int DT>
 __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, int s, int mode, float T, MergeShared& ms,
-                                          DrawShared& ds, RowSum* srs) {
+                                          DrawShared& ds, const RowPre& pre, RowSum* srs) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int C = P.C;
-  const ChunkStat* cs = P.cstat + r * C;
+  const ChunkStat* cs = pre.cs;
   int kk = 0;
   if (mode == M_LIST) {
-    const int K = a.top_ks[b] < 1 ? 1 : a.top_ks[b];
+    const int K = pre.top_k < 1 ? 1 : pre.top_k;
     if (tid == 0) {
       int o = 0;
       for (int c = 0; c < C; ++c) {
@@ -508,14 +570,29 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
       }
       ms.off[C] = o;
     }
-    __syncthreads();
-    const int n_all = ms.off[C];
-    for (int c = 0; c < C; ++c) {
-      const int o = ms.off[c], nc = ms.off[c + 1] - o;
-      const uint64_t* src = P.cand + (r * C + c) * (int64_t)P.kcand;
-      for (int i = tid; i < nc; i += CT) ms.buf[o + i] = src[i];
+    // every chunk's candidate slots, loaded together (in-bounds addresses, unused slots dropped)
+    const int kc = P.kcand, nslot = C * kc;
+    const uint64_t* src = P.cand + r * (int64_t)nslot;
+    constexpr int CU = 4;
+    for (int base = 0; base < nslot; base += CT * CU) {
+      uint64_t v[CU];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) {
+        const int idx = base + u * CT + tid;
+        v[u] = src[idx < nslot ? idx : nslot - 1];
+      }
+      if (base == 0) __syncthreads();  // ms.off
+#pragma unroll
+      for (int u = 0; u < CU; ++u) {
+        const int idx = base + u * CT + tid;
+        if (idx < nslot) {
+          const int c = idx / kc, i = idx - c * kc;
+          if (i < ms.off[c + 1] - ms.off[c]) ms.buf[ms.off[c] + i] = v[u];
+        }
+      }
     }
     __syncthreads();
+    const int n_all = ms.off[C];
     // rank of each candidate among the row's candidates (values are distinct)
     for (int i = tid; i < n_all; i += CT) {
       const uint64_t v = ms.buf[i];
@@ -543,7 +620,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   const uint64_t at_max = __ballot(lane < C && m_l == M);
   int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
   if (arg == INT_MAX) arg = 0;  // every value is -inf: the first id
-  const int64_t tok = step_token(a, b, s);
+  const int64_t tok = pre.tok;
   RowSum rs;
   rs.mode = mode;
   rs.argmax = arg;
@@ -563,7 +640,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   if (mode == M_GREEDY) {
     rs.nlist = 1;
     rs.p_draft = tok == arg ? 1.f : 0.f;
-    const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
+    const int32_t ok = tok >= 0 ? step_accept_lds(ds, a.K, tok, rs.p_draft, pre.u) : 0;
     if (lane == 0) {
       list[0] = ListEntry{arg, 1.f};
       P.rowsum[r] = rs;
@@ -605,15 +682,15 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     const float p = live ? prob_of(value_of_key<DT>(unpack_key(pk)), T, m_f, invZ) : 0.f;
     double lo_p, hi_p;
     const double S_all = wave_tiles((double)p, lo_p, hi_p);
-    const float top_p = a.top_ps[b];
-    const float min_p = a.min_ps ? a.min_ps[b] : 0.f;
-    bool keep = live && lane < a.top_ks[b] && !topp_fails(a.backend, lo_p, p, top_p);
+    const float top_p = pre.top_p;
+    const float min_p = pre.min_p;
+    bool keep = live && lane < pre.top_k && !topp_fails(a.backend, lo_p, p, top_p);
     if (a.need_min_p) {
       if (a.backend == DSV_BACKEND_FLASHINFER) {
         // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
         double lo_a, hi_a;
         wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
-        keep = live && lane < a.top_ks[b] && lo_a <= (double)top_p;
+        keep = live && lane < pre.top_k && lo_a <= (double)top_p;
       }
       const float thr = __shfl(p, 0, WAVE) * min_p;
       if (p < thr) keep = false;
@@ -636,7 +713,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     rs.nlist = __popcll(__ballot(keep));
     if (lane == 0) ds.nlist = rs.nlist;
   }
-  const int32_t ok = tok >= 0 ? step_accept_wave(a, b, s, tok, rs.p_draft) : 0;
+  const int32_t ok = tok >= 0 ? step_accept_lds(ds, a.K, tok, rs.p_draft, pre.u) : 0;
   if (lane == 0) {
     P.rowsum[r] = rs;
     *srs = rs;
@@ -673,10 +750,12 @@ struct NucMergeShared {
 // p of a nucleus row at its draft token and the step decision; RowSum out (wave 0).
 template <int DT>
 __device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int b, int s, RowSum rs, float T,
-                                               float xtok, int64_t tok, int64_t tie_tok, RowSum* srs) {
+                                               float xtok, int64_t tok, int64_t tie_tok, RowSum* srs,
+                                               const DrawShared* fq = nullptr, float coin = 0.f) {
   const bool kept = key_of<DT>(xtok) > rs.vcut || (key_of<DT>(xtok) == rs.vcut && tie_tok < (int64_t)rs.ktie);
   rs.p_draft = (tok >= 0 && tok < P.a.vocab && kept) ? prob_of(xtok, T, rs.m_f, rs.invZ) / rs.S_f : 0.f;
-  const int32_t ok = tok >= 0 ? step_accept_wave(P.a, b, s, tok, rs.p_draft) : 0;
+  int32_t ok = 0;
+  if (tok >= 0) ok = fq ? step_accept_lds(*fq, P.a.K, tok, rs.p_draft, coin) : step_accept_wave(P.a, b, s, tok, rs.p_draft);
   if (threadIdx.x == 0) {
     P.rowsum[r] = rs;
     if (srs) *srs = rs;
@@ -686,12 +765,12 @@ __device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int 
 
 template <int DT>
 __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh,
-                                              DrawShared& ds, RowSum* srs) {
+                                              DrawShared& ds, const RowPre& pre, RowSum* srs) {
   constexpr int NW = CT / WAVE;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   const int C = P.C;
-  const ChunkStat* cs = P.cstat + r * C;
+  const ChunkStat* cs = pre.cs;
   float m_l = -INFINITY;
   int32_t arg_l = INT_MAX;
   double s_l = 0.0;
@@ -720,10 +799,10 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     sh.cw[tid] = w_l;
     sh.ck[tid] = w_l != WIN_EMPTY ? key_of<DT>(m_l) : 0u;
   }
-  const float top_p = a.top_ps[b];
-  const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
-  const int topk = a.top_ks[b];
-  const int64_t tok = step_token(a, b, s);
+  const float top_p = pre.top_p;
+  const float min_p = a.need_min_p ? pre.min_p : 0.f;
+  const int topk = pre.top_k;
+  const int64_t tok = pre.tok;
   if (tid == 0) {
     const double eps = (Z * (double)invZ - (double)top_p - 1e-6) / (double)a.vocab;
     uint32_t kb = 0x80u;  // the lowest finite key: no floor
@@ -774,12 +853,20 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   for (int q = tid; q < W; q += CT) {
     const uint32_t k = kmax - (uint32_t)q;
     uint32_t cnt = 0;
-    for (int c = 0; c < C; ++c) {
-      const uint32_t wl = sh.cw[c];
-      if (wl == WIN_EMPTY || k < wl || k > sh.ck[c]) continue;
-      const uint32_t o = k - wl;
-      const uint32_t word = P.hpart[(r * C + c) * (int64_t)(HWIN / 2) + (o >> 1)];
-      cnt += (word >> ((o & 1u) * 16u)) & 0xFFFFu;
+    for (int c0 = 0; c0 < C; c0 += 8) {  // eight chunks' words loaded together (in-bounds addresses)
+      uint32_t word[8], o[8];
+      bool in[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + u;
+        const uint32_t wl = c < C ? sh.cw[c] : WIN_EMPTY;
+        in[u] = wl != WIN_EMPTY && k >= wl && k <= sh.ck[c < C ? c : 0];
+        o[u] = in[u] ? k - wl : 0u;
+        word[u] = P.hpart[(r * C + (c < C ? c : 0)) * (int64_t)(HWIN / 2) + (o[u] >> 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (in[u]) cnt += (word[u] >> ((o[u] & 1u) * 16u)) & 0xFFFFu;
     }
     sh.h[q] = cnt;
   }
@@ -907,10 +994,19 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     if (wl != WIN_EMPTY) {
       const uint32_t k0 = rs.vcut + 1u > wl ? rs.vcut + 1u : wl;
       const uint32_t* hp = P.hpart + (r * C + c) * (int64_t)(HWIN / 2);
-      for (uint32_t k = k0 + (uint32_t)lane; k <= kh; k += WAVE) {
-        const uint32_t o = k - wl;
-        const uint32_t cnt = (hp[o >> 1] >> ((o & 1u) * 16u)) & 0xFFFFu;
-        if (cnt) mc += (double)cnt * (double)bp(value_of_key<DT>(k));
+      for (uint32_t k1 = k0 + (uint32_t)lane; k1 <= kh; k1 += 4 * WAVE) {  // four keys a lane together
+        uint32_t word[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t k = k1 + (uint32_t)(u * WAVE);
+          word[u] = hp[(k <= kh ? k - wl : 0u) >> 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t k = k1 + (uint32_t)(u * WAVE);
+          const uint32_t cnt = k <= kh ? (word[u] >> (((k - wl) & 1u) * 16u)) & 0xFFFFu : 0u;
+          if (cnt) mc += (double)cnt * (double)bp(value_of_key<DT>(k));
+        }
       }
       if (lane == 0 && rs.vcut >= wl && rs.vcut <= kh) {
         const uint32_t o = rs.vcut - wl;
@@ -945,7 +1041,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       }
     }
     tie_tok = wave_sum(tie_tok);
-    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok, srs);
+    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok, srs, &ds, pre.u);
   }
 }
 
@@ -1672,12 +1768,14 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
   __shared__ MergeShared ms;
   __shared__ NucMergeShared ns;
   __shared__ DrawShared ds;
+  __shared__ RowPre pre;
   __shared__ RowSum srs;
   const dsv_verify_args& a = P.a;
   const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   int b, s;
   if (!row_request(a, r, b, s)) {
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
       P.rowsum[r].mode = M_SKIP;
       P.step_ok[r] = 0;
     }
@@ -1685,29 +1783,44 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
   }
   const int mode = row_mode(a, b, 0);
   const float T = a.temperatures[b];
+  const int cap = req_cap(a, b);
+  const bool resid = s < cap - 1;  // the row tests draft s+1, and ends the prefix when it is rejected
+  const bool tests = a.candidates != nullptr && resid;
+  // one round of reads before the merge: the chunk statistics (wave 0), the draft token, its
+  // coin and q lanes, and for dense rows the adjusted logits at the q ids (wave 1)
+  if (tid < WAVE) {
+    if (lane < P.C) pre.cs[lane] = P.cstat[r * P.C + lane];
+    if (lane == 0) {
+      pre.tok = tests ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
+      pre.u = tests ? a.uniforms[(int64_t)b * (a.T - 1) + s] : 0.f;
+      pre.uf = a.candidates ? a.uniform_final[b] : 0.f;
+      pre.top_p = a.top_ps ? a.top_ps[b] : 1.f;
+      pre.min_p = a.min_ps ? a.min_ps[b] : 0.f;
+      pre.top_k = a.top_ks[b];
+    }
+  } else if (tid < 2 * WAVE) {
+    fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds);
+  }
+  __syncthreads();
   if (mode == M_HIST) {
-    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, T, ns, ds, &srs);
+    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &srs);
   } else {
-    merge_row<DT>(P, r, b, s, mode, T, ms, ds, &srs);
+    merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &srs);
   }
   if (!a.candidates) return;  // target-distribution entry: no draw
   __syncthreads();
   // the bonus token this row gives when it is the request's accepted length (k_final picks it)
   const RowSum rs = srs;
-  const int cap = req_cap(a, b);
-  const bool resid = s < cap - 1;  // row s ends the prefix when draft s+1 is rejected
   int64_t bonus;
   if (rs.mode == M_GREEDY) {
     bonus = rs.argmax;
   } else if (rs.mode == M_LIST) {
-    stage_q(a, b, s, resid, ds);
-    bonus = threadIdx.x < WAVE ? list_draw(a, resid, a.uniform_final[b], ds) : 0;
+    bonus = tid < WAVE ? list_draw(a, resid, pre.uf, ds) : 0;
   } else if (rs.flags & FLAG_FULL_HIST) {
     bonus = BONUS_LATER;
   } else {
     // the chunk and threshold; k_final scans the chunk when this row is the accepted one
-    stage_q(a, b, s, resid, ds);
-    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, resid, a.uniform_final[b], ds);
+    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, resid, pre.uf, ds, true);
     DrawPlan* pl = P.plans + r;
     if (threadIdx.x < QMAX) pl->qd[threadIdx.x] = ds.qd[threadIdx.x];
     if (threadIdx.x == 0) {
@@ -1782,19 +1895,26 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     return;
   }
   if (row0 + cap > a.rows) cap = (int)(a.rows - row0);
-  if (tid < WAVE) {  // the first rejected step
+  if (tid < WAVE) {
+    // the first rejected step (the last row ends every prefix) and the bonus its row drew, read
+    // together
     int acc = cap - 1;
-    for (int s0 = 0; s0 < cap - 1; s0 += WAVE) {
+    int64_t drawn = 0;
+    for (int s0 = 0; s0 < cap; s0 += WAVE) {
       const int s = s0 + lane;
-      const uint64_t rej = __ballot(s < cap - 1 && P.step_ok[row0 + s] == 0);
-      if (rej) {
-        acc = s0 + __ffsll((long long)rej) - 1;
+      const int32_t ok = s < cap - 1 ? P.step_ok[row0 + s] : 0;
+      const int64_t rb = s < cap ? P.rbonus[row0 + s] : 0;
+      const uint64_t end = __ballot(s < cap && ok == 0);
+      if (end) {
+        const int l = __ffsll((long long)end) - 1;
+        acc = s0 + l;
+        drawn = __shfl(rb, l, WAVE);
         break;
       }
     }
     if (tid == 0) {
       sh.acc = acc;
-      sh.bonus = P.rbonus[row0 + acc];
+      sh.bonus = drawn;
     }
   }
   __syncthreads();
@@ -1802,18 +1922,34 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   int64_t bonus = sh.bonus;
   if (bonus == BONUS_PLAN) {  // the row merge planned the draw: scan the chunk
     const int64_t rstar = row0 + acc;
-    const RowSum rs = P.rowsum[rstar];
     const bool resid = acc < cap - 1;
-    stage_q(a, b, acc, resid, sh);
     const DrawPlan* pl = P.plans + rstar;
-    if (tid < QMAX) sh.qd[tid] = pl->qd[tid];
-    if (tid == 0) {
-      sh.thr = pl->thr;
-      sh.chunk_lo = pl->chunk_lo;
-      sh.chunk = pl->chunk;
-      sh.tieq = pl->tieq;
-      sh.use_r = pl->use_r;
+    if (tid < WAVE) {
+      // the plan and the q lanes of the rejected draft in one round (dense_pick's first barrier
+      // publishes them): ids, clamped values, whether the lane is the last with its id
+      const int64_t qi = ((int64_t)b * (a.T - 1) + acc) * a.K;
+      const bool on = resid && lane < a.K;
+      const int64_t qid = on ? load_index(a.q_ids, a.q_ids_i64, qi + lane) : -1;
+      const float qv = on ? clamp01(a.q_values[qi + lane]) : 0.f;
+      const double qd = pl->qd[lane];
+      if (lane == 0) {
+        sh.thr = pl->thr;
+        sh.chunk_lo = pl->chunk_lo;
+        sh.chunk = pl->chunk;
+        sh.tieq = pl->tieq;
+        sh.use_r = pl->use_r;
+      }
+      sh.qid[lane] = qid;
+      sh.qv[lane] = qv;
+      sh.qd[lane] = qd;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      bool last = qid >= 0 && qid < V;
+      for (int l2 = lane + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != qid;
+      sh.qlast[lane] = last;
     }
+    const RowSum rs = P.rowsum[rstar];
     bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, a.temperatures[b], sh);
   } else if (bonus == BONUS_LATER) {
     const int64_t rstar = row0 + acc;
