@@ -73,46 +73,96 @@ __device__ __forceinline__ float exp_fast(float x) {
 // ---------------------------------------------------------------------------------------
 // Wave / block reductions (wave64).
 // ---------------------------------------------------------------------------------------
+// Lane moves through DPP (gfx9 controls): quad permutes, row shifts / mirrors, row broadcasts
+// and the whole-wave shift.  They run in the VALU, not through the LDS crossbar.
+enum : int {
+  DPP_QUAD_XOR1 = 0xB1,        // quad_perm [1, 0, 3, 2]
+  DPP_QUAD_XOR2 = 0x4E,        // quad_perm [2, 3, 0, 1]
+  DPP_ROW_SHR1 = 0x111,
+  DPP_ROW_SHR2 = 0x112,
+  DPP_ROW_SHR4 = 0x114,
+  DPP_ROW_SHR8 = 0x118,
+  DPP_WAVE_SHR1 = 0x138,
+  DPP_ROW_MIRROR = 0x140,
+  DPP_ROW_HALF_MIRROR = 0x141,
+  DPP_ROW_BCAST15 = 0x142,
+  DPP_ROW_BCAST31 = 0x143,
+};
+
+// Lane value moved by CTRL.  Lanes of disabled rows (ROWS mask) keep `old`; lanes whose source
+// lies outside the pattern's range read 0 with ZERO, else keep `old`.
+template <int CTRL, int ROWS = 0xF, bool ZERO = false, typename T>
+__device__ __forceinline__ T dpp(T old, T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                             CTRL, ROWS, 0xF, ZERO));
+  } else {
+    const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)o, (int)(uint32_t)x, CTRL, ROWS, 0xF, ZERO);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(o >> 32), (int)(uint32_t)(x >> 32), CTRL,
+                                                              ROWS, 0xF, ZERO);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
+// The value of lane L (uniform).
+template <int L, typename T>
+__device__ __forceinline__ T readlane(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
+  } else {
+    const uint64_t x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, L);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), L);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
+// Reduction over the 64 lanes (every lane active), result in every lane: quads, half rows and
+// rows through DPP, then the four row results in a fixed order.
+template <typename T, class F>
+__device__ __forceinline__ T wave_reduce(T v, F op) {
+  v = op(v, dpp<DPP_QUAD_XOR1>(v, v));
+  v = op(v, dpp<DPP_QUAD_XOR2>(v, v));
+  v = op(v, dpp<DPP_ROW_HALF_MIRROR>(v, v));
+  v = op(v, dpp<DPP_ROW_MIRROR>(v, v));
+  return op(op(readlane<0>(v), readlane<16>(v)), op(readlane<32>(v), readlane<48>(v)));
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+  return wave_reduce(v, [](T x, T y) { return x + y; });
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t w = __shfl_xor(v, o, WAVE);
-    v = w > v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor(v, o, WAVE);
-    v = w > v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, [](uint64_t x, uint64_t y) { return x > y ? x : y; });
 }
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor(v, o, WAVE);
-    v = w < v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, [](uint64_t x, uint64_t y) { return x < y ? x : y; });
 }
-// Inclusive prefix sum over lanes 0..63.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
+}
+// Inclusive prefix sum over lanes 0..63 (every lane active): row scans by shifts, then the row
+// totals carried into the rows above.
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T v) {
-  const int lane = threadIdx.x & (WAVE - 1);
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    T w = __shfl_up(v, o, WAVE);
-    if (lane >= o) v += w;
-  }
+  v += dpp<DPP_ROW_SHR1, 0xF, true>(T(0), v);
+  v += dpp<DPP_ROW_SHR2, 0xF, true>(T(0), v);
+  v += dpp<DPP_ROW_SHR4, 0xF, true>(T(0), v);
+  v += dpp<DPP_ROW_SHR8, 0xF, true>(T(0), v);
+  v += dpp<DPP_ROW_BCAST15, 0xA>(T(0), v);
+  v += dpp<DPP_ROW_BCAST31, 0xC>(T(0), v);
   return v;
+}
+// The value of the lane below (lane 0: `first`).
+template <typename T>
+__device__ __forceinline__ T wave_prev(T v, T first) {
+  return dpp<DPP_WAVE_SHR1, 0xF, false>(first, v);
 }
 
 // Block-wide reductions over NW waves (the block size / 64, a compile-time constant so that

@@ -549,18 +549,16 @@ __device__ __forceinline__ double block_tiles(double v, double* scratch, double&
     tot += scratch[i];
   }
   hi = base + incl;
-  const double prev = __shfl_up(hi, 1, WAVE);
-  lo = lane == 0 ? base : prev;
+  lo = wave_prev(hi, base);
+  (void)lane;
   return tot;
 }
 
 // The same over the lanes of one wave (values of lanes >= n count as zero).
 __device__ __forceinline__ double wave_tiles(double v, double& lo, double& hi) {
-  const int lane = threadIdx.x & (WAVE - 1);
   hi = wave_incl_scan(v);
-  const double prev = __shfl_up(hi, 1, WAVE);
-  lo = lane == 0 ? 0.0 : prev;
-  return __shfl(hi, WAVE - 1, WAVE);
+  lo = wave_prev(hi, 0.0);
+  return readlane<WAVE - 1>(hi);
 }
 
 }  // namespace dsv

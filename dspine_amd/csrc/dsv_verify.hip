@@ -256,6 +256,7 @@ struct RowPre {
   float u;      // its coin
   float uf;     // the request's bonus coin
   float top_p, min_p;
+  float pres, rep;  // the request's penalties (0 and 1 without a history)
   int32_t top_k;
 };
 
@@ -334,15 +335,14 @@ struct DrawPlan {
 // tieq, use_r, qd).
 template <int DT, bool ALIGNED, int NT>
 __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
-                                           bool resid, float uf, DrawShared& sh, bool have_qx = false) {
+                                           float pres, float rep, bool resid, float uf, DrawShared& sh,
+                                           bool have_qx = false) {
   constexpr int NW = NT / WAVE;
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int C = P.C;
   const bool pen = P.pbits != nullptr;
-  const float pres = pen && a.presence ? a.presence[b] : 0.f;
-  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
   const bool hist = rs.mode == M_HIST;
   const BonusP bp = bonus_p<DT>(rs, T);
   const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
@@ -441,16 +441,13 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
 // mass holds the threshold, then its ids.  Returns the token (every thread).
 template <int DT, bool ALIGNED, int NT>
 __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
-                                              DrawShared& sh) {
+                                              float pres, float rep, DrawShared& sh) {
   constexpr int NW = NT / WAVE;
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
   static_assert(FE <= 64, "a thread's span fits a 64-bit mask");
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
-  const bool pen = P.pbits != nullptr;
-  const float pres = pen && a.presence ? a.presence[b] : 0.f;
-  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
   const bool hist = rs.mode == M_HIST;
   const BonusP bp = bonus_p<DT>(rs, T);
   const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
@@ -1797,6 +1794,8 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
       pre.top_p = a.top_ps ? a.top_ps[b] : 1.f;
       pre.min_p = a.min_ps ? a.min_ps[b] : 0.f;
       pre.top_k = a.top_ks[b];
+      pre.pres = P.pbits && a.presence ? a.presence[b] : 0.f;
+      pre.rep = P.pbits && a.repetition ? a.repetition[b] : 1.f;
     }
   } else if (tid < 2 * WAVE) {
     fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds);
@@ -1820,7 +1819,7 @@ __global__ __launch_bounds__(CT) void k_merge(KParams P) {
     bonus = BONUS_LATER;
   } else {
     // the chunk and threshold; k_final scans the chunk when this row is the accepted one
-    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, resid, pre.uf, ds, true);
+    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, pre.pres, pre.rep, resid, pre.uf, ds, true);
     DrawPlan* pl = P.plans + r;
     if (threadIdx.x < QMAX) pl->qd[threadIdx.x] = ds.qd[threadIdx.x];
     if (threadIdx.x == 0) {
@@ -1895,6 +1894,12 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     return;
   }
   if (row0 + cap > a.rows) cap = (int)(a.rows - row0);
+  // the request's parameters for a dense draw, read with the step decisions
+  const float T = a.temperatures[b];
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const float uf = a.uniform_final[b];
   if (tid < WAVE) {
     // the first rejected step (the last row ends every prefix) and the bonus its row drew, read
     // together
@@ -1950,17 +1955,13 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       sh.qlast[lane] = last;
     }
     const RowSum rs = P.rowsum[rstar];
-    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, a.temperatures[b], sh);
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh);
   } else if (bonus == BONUS_LATER) {
     const int64_t rstar = row0 + acc;
     const RowSum rs = P.rowsum[rstar];
-    const float T = a.temperatures[b];
     const bool resid = acc < cap - 1;
     stage_q(a, b, acc, resid, sh);
     const char* rowp = row_ptr(a, rstar);
-    const bool pen = P.pbits != nullptr;
-    const float pres = pen && a.presence ? a.presence[b] : 0.f;
-    const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
     const BonusP bp = bonus_p<DT>(rs, T);
     for (int c = 0; c < P.C; ++c) {  // chunk masses: a scan of every chunk
       double m = 0.0;
@@ -1980,8 +1981,8 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       }
     }
     __syncthreads();
-    dense_plan<DT, ALIGNED, FCT>(P, b, rowp, rs, T, resid, a.uniform_final[b], sh);
-    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, sh);
+    dense_plan<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, resid, uf, sh);
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh);
     (void)CHE;
   }
   write_outputs(a, b, acc, bonus);
