@@ -43,6 +43,7 @@ struct KParams {
   uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
   uint32_t* hpart;        // [rows, C, HWIN / 2]: nucleus rows' per-chunk window counts (16-bit pairs)
   uint32_t* nhist;        // [NUC_GRID, 65536]: full-histogram counts, one area per k_nuc workgroup
+  int32_t* nuc_rows;      // [rows + 1]: the number of full-histogram rows, then their ids
   int64_t pwords;
   int32_t C;              // chunks per row
   int32_t kcand;          // candidate slots per chunk
@@ -839,6 +840,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       P.rowsum[r] = rs;
       *srs = rs;
       P.step_ok[r] = 0;
+      P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
     }
     return;
   }
@@ -953,6 +955,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       P.rowsum[r] = rs;
       *srs = rs;
       P.step_ok[r] = 0;
+      P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
     }
     return;
   }
@@ -1058,9 +1061,6 @@ struct NucShared {
   int64_t wc[NUC_WAVES];
   uint64_t cut[NUC_WAVES];  // (tie << 32 | key) of each wave's first cut key, ~0 if none
   double cutS[NUC_WAVES];
-  int32_t ri[NUC_WAVES];
-  int32_t mine[NUC_THREADS];  // this workgroup's rows among the current block of rows
-  int32_t nmine;
   float xtok;
   uint32_t ktok;
 };
@@ -1283,33 +1283,13 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
   __shared__ NucShared sh;
   const dsv_verify_args& a = P.a;
   uint32_t* hist = reinterpret_cast<uint32_t*>(dyn);
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
-  int64_t seen = 0;  // full-histogram rows before the current block of rows
-  for (int64_t r0 = 0; r0 < a.rows; r0 += NUC_THREADS) {
-    const int64_t r = r0 + tid;
-    bool f = false;
-    if (r < a.rows) {
-      const RowSum& rs = P.rowsum[r];
-      f = rs.mode == M_HIST && (rs.flags & FLAG_FULL_HIST);
-    }
-    const uint64_t bal = __ballot(f);
-    if (lane == 0) sh.ri[wid] = __popcll(bal);
-    if (tid == 0) sh.nmine = 0;
-    __syncthreads();
-    int64_t before = seen, total = 0;
-    for (int i = 0; i < NUC_WAVES; ++i) {
-      if (i < wid) before += sh.ri[i];
-      total += sh.ri[i];
-    }
-    const int64_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
-    if (f && rank % gridDim.x == blockIdx.x) sh.mine[atomicAdd(&sh.nmine, 1)] = (int32_t)r;
-    __syncthreads();
-    const int nm = sh.nmine;
-    for (int i = 0; i < nm; ++i) {
-      if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, sh.mine[i], hist, sh);
-    }
-    seen += total;
-    __syncthreads();
+  // the rows the merge listed (a count, then row ids; their order does not affect any row)
+  int n = P.nuc_rows[0];
+  n = n < 0 ? 0 : (n > a.rows ? (int)a.rows : n);
+  for (int i = blockIdx.x; i < n; i += gridDim.x) {
+    const int32_t row = P.nuc_rows[1 + i];
+    if (row < 0 || row >= a.rows) continue;
+    if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, row, hist, sh);
   }
 }
 
@@ -1754,6 +1734,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   if (tid == 0) {
     if (tok_here) out.xtok = s_xtok;
     *st = out;
+    if (blockIdx.x == 0 && P.nuc_rows) P.nuc_rows[0] = 0;  // the merge lists full-histogram rows
   }
 }
 
@@ -2193,7 +2174,7 @@ using namespace dsv;
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, hpart, nhist, rbonus, rties, plans, step_ok, pbits, total;
+  int64_t rowsum, lists, cstat, cand, hpart, nhist, nuc, rbonus, rties, plans, step_ok, pbits, total;
 };
 static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
   if (dtype == DSV_BF16) {
@@ -2228,6 +2209,7 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.cand, rows * C * (int64_t)kcand * 8);
   take(w.hpart, kcand ? rows * C * (int64_t)(HWIN / 2) * 4 : 0);
   take(w.nhist, kcand ? (int64_t)NUC_GRID * 65536 * 4 : 0);
+  take(w.nuc, (rows + 1) * 4);
   take(w.rbonus, rows * 8);
   take(w.rties, rows * NCHK * 4);
   take(w.plans, rows * (int64_t)sizeof(DrawPlan));
@@ -2308,6 +2290,7 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   P.cand = reinterpret_cast<uint64_t*>(ws + w.cand);
   P.hpart = reinterpret_cast<uint32_t*>(ws + w.hpart);
   P.nhist = reinterpret_cast<uint32_t*>(ws + w.nhist);
+  P.nuc_rows = reinterpret_cast<int32_t*>(ws + w.nuc);
   P.rbonus = reinterpret_cast<int64_t*>(ws + w.rbonus);
   P.rties = reinterpret_cast<int32_t*>(ws + w.rties);
   P.plans = reinterpret_cast<DrawPlan*>(ws + w.plans);
