@@ -120,6 +120,20 @@ __device__ __forceinline__ T readlane(T v) {
   }
 }
 
+// The value of lane l (l uniform across the wave).
+template <typename T>
+__device__ __forceinline__ T readlane_at(T v, int l) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  } else {
+    const uint64_t x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
 // Reduction over the 64 lanes (every lane active), result in every lane: quads, half rows and
 // rows through DPP, then the four row results in a fixed order.
 template <typename T, class F>

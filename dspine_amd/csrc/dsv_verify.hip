@@ -154,6 +154,7 @@ struct DrawShared {
   float qraw[QMAX];     // q of the lane as given (the draft test sums these)
   int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
   int32_t qrank[QMAX];  // q id at a split cut key: values at the cut key before it (id order), else -1
+  int32_t qc[QMAX];     // chunk of a residual q id (last lane with its id), else -1
   float qx[QMAX];       // adjusted value at the q id
   double qd[QMAX];      // P - max(P - q, 0) at a q id (the residual's reduction), else 0
   double cm[NCHK];      // chunk masses of P above the cut (every id of an unfiltered row)
@@ -319,7 +320,7 @@ __device__ __forceinline__ int64_t list_draw(const dsv_verify_args& a, bool resi
   if (!resid || !(mass > 0.0)) mass = wave_tiles(Pi, lo, hi);
   const double thr = (double)uf * mass;
   const uint64_t hit = __ballot(live && lo <= thr && thr < hi);
-  return hit ? __shfl((int64_t)e.id, __ffsll((long long)hit) - 1, WAVE) : a.vocab - 1;
+  return hit ? readlane_at((int64_t)e.id, __ffsll((long long)hit) - 1) : a.vocab - 1;
 }
 
 // What a dense row's draw needs after the chunk is known (the row merge writes it; k_final
@@ -362,6 +363,7 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
     if (lane < QMAX) {
       sh.qx[lane] = xq;
       sh.qrank[lane] = (qlive && tie_cut && key_of<DT>(xq) == rs.vcut) ? 0 : -1;
+      sh.qc[lane] = qlive ? (int32_t)(sh.qid[lane] / CHE) : -1;
     }
   }
   __syncthreads();
@@ -395,13 +397,7 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // lanes hold the chunks: masses with the kept values at the cut key, then the residual's
     const int32_t ctl = lane < C ? sh.ct[lane] : 0;
-    int32_t tie_prefix = ctl;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int32_t t = __shfl_up(tie_prefix, o, WAVE);
-      if (lane >= o) tie_prefix += t;
-    }
-    tie_prefix -= ctl;
+    const int32_t tie_prefix = wave_incl_scan(ctl) - ctl;
     int32_t kt = 0;
     if (hist) {
       const int64_t room = (int64_t)rs.ktie - tie_prefix;
@@ -411,7 +407,7 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
     double Mr = Mp;
     if (resid && lane < C)
       for (int l = 0; l < a.K; ++l)
-        if (sh.qlast[l] && sh.qid[l] / CHE == lane) Mr -= sh.qd[l];
+        if (sh.qc[l] == lane) Mr -= sh.qd[l];
     double lo_r, hi_r, lo_p, hi_p;
     const double mr = wave_tiles(Mr, lo_r, hi_r);
     const double mp = wave_tiles(Mp, lo_p, hi_p);
@@ -613,10 +609,9 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   }
   // the row max and the first id attaining it (chunks cover increasing ids)
   float M = m_l;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+  M = wave_max_f32(M);
   const uint64_t at_max = __ballot(lane < C && m_l == M);
-  int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
+  int32_t arg = readlane_at(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0);
   if (arg == INT_MAX) arg = 0;  // every value is -inf: the first id
   const int64_t tok = pre.tok;
   RowSum rs;
@@ -690,7 +685,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
         wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
         keep = live && lane < pre.top_k && lo_a <= (double)top_p;
       }
-      const float thr = __shfl(p, 0, WAVE) * min_p;
+      const float thr = readlane<0>(p) * min_p;
       if (p < thr) keep = false;
     }
     const double Sk = wave_sum(keep ? (double)p : 0.0);
@@ -699,11 +694,11 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     rs.S_f = S_f;
     const float Pj = p / S_f;
     const uint64_t at_tok = __ballot(keep && (int64_t)id == tok);
-    rs.p_draft = at_tok ? __shfl(Pj, __ffsll((long long)at_tok) - 1, WAVE) : 0.f;
+    rs.p_draft = at_tok ? readlane_at(Pj, __ffsll((long long)at_tok) - 1) : 0.f;
     // the kept support, sorted by id
     const int32_t kid = keep ? id : INT_MAX;
     int rank = 0;
-    for (int i = 0; i < kk; ++i) rank += __shfl(kid, i, WAVE) < kid;
+    for (int i = 0; i < kk; ++i) rank += readlane_at(kid, i) < kid;
     if (keep) {
       list[rank] = ListEntry{id, Pj};
       ds.lst[rank] = ListEntry{id, Pj};
@@ -732,8 +727,10 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
 // the merged window counts decide the cut exactly; otherwise the row takes the full-histogram
 // path (k_nuc).
 // ---------------------------------------------------------------------------------------
+constexpr int HC_KEYS = 512;  // merged keys whose per-chunk counts stay in LDS (rows of <= 8 chunks)
 struct NucMergeShared {
   uint32_t h[HWIN];  // merged counts, position q = kmax - key
+  uint16_t hc[8 * HC_KEYS];  // per-chunk counts at position q (chunk c at c * HC_KEYS + q)
   uint32_t cw[16], ck[16];
   double wm[CT / WAVE];
   int64_t wc[CT / WAVE];
@@ -781,10 +778,9 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     x_l = cs[lane].kx;
   }
   float M = m_l;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+  M = wave_max_f32(M);
   const uint64_t at_max = __ballot(lane < C && m_l == M);
-  int32_t arg = __shfl(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0, WAVE);
+  int32_t arg = readlane_at(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0);
   if (arg == INT_MAX) arg = 0;
   const float c2 = log2e_over(T);
   const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
@@ -849,6 +845,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   // scanned (the first value below kb, if the scan keeps every value, is found separately).
   const uint32_t kscan = sh.kb_row > kcov ? sh.kb_row : kcov;
   const int W = (int)(kmax - kscan) + 1;  // <= HWIN: the max's own chunk window ends at kmax
+  const bool keep_hc = W <= HC_KEYS && C <= 8;  // the per-chunk counts serve the bonus masses too
   for (int q = tid; q < W; q += CT) {
     const uint32_t k = kmax - (uint32_t)q;
     uint32_t cnt = 0;
@@ -864,8 +861,11 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
         word[u] = P.hpart[(r * C + (c < C ? c : 0)) * (int64_t)(HWIN / 2) + (o[u] >> 1)];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (in[u]) cnt += (word[u] >> ((o[u] & 1u) * 16u)) & 0xFFFFu;
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t cu = in[u] ? (word[u] >> ((o[u] & 1u) * 16u)) & 0xFFFFu : 0u;
+        cnt += cu;
+        if (keep_hc && c0 == 0) sh.hc[u * HC_KEYS + q] = (uint16_t)cu;
+      }
     }
     sh.h[q] = cnt;
   }
@@ -908,13 +908,8 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     const float p = cnt ? prob_of(value_of_key<DT>(k), T, m_f, invZ) : 0.f;
     double lo_m, hi_m;
     const double it_m = wave_tiles((double)cnt * (double)p, lo_m, hi_m);
-    int64_t c_excl = cnt;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int64_t t = __shfl_up(c_excl, o, WAVE);
-      if (lane >= o) c_excl += t;
-    }
-    const int64_t it_c = __shfl(c_excl, WAVE - 1, WAVE);
+    int64_t c_excl = wave_incl_scan((int64_t)cnt);
+    const int64_t it_c = readlane<WAVE - 1>(c_excl);
     c_excl -= cnt;
     uint64_t f = ~0ull;
     double fS = 0.0;
@@ -929,8 +924,8 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     const uint64_t who = __ballot(f != ~0ull);
     if (who) {
       const int src = __ffsll((long long)who) - 1;
-      cut = __shfl(f, src, WAVE);
-      cutS = __shfl(fS, src, WAVE);
+      cut = readlane_at(f, src);
+      cutS = readlane_at(fS, src);
     }
     run_S += it_m;
     run_C += it_c;
@@ -987,6 +982,26 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   // values at the cut key.  Every key above the cut is in every window (the cut is at or above
   // kcov, or below every counted value), so the window counts hold them all.
   const BonusP bp = bonus_p<DT>(rs, T);
+  if (keep_hc && fc != ~0ull) {
+    // the cut is in the merged window: every key above it, and the cut key, are in the LDS counts
+    for (int c = wid; c < C; c += NW) {
+      double mc = 0.0;
+      int32_t tc = 0;
+      for (int q = lane; q < W; q += WAVE) {
+        const uint32_t k = kmax - (uint32_t)q;
+        const uint32_t cnt = sh.hc[c * HC_KEYS + q];
+        if (k > rs.vcut && cnt) mc += (double)cnt * (double)bp(value_of_key<DT>(k));
+        if (k == rs.vcut) tc = (int32_t)cnt;
+      }
+      mc = wave_sum(mc);
+      tc = wave_sum(tc);
+      if (lane == 0) {
+        ds.cm[c] = mc;
+        ds.ct[c] = tc;
+        P.rties[r * NCHK + c] = tc;
+      }
+    }
+  } else {
   for (int c = wid; c < C; c += NW) {
     const uint32_t wl = sh.cw[c], kh = sh.ck[c];
     double mc = 0.0;
@@ -1019,6 +1034,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       ds.ct[c] = tc;
       P.rties[r * NCHK + c] = tc;
     }
+  }
   }
   const float xt = sh.xtok;
   if (tid < WAVE) {
@@ -1211,13 +1227,8 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
     double lo_m, hi_m;
     const double it_m = wave_tiles((double)c_hi * (double)p_hi + (double)c_lo * (double)p_lo, lo_m, hi_m);
     const int64_t c_word = (int64_t)c_hi + c_lo;
-    int64_t c_excl = c_word;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int64_t t = __shfl_up(c_excl, o, WAVE);
-      if (lane >= o) c_excl += t;
-    }
-    const int64_t it_c = __shfl(c_excl, WAVE - 1, WAVE);
+    int64_t c_excl = wave_incl_scan(c_word);
+    const int64_t it_c = readlane<WAVE - 1>(c_excl);
     c_excl -= c_word;
     uint64_t f = ~0ull;
     double fS = 0.0;
@@ -1243,8 +1254,8 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
     const uint64_t who = __ballot(f != ~0ull);
     if (who) {
       const int src = __ffsll((long long)who) - 1;
-      cut = __shfl(f, src, WAVE);
-      cutS = __shfl(fS, src, WAVE);
+      cut = readlane_at(f, src);
+      cutS = readlane_at(fS, src);
     }
     run_S += it_m;
     run_C += it_c;
@@ -1742,7 +1753,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 // k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0)
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT) void k_merge(KParams P) {
+__global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   __shared__ MergeShared ms;
   __shared__ NucMergeShared ns;
   __shared__ DrawShared ds;
@@ -1894,7 +1905,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       if (end) {
         const int l = __ffsll((long long)end) - 1;
         acc = s0 + l;
-        drawn = __shfl(rb, l, WAVE);
+        drawn = readlane_at(rb, l);
         break;
       }
     }
