@@ -5,7 +5,9 @@ Workload (the headline configuration): 64 requests x 17 rows x 151936 vocab bf16
 per-request temperature {0, 0.6, 1.0}, top-k {off, 20}, top-p {1.0, 0.95}, presence/repetition
 penalties over a 512-token history, sparse draft q [64, 16, 16], int32 page table.  One step =
 logit adjustments -> target distribution -> chain rejection -> residual resample -> accepted-prefix
-compaction + KV-slot gather, on inputs already resident in HBM, replayed from a HIP graph.
+compaction + KV-slot gather, on inputs already resident in HBM.  K steps are timed as plain stream
+launches and as HIP-graph replays (each bracketed by device synchronisation); the faster is the
+step time.
 
 Prints ONE JSON line (metric: verified rows/s) with the roofline of the dominant kernel -- the
 chunk pass k_chunk, which reads every logit once; its launches are bracketed by HIP events on
