@@ -1287,6 +1287,288 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   __syncthreads();
 }
 
+// ---------------------------------------------------------------------------------------
+// Float32 nucleus rows: the cut by a radix descent over the 32-bit value keys.  Level 0 bins the
+// keys' top 11 bits over the row, level 1 the next 11 bits inside one level-0 bin, level 2 the
+// last 10 bits inside one level-1 bin (exact keys).  Level 0 / 1 bins carry value counts and
+// masses in fixed point (p scaled by 2^62, integer sums: independent of the order of the
+// additions).  The cut test of a key gets stronger as the key falls (more values and mass ahead,
+// smaller p), so a bin can hold the cut only when the test holds at its smallest key, which is
+// bounded with the bin's lowest possible p; the first such bin (descending), or failing that
+// the next non-empty bin, holds the cut.  Each bin searched costs one pass over the row.
+// ---------------------------------------------------------------------------------------
+constexpr int F32_BINS = 2048, F32_KEYS = 1024;
+constexpr double FX_ONE = 4611686018427387904.0;  // 2^62
+constexpr uint32_t F32_NEG_INF_KEY = 0x007FFFFFu;  // key of -inf; keys at or below it hold no value
+struct F32NucLds {
+  uint32_t cnt[2][F32_BINS];
+  uint64_t mass[2][F32_BINS];
+  uint32_t pcnt[2][F32_BINS];   // values in the bins above (descending bin order)
+  uint64_t pmass[2][F32_BINS];  // their mass
+  uint32_t cnt3[F32_KEYS];
+};
+struct F32NucShared {
+  uint64_t u[NUC_WAVES], v[NUC_WAVES];
+  double d[NUC_WAVES];
+  int32_t best;
+  uint32_t cut_key;
+  int32_t cut_tie;
+  double cut_S;
+};
+
+// One pass over the row: counts (and, levels 0 and 1, masses) of the values whose key matches the
+// level's prefix.  Level 0 also counts the values at the draft token's key before the token.
+template <bool ALIGNED>
+__device__ __forceinline__ void f32_pass(const KParams& P, int b, const char* rowp, float pres, float rep, float T,
+                                         float m_f, float invZ, int level, uint32_t prefix, F32NucLds& L,
+                                         uint32_t ktok, int64_t tok, uint32_t& tie_before) {
+  const int tid = threadIdx.x;
+  const int64_t V = P.a.vocab;
+  const bool pen = P.pbits != nullptr;
+  uint32_t* cnt = level == 2 ? L.cnt3 : L.cnt[level];
+  uint64_t* mass = level == 2 ? nullptr : L.mass[level];
+  const int nb = level == 2 ? F32_KEYS : F32_BINS;
+  for (int i = tid; i < nb; i += NUC_THREADS) {
+    cnt[i] = 0u;
+    if (mass) mass[i] = 0ull;
+  }
+  __syncthreads();
+  auto count = [&](float x, int64_t j) {
+    const uint32_t k = f32_key(x);
+    if (k <= F32_NEG_INF_KEY) return;
+    uint32_t bin;
+    if (level == 0) {
+      bin = k >> 21;
+      tie_before += (k == ktok && j < tok) ? 1u : 0u;
+    } else if (level == 1) {
+      if ((k >> 21) != prefix) return;
+      bin = (k >> 10) & (F32_BINS - 1);
+    } else {
+      if ((k >> 10) != prefix) return;
+      bin = k & (F32_KEYS - 1);
+    }
+    atomicAdd(&cnt[bin], 1u);
+    if (mass) atomicAdd((unsigned long long*)&mass[bin], (unsigned long long)((double)prob_of(x, T, m_f, invZ) * FX_ONE));
+  };
+  constexpr int U = 4;
+  const int64_t ve = ALIGNED ? V / 4 : (V + 3) / 4;
+  for (int64_t q0 = 0; q0 < ve; q0 += (int64_t)NUC_THREADS * U) {
+    uint4 w[U];
+    uint32_t bits[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
+      if constexpr (ALIGNED)
+        w[u] = load_vec_raw(rowp, vi < ve ? vi : ve - 1);
+      else
+        w[u] = load_vec<DSV_F32>(rowp, vi, V, false);
+      const uint32_t bw = pen ? pen_bits(P, b, (vi < ve ? vi : 0) * 4, 4) : 0u;
+      bits[u] = vi < ve ? bw : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t vi = q0 + (int64_t)u * NUC_THREADS + tid;
+      if (vi >= ve) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t j = vi * 4 + e;
+        float x = vec_elem<DSV_F32>(w[u], e);
+        if ((bits[u] >> e) & 1u) x = penalize<DSV_F32>(x, pres, rep);
+        if (ALIGNED || j < V) count(x, j);
+      }
+    }
+  }
+  if (ALIGNED && tid == 0)
+    for (int64_t j = ve * 4; j < V; ++j) {  // the row's partial last vector
+      float x = load_elem<DSV_F32>(rowp, j);
+      if (pen && pen_test(P, b, j)) x = penalize<DSV_F32>(x, pres, rep);
+      count(x, j);
+    }
+  __syncthreads();
+}
+
+// Exclusive prefixes of a level's bins in descending bin order (thread t owns bins 2047 - 4t ..
+// 2044 - 4t, highest first).
+__device__ __forceinline__ void f32_prefix(F32NucLds& L, int level, F32NucShared& sh) {
+  const int tid = threadIdx.x;
+  uint64_t c = 0, m = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int bin = F32_BINS - 1 - 4 * tid - e;
+    L.pcnt[level][bin] = (uint32_t)c;
+    L.pmass[level][bin] = m;
+    c += L.cnt[level][bin];
+    m += L.mass[level][bin];
+  }
+  uint64_t tc = 0, tm = 0;
+  const uint64_t cb = block_excl_scan<NUC_WAVES>(c, sh.u, &tc);
+  const uint64_t mb = block_excl_scan<NUC_WAVES>(m, sh.v, &tm);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int bin = F32_BINS - 1 - 4 * tid - e;
+    L.pcnt[level][bin] += (uint32_t)cb;
+    L.pmass[level][bin] += mb;
+  }
+  __syncthreads();
+}
+
+// The first non-empty bin of a level after descending rank `after` (rank = 2047 - bin) -- with
+// `test`, the first one that can hold the cut given the values and mass ahead of the level
+// (base_c, base_m).  Returns the bin, -1 for none.
+__device__ __forceinline__ int f32_next(const F32NucLds& L, int level, int after, bool test, uint32_t prefix,
+                                        uint64_t base_c, uint64_t base_m, float T, float m_f, float invZ, int backend,
+                                        int topk, float min_p, float thr_minp, float top_p, F32NucShared& sh) {
+  const int tid = threadIdx.x;
+  if (tid == 0) sh.best = INT_MAX;
+  __syncthreads();
+  int best = INT_MAX;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int rank = 4 * tid + e, bin = F32_BINS - 1 - rank;
+    const uint32_t cb = L.cnt[level][bin];
+    if (rank <= after || cb == 0u || rank >= best) continue;
+    bool ok = true;
+    if (test) {
+      uint32_t klo = level == 0 ? (uint32_t)bin << 21 : (prefix << 21) | ((uint32_t)bin << 10);
+      if (klo <= F32_NEG_INF_KEY) klo = F32_NEG_INF_KEY + 1u;
+      const float p_lo = prob_of(key_to_f32(klo), T, m_f, invZ);
+      const uint64_t n_ge = base_c + L.pcnt[level][bin] + cb;
+      const double S_ge = (double)(base_m + L.pmass[level][bin] + L.mass[level][bin]) / FX_ONE;
+      ok = (min_p > 0.f && p_lo < thr_minp) || (n_ge - 1 >= (uint64_t)(topk > 0 ? topk : 0)) ||
+           topp_fails(backend, S_ge - (double)p_lo, p_lo, top_p);
+    }
+    if (ok) best = rank;
+  }
+  if (best != INT_MAX) atomicMin(&sh.best, best);
+  __syncthreads();
+  const int r = sh.best;
+  __syncthreads();
+  return r == INT_MAX ? -1 : F32_BINS - 1 - r;
+}
+
+// The exact keys of one level-1 bin in descending order: the first key with a failing tie.
+// Returns true with the cut in sh (key, tie, mass ahead of the cut).
+__device__ __forceinline__ bool f32_walk(const F32NucLds& L, uint32_t prefix, uint64_t base_c, uint64_t base_m,
+                                         float T, float m_f, float invZ, int backend, int topk, float min_p,
+                                         float thr_minp, float top_p, F32NucShared& sh) {
+  const int tid = threadIdx.x;
+  uint32_t c[2];
+  float pk[2];
+  double m = 0.0;
+  uint64_t n = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint32_t lo = (uint32_t)(F32_KEYS - 1 - 2 * tid - e);
+    c[e] = L.cnt3[lo];
+    pk[e] = c[e] ? prob_of(key_to_f32((prefix << 10) | lo), T, m_f, invZ) : 0.f;
+    m += (double)c[e] * (double)pk[e];
+    n += c[e];
+  }
+  uint64_t tn = 0;
+  double tm = 0.0;
+  const uint64_t nb = block_excl_scan<NUC_WAVES>(n, sh.u, &tn);
+  const double mb = block_excl_scan<NUC_WAVES>(m, sh.d, &tm);
+  if (tid == 0) sh.best = INT_MAX;
+  __syncthreads();
+  double Sb = (double)base_m / FX_ONE + mb;
+  uint64_t Nb = base_c + nb;
+  int32_t my_tie = 0;
+  uint32_t my_key = 0;
+  double my_S = 0.0;
+  int my_rank = INT_MAX;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (c[e] && my_rank == INT_MAX) {
+      const int64_t fail = cut_index(backend, c[e], pk[e], Sb, (int64_t)Nb, topk, min_p, thr_minp, top_p);
+      if (fail < (int64_t)c[e]) {
+        my_rank = 2 * tid + e;
+        my_key = (prefix << 10) | (uint32_t)(F32_KEYS - 1 - my_rank);
+        my_tie = (int32_t)fail;
+        my_S = Sb + (double)fail * (double)pk[e];
+      }
+    }
+    Sb += (double)c[e] * (double)pk[e];
+    Nb += c[e];
+  }
+  if (my_rank != INT_MAX) atomicMin(&sh.best, my_rank);
+  __syncthreads();
+  const bool found = sh.best != INT_MAX;
+  if (found && my_rank == sh.best) {
+    sh.cut_key = my_key;
+    sh.cut_tie = my_tie;
+    sh.cut_S = my_S;
+  }
+  __syncthreads();
+  return found;
+}
+
+template <bool ALIGNED>
+__device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucLds& L, F32NucShared& sh) {
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x;
+  int b = 0, s = 0;
+  row_request(a, r, b, s);
+  RowSum rs = P.rowsum[r];
+  const int64_t V = a.vocab;
+  const char* rowp = row_ptr(a, r);
+  const float T = a.temperatures[b];
+  const int topk = a.top_ks[b];
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const float top_p = a.top_ps[b];
+  const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
+  const int64_t tok = step_token(a, b, s);
+  float xt = -INFINITY;
+  if (tok >= 0 && tok < V) {
+    xt = load_elem<DSV_F32>(rowp, tok);
+    if (pen && pen_test(P, b, tok)) xt = penalize<DSV_F32>(xt, pres, rep);
+  }
+  const uint32_t ktok = f32_key(xt);
+  const float m_f = rs.m_f, invZ = rs.invZ;
+  const float thr_minp = prob_of(key_to_f32(rs.kmax), T, m_f, invZ) * min_p;
+  uint32_t tie_before = 0, unused = 0;
+  f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 0, 0u, L, ktok, tok, tie_before);
+  f32_prefix(L, 0, sh);
+  const int64_t tie_tok = (int64_t)block_sum<NUC_WAVES>((uint64_t)tie_before, sh.u);
+  bool found = false;
+  int b0 = f32_next(L, 0, -1, true, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, topk, min_p, thr_minp, top_p, sh);
+  // the first bin that can hold the cut, else the next non-empty one (a margin of rounding may
+  // need one more)
+  for (int t0 = 0; t0 < 3 && b0 >= 0 && !found; ++t0) {
+    const uint64_t c0 = L.pcnt[0][b0], m0 = L.pmass[0][b0];
+    f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 1, (uint32_t)b0, L, ktok, tok, unused);
+    f32_prefix(L, 1, sh);
+    int b1 = f32_next(L, 1, -1, true, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, topk, min_p, thr_minp, top_p, sh);
+    for (int t1 = 0; t1 < 3 && b1 >= 0 && !found; ++t1) {
+      const uint32_t prefix = ((uint32_t)b0 << 11) | (uint32_t)b1;
+      f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 2, prefix, L, ktok, tok, unused);
+      found = f32_walk(L, prefix, c0 + L.pcnt[1][b1], m0 + L.pmass[1][b1], T, m_f, invZ, a.backend, topk, min_p,
+                       thr_minp, top_p, sh);
+      if (!found)
+        b1 = f32_next(L, 1, F32_BINS - 1 - b1, false, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, topk, min_p,
+                      thr_minp, top_p, sh);
+    }
+    if (!found)
+      b0 = f32_next(L, 0, F32_BINS - 1 - b0, false, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, topk, min_p, thr_minp,
+                    top_p, sh);
+  }
+  if (tid < WAVE) {
+    if (found) {
+      rs.vcut = sh.cut_key;
+      rs.ktie = sh.cut_tie;
+      rs.S_kept = sh.cut_S;
+    } else {  // every value is kept
+      rs.vcut = 0u;
+      rs.ktie = INT_MAX;
+      rs.S_kept = (double)(L.pmass[0][0] + L.mass[0][0]) / FX_ONE;
+    }
+    rs.S_f = (float)rs.S_kept;
+    nucleus_finish<DSV_F32>(P, r, b, s, rs, T, xt, tok, tie_tok, nullptr);
+  }
+  __syncthreads();
+}
+
 // The i-th full-histogram row in row order goes to workgroup i % gridDim.x.
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
@@ -1300,7 +1582,12 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
   for (int i = blockIdx.x; i < n; i += gridDim.x) {
     const int32_t row = P.nuc_rows[1 + i];
     if (row < 0 || row >= a.rows) continue;
-    if constexpr (DT == DSV_BF16) nuc_row<DT, ALIGNED>(P, row, hist, sh);
+    if constexpr (DT == DSV_BF16) {
+      nuc_row<DT, ALIGNED>(P, row, hist, sh);
+    } else {
+      __shared__ F32NucShared fsh;
+      nuc_row_f32<ALIGNED>(P, row, *reinterpret_cast<F32NucLds*>(dyn), fsh);
+    }
   }
 }
 
@@ -1749,6 +2036,49 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   }
 }
 
+// Float32 nucleus rows: the row statistics here, the cut by the radix descent of k_nuc (wave 0).
+template <int DT>
+__device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float T, const RowPre& pre, RowSum* srs) {
+  if (threadIdx.x >= WAVE) return;
+  const int lane = threadIdx.x;
+  const int C = P.C;
+  float m_l = -INFINITY;
+  int32_t arg_l = INT_MAX;
+  double s_l = 0.0;
+  if (lane < C) {
+    m_l = pre.cs[lane].m;
+    arg_l = pre.cs[lane].arg;
+    s_l = pre.cs[lane].s;
+  }
+  const float M = wave_max_f32(m_l);
+  const uint64_t at_max = __ballot(lane < C && m_l == M);
+  int32_t arg = readlane_at(arg_l, at_max ? __ffsll((long long)at_max) - 1 : 0);
+  if (arg == INT_MAX) arg = 0;
+  const float c2 = log2e_over(T);
+  const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
+  RowSum rs;
+  rs.mode = M_HIST;
+  rs.argmax = arg;
+  rs.kmax = key_of<DT>(M);
+  rs.vcut = 0u;
+  rs.ktie = INT_MAX;
+  rs.nlist = 0;
+  rs.flags = FLAG_FULL_HIST;
+  rs.norm = 0;
+  rs.m_f = M / T;
+  rs.invZ = (float)(1.0 / Z);
+  rs.Z = Z;
+  rs.S_kept = 1.0;
+  rs.S_f = 1.f;
+  rs.p_draft = 0.f;
+  if (lane == 0) {
+    P.rowsum[r] = rs;
+    *srs = rs;
+    P.step_ok[r] = 0;
+    P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0)
 // ---------------------------------------------------------------------------------------
@@ -1794,7 +2124,10 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   }
   __syncthreads();
   if (mode == M_HIST) {
-    if constexpr (DT == DSV_BF16) merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &srs);
+    if constexpr (DT == DSV_BF16)
+      merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &srs);
+    else
+      defer_nucleus<DT>(P, r, T, pre, &srs);
   } else {
     merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &srs);
   }
@@ -2275,10 +2608,6 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   if (a.backend != DSV_BACKEND_PYTORCH && a.backend != DSV_BACKEND_FLASHINFER)
     DSV_FAIL(DSV_ERR_INVALID, "%s: unknown backend %d", what, a.backend);
   hist_possible = a.filter && a.max_top_k > DSV_LIST_K;
-  if (hist_possible && a.logits_dtype != DSV_BF16)
-    DSV_FAIL(DSV_ERR_UNSUPPORTED,
-             "%s: float32 logits with top_k > %d and a top-p / min-p cut are not implemented; use bfloat16", what,
-             DSV_LIST_K);
   if (hist_possible && a.backend == DSV_BACKEND_FLASHINFER && a.need_min_p)
     DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: flashinfer min-p branch with top_k > %d is not implemented", what, DSV_LIST_K);
   const int C = chunks_per_row(a.vocab, a.logits_dtype);
@@ -2342,17 +2671,30 @@ static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipSt
       hipLaunchKernelGGL((k_merge<DSV_F32, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
   }
   DSV_CHECK_LAUNCH("k_chunk / k_merge");
-  if (hist_possible) {  // nucleus rows whose chunk windows fall short of the row floor
-    const size_t nuc_lds = (size_t)HIST_WORDS * 4;
+  if (hist_possible) {  // nucleus rows the merge listed: the full histogram (bf16) or radix descent (fp32)
     const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
-    if (P.aligned) {
-      (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)nuc_lds);
-      hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+    if (a.logits_dtype == DSV_BF16) {
+      const size_t nuc_lds = (size_t)HIST_WORDS * 4;
+      if (P.aligned) {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      } else {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      }
     } else {
-      (void)hipFuncSetAttribute((const void*)k_nuc<DSV_BF16, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)nuc_lds);
-      hipLaunchKernelGGL((k_nuc<DSV_BF16, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      const size_t nuc_lds = sizeof(F32NucLds);
+      if (P.aligned) {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_F32, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_F32, true>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      } else {
+        (void)hipFuncSetAttribute((const void*)k_nuc<DSV_F32, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)nuc_lds);
+        hipLaunchKernelGGL((k_nuc<DSV_F32, false>), dim3(grid), dim3(NUC_THREADS), nuc_lds, stream, P);
+      }
     }
     DSV_CHECK_LAUNCH("k_nuc");
   }

@@ -271,6 +271,26 @@ def test_build_target_probs(device, dtype, flags):
     torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_build_target_probs_nucleus(device, dtype):
+    """Rows with top-k off and a top-p cut (the full-histogram path for bf16, the radix descent
+    for float32), mixed with min-p and top-k > 64 rows."""
+    from dspine_amd.runtime.worker import build_dspine_target_probs
+
+    O = _O()
+    bs, T, V = 6, 2, 50021
+    g = torch.Generator().manual_seed(31)
+    logits = (torch.randn(bs * T, V, generator=g) * 2.5).to(dtype)
+    logits[2 * T:3 * T, :40] = 6.0  # a tie group straddling the cut
+    info = W.sampling_info([1.0, 0.7, 1.0, 1.3, 1.0, 0.9], [0, 0, 0, 100, 200, 0],
+                           [0.9, 0.5, 0.95, 0.8, 0.99, 1.0], [0.0, 0.0, 0.0, 0.0, 0.0, 0.05])
+    got = build_dspine_target_probs(next_token_logits=logits.to(device), sampling_info=W.info_to(info, device),
+                                    block_size=T, bs=bs, sampling_backend="pytorch")
+    torch.cuda.synchronize()
+    ref = O.build_target_probs(logits, info, T, bs, "pytorch", exact_softmax=True)
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
+
+
 @pytest.mark.parametrize("normalize", [True, False])
 def test_filter_target_probs(device, normalize):
     from dspine_amd.runtime.worker import filter_target_probs
@@ -279,6 +299,8 @@ def test_filter_target_probs(device, normalize):
     bs, T, V = 8, 2, 5003
     logits, info = _target_case(6, bs, T, V, torch.float32)
     info.is_any_greedy = False
+    info.top_ks[2] = 1 << 30  # a top-p only row (top-p 0.8): the float32 nucleus path
+    info.max_top_k = int(info.top_ks.max())
     temps = torch.repeat_interleave(info.temperatures.view(-1).clamp_min(0.5), T)
     probs = O.softmax_temp(logits, temps, exact=True)
     got = filter_target_probs(probs.to(device), W.info_to(info, device), T, bs, "pytorch", normalize=normalize)

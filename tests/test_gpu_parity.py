@@ -246,11 +246,7 @@ def _small_batch(seed, bs=24, T=8, V=997, K=8, dtype=torch.float32, mixed=True, 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("penalties", [False, True])
 def test_verify_small_mixed(device, seed, dtype, penalties):
-    if dtype == torch.float32:
-        # float32 nucleus rows (top-k > 64 with top-p) are rejected up front; keep top-k small
-        batch = _small_batch(seed, dtype=dtype, mixed=False, penalties=penalties)
-    else:
-        batch = _small_batch(seed, dtype=dtype, penalties=penalties)
+    batch = _small_batch(seed, dtype=dtype, penalties=penalties)
     bs = batch["candidates"].shape[0]
     gpu = run_gpu_verify(batch, device)
     ref = run_oracle(batch, list(range(bs)))
@@ -305,8 +301,9 @@ def test_greedy_and_topk_row_layouts(device, V, stride):
         assert np.array_equal(got.cpu().numpy(), r)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("case", ["flat", "constant", "peaked", "wide_tail"])
-def test_verify_nucleus_paths(device, case):
+def test_verify_nucleus_paths(device, case, dtype):
     # nucleus rows (top-k off, top-p < 1) that exercise each way the cut is found: "flat"
     # (temperature 40: the counted windows cannot reach the row floor -> full histogram),
     # "constant" (151936 equal values: more ties than a 16-bit counter holds), "peaked" (one
@@ -314,7 +311,7 @@ def test_verify_nucleus_paths(device, case):
     # windows), "wide_tail" (heavy-tailed logits, T = 1)
     V = 151936
     bs, T = 4, 3
-    batch = _small_batch(21, bs=bs, T=T, V=V, K=4, dtype=torch.bfloat16, mixed=False, penalties=True)
+    batch = _small_batch(21, bs=bs, T=T, V=V, K=4, dtype=dtype, mixed=False, penalties=True)
     g = torch.Generator().manual_seed(22)
     rows = bs * T
     if case == "flat":
@@ -331,7 +328,7 @@ def test_verify_nucleus_paths(device, case):
     else:
         logits = 2.0 * torch.distributions.StudentT(3.0).sample((rows, V))
         temps = [1.0] * bs
-    batch["logits"] = logits.to(torch.bfloat16)
+    batch["logits"] = logits.to(dtype)
     batch["info"] = W.sampling_info(temps, [0] * bs, [0.9, 0.5, 0.95, 0.99][:bs])
     base = batch["logits"].float()
     for b in range(bs):  # a likely token as a q lane, so some drafts are accepted
