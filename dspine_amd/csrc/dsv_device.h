@@ -60,7 +60,7 @@ constexpr uint32_t WIN_EMPTY = 0x10000u;
 constexpr uint32_t KX_UNKNOWN = 0xFFFFFFFFu;  // ChunkStat::kx when the chunk did not track it
 constexpr int STAGE_MAX = 96;        // list rows: threads whose vectors fit the LDS stage
 constexpr int WHITV = 64;            // LDS slots of a wave for vectors holding history hits
-constexpr int NCHK = 16;             // most chunks a row may have (per-row chunk arrays)
+constexpr int NCHK = 32;             // most chunks a row may have (per-row chunk arrays)
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
 constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram

@@ -541,9 +541,9 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
 // runs on wave 0.
 // ---------------------------------------------------------------------------------------
 struct MergeShared {
-  uint64_t buf[16 * DSV_LIST_K];
+  uint64_t buf[NCHK * DSV_LIST_K];
   uint64_t top[DSV_LIST_K];
-  int32_t off[17];
+  int32_t off[NCHK + 1];
 };
 
 template <int DT>
@@ -731,7 +731,7 @@ constexpr int HC_KEYS = 512;  // merged keys whose per-chunk counts stay in LDS 
 struct NucMergeShared {
   uint32_t h[HWIN];  // merged counts, position q = kmax - key
   uint16_t hc[8 * HC_KEYS];  // per-chunk counts at position q (chunk c at c * HC_KEYS + q)
-  uint32_t cw[16], ck[16];
+  uint32_t cw[NCHK], ck[NCHK];
   double wm[CT / WAVE];
   int64_t wc[CT / WAVE];
   uint64_t cut[CT / WAVE];
@@ -2084,8 +2084,12 @@ __device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
-  __shared__ MergeShared ms;
-  __shared__ NucMergeShared ns;
+  __shared__ union {  // a row merges as a support list or as a nucleus, never both
+    MergeShared ms;
+    NucMergeShared ns;
+  } mu;
+  MergeShared& ms = mu.ms;
+  NucMergeShared& ns = mu.ns;
   __shared__ DrawShared ds;
   __shared__ RowPre pre;
   __shared__ RowSum srs;
@@ -2611,7 +2615,8 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   if (hist_possible && a.backend == DSV_BACKEND_FLASHINFER && a.need_min_p)
     DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: flashinfer min-p branch with top_k > %d is not implemented", what, DSV_LIST_K);
   const int C = chunks_per_row(a.vocab, a.logits_dtype);
-  if (C > 16) DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab %lld needs %d chunks (> 16)", what, (long long)a.vocab, C);
+  if (C > NCHK)
+    DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab %lld needs %d chunks (> %d)", what, (long long)a.vocab, C, NCHK);
   const bool history = a.hist_ids && a.hist_len > 0;
   const WsLayout w = ws_layout(a.rows, a.bs, a.vocab, a.logits_dtype, DSV_LIST_K, history);
   if (a.workspace_bytes < w.total)

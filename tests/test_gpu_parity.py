@@ -342,6 +342,17 @@ def test_verify_nucleus_paths(device, case, dtype):
     assert len(compare_outputs(gpu, ref, range(bs), f"nucleus {case}")) <= 1
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_large_vocab(device, dtype):
+    """262144-wide rows (26 float32 / 13 bf16 chunks a row), ragged, mixed list / nucleus /
+    greedy rows with penalties."""
+    batch = _small_batch(41, bs=6, T=4, V=262144, K=8, dtype=dtype, ragged=True, penalties=True)
+    bs = batch["candidates"].shape[0]
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)), exact_softmax=True)
+    assert len(compare_outputs(gpu, ref, range(bs), f"large vocab {dtype}")) <= 1
+
+
 def test_verify_unfiltered(device):
     batch = _small_batch(7, dtype=torch.bfloat16, mixed=False)
     batch["info"] = W.sampling_info([0.7] * 24, [0] * 24, [1.0] * 24)
