@@ -154,7 +154,6 @@ struct DrawShared {
   float qraw[QMAX];     // q of the lane as given (the draft test sums these)
   int32_t qlast[QMAX];  // lane is the last one with its id (its q is the residual's)
   int32_t qrank[QMAX];  // q id at a split cut key: values at the cut key before it (id order), else -1
-  int32_t qc[QMAX];     // chunk of a residual q id (last lane with its id), else -1
   float qx[QMAX];       // adjusted value at the q id
   double qd[QMAX];      // P - max(P - q, 0) at a q id (the residual's reduction), else 0
   double cm[NCHK];      // chunk masses of P above the cut (every id of an unfiltered row)
@@ -165,6 +164,8 @@ struct DrawShared {
   double chunk_lo, thr, pick_lo;
   int32_t acc, chunk, tieq, use_r, pick_thread, ptb;
   uint64_t ptmask;   // the picked thread's span positions at the cut key
+  uint64_t rmask;    // q lanes that need their rank at a split cut key
+  uint64_t qmask;    // residual q lanes whose id lies in the planned chunk
   float pw[64];      // the picked thread's span weights
 };
 
@@ -206,9 +207,18 @@ __device__ __forceinline__ void stage_q(const dsv_verify_args& a, int b, int ste
   __syncthreads();
 }
 
+// (one wave, lanes holding q lanes) whether the lane's id is a valid token that no later lane of
+// the first K repeats: its q is the one the residual uses
+__device__ __forceinline__ bool q_last_lane(int64_t qid, int K, int64_t V) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  bool last = qid >= 0 && qid < V;
+  for (int l2 = 1; l2 < K; ++l2) last = last && !(l2 > lane && readlane_at(qid, l2) == qid);
+  return last;
+}
+
 // The q lanes of draft step+1 for one wave (lanes are the q lanes): ids, given and clamped
 // values, whether the lane is the last with its id, and -- want_x -- the adjusted logit at each
-// such id.  Leaves them in sh for the wave (fenced), the workgroup sees them after a barrier.
+// such id.  Leaves them in sh; the workgroup sees them after a barrier.
 template <int DT>
 __device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, bool live, const char* rowp,
                                              bool want_x, DrawShared& sh) {
@@ -223,11 +233,7 @@ __device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, 
   sh.qv[lane] = clamp01(qr);
   sh.qd[lane] = 0.0;
   sh.qrank[lane] = -1;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  bool last = qid >= 0 && qid < a.vocab;
-  for (int l2 = lane + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != qid;
+  const bool last = q_last_lane(qid, a.K, a.vocab);
   sh.qlast[lane] = last;
   float xq = -INFINITY;
   if (want_x && last) {
@@ -332,6 +338,39 @@ struct DrawPlan {
   double qd[QMAX];       // the residual's reduction at each q lane
 };
 
+// (rare) the rank of q id l among the values of the cut key: the values of that key ahead of it
+// in its chunk, over the workgroup, plus the cut-key counts of the chunks before (thread 0 writes
+// sh.qrank[l]).
+template <int DT, bool ALIGNED, int NT>
+__device__ __forceinline__ void q_cut_rank(const KParams& P, int b, const char* rowp, uint32_t vcut, float pres,
+                                           float rep, int l, DrawShared& sh) {
+  constexpr int NW = NT / WAVE;
+  constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
+  const int64_t qid = sh.qid[l];
+  const int cq = (int)(qid / CHE);
+  const int64_t clo = (int64_t)cq * CHE;
+  const int64_t chi = clo + CHE < P.a.vocab ? clo + CHE : P.a.vocab;
+  int32_t before = 0;
+  // one vector at a time (a rare path: few registers), the values at the cut key before qid
+#pragma unroll 1
+  for (int64_t vi = clo / n + threadIdx.x; vi * n < qid; vi += NT) {
+    const uint4 w = load_vec<DT>(rowp, vi, chi, ALIGNED);
+    const uint32_t bits = P.pbits ? pen_bits(P, b, vi * n, n) : 0u;
+#pragma unroll
+    for (int e = 0; e < n; ++e) {
+      float x = vec_elem<DT>(w, e);
+      if ((bits >> e) & 1u) x = penalize<DT>(x, pres, rep);
+      before += (key_of<DT>(x) == vcut) & (vi * n + e < qid);
+    }
+  }
+  before = block_sum<NW>(before, sh.red_i);
+  if (threadIdx.x == 0) {
+    for (int c = 0; c < cq; ++c) before += sh.ct[c];
+    sh.qrank[l] = before;
+  }
+  __syncthreads();
+}
+
 // Dense draw, first part, over the NT threads of the workgroup: sh.cm / sh.ct hold the chunk
 // masses and cut counts, q is staged when resid.  Leaves the plan in sh (chunk, thr, chunk_lo,
 // tieq, use_r, qd).
@@ -339,17 +378,15 @@ template <int DT, bool ALIGNED, int NT>
 __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
                                            float pres, float rep, bool resid, float uf, DrawShared& sh,
                                            bool have_qx = false) {
-  constexpr int NW = NT / WAVE;
-  constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
+  constexpr int CHE = Elems<DT>::chunk;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int C = P.C;
   const bool pen = P.pbits != nullptr;
   const bool hist = rs.mode == M_HIST;
-  const BonusP bp = bonus_p<DT>(rs, T);
-  const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
   const bool tie_cut = hist && rs.ktie > 0 && rs.ktie != INT_MAX;  // the cut splits a key's values
   // the q ids' adjusted values; ids at a split cut key need their rank among its values
+  int32_t qc = -1;  // (wave 0) the chunk of the lane's residual q id
   if (tid < WAVE) {
     const bool qlive = resid && lane < a.K && sh.qlast[lane];
     float xq = -INFINITY;
@@ -360,41 +397,32 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
       xq = load_elem<DT>(rowp, qid);
       if (pen && pen_test(P, b, qid)) xq = penalize<DT>(xq, pres, rep);
     }
+    const bool need = qlive && tie_cut && key_of<DT>(xq) == rs.vcut;
+    if (qlive) qc = (int32_t)(sh.qid[lane] / CHE);
     if (lane < QMAX) {
       sh.qx[lane] = xq;
-      sh.qrank[lane] = (qlive && tie_cut && key_of<DT>(xq) == rs.vcut) ? 0 : -1;
-      sh.qc[lane] = qlive ? (int32_t)(sh.qid[lane] / CHE) : -1;
+      sh.qrank[lane] = need ? 0 : -1;
     }
+    const uint64_t rk = __ballot(need);
+    if (lane == 0) sh.rmask = rk;
   }
   __syncthreads();
-  for (int l = 0; l < a.K; ++l) {  // (rare) rank of a q id among the cut key's values
-    if (sh.qrank[l] < 0) continue;
-    const int64_t qid = sh.qid[l];
-    const int cq = (int)(qid / CHE);
-    const int64_t jlo = (int64_t)cq * CHE + (int64_t)tid * FE;
-    int32_t before = 0;
-    for_span<DT, ALIGNED, NT>(P, b, rowp, cq, pres, rep,
-                              [&](int i, float x) { before += (key_of<DT>(x) == rs.vcut) & (jlo + i < qid); });
-    before = block_sum<NW>(before, sh.red_i);
-    if (tid == 0) {
-      for (int c = 0; c < cq; ++c) before += sh.ct[c];
-      sh.qrank[l] = before;
-    }
-    __syncthreads();
-  }
+  for (uint64_t m = sh.rmask; m; m &= m - 1ull)  // (rare) rank of a q id among the cut key's values
+    q_cut_rank<DT, ALIGNED, NT>(P, b, rowp, rs.vcut, pres, rep, __ffsll((long long)m) - 1, sh);
+  const BonusP bp = bonus_p<DT>(rs, T);
+  const double P_cut = hist ? (double)bp(value_of_key<DT>(rs.vcut)) : 0.0;
   if (tid < WAVE) {
     // the residual's reduction at each q id (lanes hold the q lanes)
-    if (resid && lane < a.K && sh.qlast[lane]) {
+    double qd = 0.0;
+    if (qc >= 0) {
       const float xq = sh.qx[lane];
       const uint32_t k = key_of<DT>(xq);
       const bool kept = !hist || k > rs.vcut ||
                         (k == rs.vcut && (rs.ktie == INT_MAX || (sh.qrank[lane] >= 0 && sh.qrank[lane] < rs.ktie)));
       const double Pq = kept ? (double)bp(xq) : 0.0;
-      sh.qd[lane] = Pq - fmax(Pq - (double)sh.qv[lane], 0.0);
+      qd = Pq - fmax(Pq - (double)sh.qv[lane], 0.0);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (lane < QMAX) sh.qd[lane] = qd;
     // lanes hold the chunks: masses with the kept values at the cut key, then the residual's
     const int32_t ctl = lane < C ? sh.ct[lane] : 0;
     const int32_t tie_prefix = wave_incl_scan(ctl) - ctl;
@@ -405,9 +433,10 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
     }
     const double Mp = lane < C ? sh.cm[lane] + (kt > 0 ? (double)kt * P_cut : 0.0) : 0.0;
     double Mr = Mp;
-    if (resid && lane < C)
-      for (int l = 0; l < a.K; ++l)
-        if (sh.qc[l] == lane) Mr -= sh.qd[l];
+    for (uint64_t m = __ballot(qc >= 0); m; m &= m - 1ull) {  // (q lanes in id order)
+      const int l = __ffsll((long long)m) - 1;
+      if (readlane_at(qc, l) == lane && lane < C) Mr -= readlane_at(qd, l);
+    }
     double lo_r, hi_r, lo_p, hi_p;
     const double mr = wave_tiles(Mr, lo_r, hi_r);
     const double mp = wave_tiles(Mp, lo_p, hi_p);
@@ -421,10 +450,12 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
       hit = pos ? 1ull << (63 - __clzll((long long)pos)) : 0ull;
     }
     const int cstar = hit ? __ffsll((long long)hit) - 1 : -1;
+    const uint64_t qm = __ballot(qc >= 0 && qc == cstar);
     if (tid == 0) {
       sh.chunk = cstar;
       sh.thr = thr;
       sh.use_r = use_r ? 1 : 0;
+      sh.qmask = qm;
     }
     if (cstar >= 0 && lane == cstar) {
       sh.chunk_lo = clo;
@@ -482,9 +513,11 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
     kept_t = room <= 0 ? 0 : (room < tt ? (int32_t)room : tt);
   }
   double w_t = mt + (kept_t > 0 ? (double)kept_t * P_cut : 0.0);
-  if (use_r)
-    for (int l = 0; l < a.K; ++l)
-      if (sh.qlast[l] && sh.qid[l] >= jlo && sh.qid[l] < jlo + FE) w_t -= sh.qd[l];
+  const uint64_t qm = use_r ? sh.qmask : 0ull;  // the residual's q ids in this chunk
+  for (uint64_t m = qm; m; m &= m - 1ull) {
+    const int l = __ffsll((long long)m) - 1;
+    if (sh.qid[l] >= jlo && sh.qid[l] < jlo + FE) w_t -= sh.qd[l];
+  }
   double tlo, thi;
   block_tiles<NW>(w_t, sh.red_d, tlo, thi);
   const double base = sh.chunk_lo, thr = sh.thr;
@@ -517,9 +550,10 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
       const int32_t seen = __popcll(pm & ((1ull << lane) - 1ull));
       Pj = (int64_t)sh.ptb + seen < (int64_t)rs.ktie ? P_cut : 0.0;
     }
-    if (live && use_r)
-      for (int l = 0; l < a.K; ++l)
-        if (sh.qlast[l] && sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
+    for (uint64_t m = live ? qm : 0ull; m; m &= m - 1ull) {
+      const int l = __ffsll((long long)m) - 1;
+      if (sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
+    }
     double wlo, whi;
     wave_tiles(Pj, wlo, whi);
     const uint64_t hitj = __ballot(live && Pj > 0.0 && sh.pick_lo + whi > thr);
@@ -540,6 +574,14 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
 // the step decision.  Rank selection of the row's top-K uses the whole workgroup; the rest
 // runs on wave 0.
 // ---------------------------------------------------------------------------------------
+// A row's merge result in LDS; k_merge's last step stores it (global stores issued earlier
+// would hold up every later wait on the vector memory counter).
+struct RowOut {
+  RowSum rs;
+  int32_t ok;   // the step decision
+  int32_t nuc;  // 1: listed for the full-histogram pass
+};
+
 struct MergeShared {
   uint64_t buf[NCHK * DSV_LIST_K];
   uint64_t top[DSV_LIST_K];
@@ -548,7 +590,7 @@ struct MergeShared {
 
 template <int DT>
 __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, int s, int mode, float T, MergeShared& ms,
-                                          DrawShared& ds, const RowPre& pre, RowSum* srs) {
+                                          DrawShared& ds, const RowPre& pre, RowOut* ro) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int C = P.C;
@@ -635,10 +677,10 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     rs.p_draft = tok == arg ? 1.f : 0.f;
     const int32_t ok = tok >= 0 ? step_accept_lds(ds, a.K, tok, rs.p_draft, pre.u) : 0;
     if (lane == 0) {
-      list[0] = ListEntry{arg, 1.f};
-      P.rowsum[r] = rs;
-      *srs = rs;
-      P.step_ok[r] = ok;
+      if (!a.candidates) list[0] = ListEntry{arg, 1.f};  // (the step draws from LDS)
+      ro->rs = rs;
+      ro->ok = ok;
+      ro->nuc = 0;
     }
     return;
   }
@@ -700,7 +742,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     int rank = 0;
     for (int i = 0; i < kk; ++i) rank += readlane_at(kid, i) < kid;
     if (keep) {
-      list[rank] = ListEntry{id, Pj};
+      if (!a.candidates) list[rank] = ListEntry{id, Pj};
       ds.lst[rank] = ListEntry{id, Pj};
     }
     rs.nlist = __popcll(__ballot(keep));
@@ -708,9 +750,9 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   }
   const int32_t ok = tok >= 0 ? step_accept_lds(ds, a.K, tok, rs.p_draft, pre.u) : 0;
   if (lane == 0) {
-    P.rowsum[r] = rs;
-    *srs = rs;
-    P.step_ok[r] = ok;
+    ro->rs = rs;
+    ro->ok = ok;
+    ro->nuc = 0;
   }
 }
 
@@ -745,22 +787,27 @@ struct NucMergeShared {
 // p of a nucleus row at its draft token and the step decision; RowSum out (wave 0).
 template <int DT>
 __device__ __forceinline__ void nucleus_finish(const KParams& P, int64_t r, int b, int s, RowSum rs, float T,
-                                               float xtok, int64_t tok, int64_t tie_tok, RowSum* srs,
+                                               float xtok, int64_t tok, int64_t tie_tok, RowOut* ro,
                                                const DrawShared* fq = nullptr, float coin = 0.f) {
   const bool kept = key_of<DT>(xtok) > rs.vcut || (key_of<DT>(xtok) == rs.vcut && tie_tok < (int64_t)rs.ktie);
   rs.p_draft = (tok >= 0 && tok < P.a.vocab && kept) ? prob_of(xtok, T, rs.m_f, rs.invZ) / rs.S_f : 0.f;
   int32_t ok = 0;
   if (tok >= 0) ok = fq ? step_accept_lds(*fq, P.a.K, tok, rs.p_draft, coin) : step_accept_wave(P.a, b, s, tok, rs.p_draft);
   if (threadIdx.x == 0) {
-    P.rowsum[r] = rs;
-    if (srs) *srs = rs;
-    P.step_ok[r] = ok;
+    if (ro) {
+      ro->rs = rs;
+      ro->ok = ok;
+      ro->nuc = 0;
+    } else {
+      P.rowsum[r] = rs;
+      P.step_ok[r] = ok;
+    }
   }
 }
 
 template <int DT>
 __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b, int s, float T, NucMergeShared& sh,
-                                              DrawShared& ds, const RowPre& pre, RowSum* srs) {
+                                              DrawShared& ds, const RowPre& pre, RowOut* ro) {
   constexpr int NW = CT / WAVE;
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
@@ -833,10 +880,9 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   if (kmax < 0x80u) {  // no finite value
     if (tid == 0) {
       rs.flags = FLAG_FULL_HIST;
-      P.rowsum[r] = rs;
-      *srs = rs;
-      P.step_ok[r] = 0;
-      P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
+      ro->rs = rs;
+      ro->ok = 0;
+      ro->nuc = 1;
     }
     return;
   }
@@ -947,10 +993,9 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     // track its largest value): the full histogram decides it
     if (tid == 0) {
       rs.flags = FLAG_FULL_HIST;
-      P.rowsum[r] = rs;
-      *srs = rs;
-      P.step_ok[r] = 0;
-      P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
+      ro->rs = rs;
+      ro->ok = 0;
+      ro->nuc = 1;
     }
     return;
   }
@@ -1057,7 +1102,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       }
     }
     tie_tok = wave_sum(tie_tok);
-    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok, srs, &ds, pre.u);
+    nucleus_finish<DT>(P, r, b, s, rs, T, xt, tok, tie_tok, ro, &ds, pre.u);
   }
 }
 
@@ -2038,7 +2083,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 
 // Float32 nucleus rows: the row statistics here, the cut by the radix descent of k_nuc (wave 0).
 template <int DT>
-__device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float T, const RowPre& pre, RowSum* srs) {
+__device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float T, const RowPre& pre, RowOut* ro) {
   if (threadIdx.x >= WAVE) return;
   const int lane = threadIdx.x;
   const int C = P.C;
@@ -2072,10 +2117,9 @@ __device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float
   rs.S_f = 1.f;
   rs.p_draft = 0.f;
   if (lane == 0) {
-    P.rowsum[r] = rs;
-    *srs = rs;
-    P.step_ok[r] = 0;
-    P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
+    ro->rs = rs;
+    ro->ok = 0;
+    ro->nuc = 1;
   }
 }
 
@@ -2092,7 +2136,7 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   NucMergeShared& ns = mu.ns;
   __shared__ DrawShared ds;
   __shared__ RowPre pre;
-  __shared__ RowSum srs;
+  __shared__ RowOut ro;
   const dsv_verify_args& a = P.a;
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
@@ -2129,18 +2173,19 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   __syncthreads();
   if (mode == M_HIST) {
     if constexpr (DT == DSV_BF16)
-      merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &srs);
+      merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &ro);
     else
-      defer_nucleus<DT>(P, r, T, pre, &srs);
+      defer_nucleus<DT>(P, r, T, pre, &ro);
   } else {
-    merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &srs);
+    merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &ro);
   }
-  if (!a.candidates) return;  // target-distribution entry: no draw
   __syncthreads();
-  // the bonus token this row gives when it is the request's accepted length (k_final picks it)
-  const RowSum rs = srs;
-  int64_t bonus;
-  if (rs.mode == M_GREEDY) {
+  // the bonus token this row gives when it is the request's accepted length (k_final picks it);
+  // the target-distribution entry draws none
+  const RowSum& rs = ro.rs;  // (read from LDS where used: fewer live registers)
+  int64_t bonus = 0;
+  if (!a.candidates) {
+  } else if (rs.mode == M_GREEDY) {
     bonus = rs.argmax;
   } else if (rs.mode == M_LIST) {
     bonus = tid < WAVE ? list_draw(a, resid, pre.uf, ds) : 0;
@@ -2161,7 +2206,12 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
     }
     bonus = BONUS_PLAN;
   }
-  if (threadIdx.x == 0) P.rbonus[r] = bonus;
+  if (threadIdx.x == 0) {
+    P.rowsum[r] = rs;
+    P.step_ok[r] = ro.ok;
+    if (a.candidates) P.rbonus[r] = bonus;
+    if (ro.nuc) P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2266,22 +2316,21 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       const int64_t qid = on ? load_index(a.q_ids, a.q_ids_i64, qi + lane) : -1;
       const float qv = on ? clamp01(a.q_values[qi + lane]) : 0.f;
       const double qd = pl->qd[lane];
+      const int32_t ch = pl->chunk;
       if (lane == 0) {
         sh.thr = pl->thr;
         sh.chunk_lo = pl->chunk_lo;
-        sh.chunk = pl->chunk;
+        sh.chunk = ch;
         sh.tieq = pl->tieq;
         sh.use_r = pl->use_r;
       }
       sh.qid[lane] = qid;
       sh.qv[lane] = qv;
       sh.qd[lane] = qd;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      bool last = qid >= 0 && qid < V;
-      for (int l2 = lane + 1; l2 < a.K && last; ++l2) last = sh.qid[l2] != qid;
+      const bool last = q_last_lane(qid, a.K, V);
       sh.qlast[lane] = last;
+      const uint64_t qm = __ballot(last && ch >= 0 && qid / CHE == ch);
+      if (lane == 0) sh.qmask = qm;
     }
     const RowSum rs = P.rowsum[rstar];
     bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh);
