@@ -83,8 +83,9 @@ __device__ __forceinline__ int req_cap(const dsv_verify_args& a, int b) {
 // Row r -> (request b, position s); false when r is not a verified row.
 __device__ __forceinline__ bool row_request(const dsv_verify_args& a, int64_t r, int& b, int& s) {
   if (a.row_offsets == nullptr) {
-    b = (int)(r / a.T);
-    s = (int)(r - (int64_t)b * a.T);
+    // (rows < 2^31: a 32-bit division)
+    b = (int)((uint32_t)r / (uint32_t)a.T);
+    s = (int)((uint32_t)r - (uint32_t)b * (uint32_t)a.T);
   } else {
     if (load_index(a.row_offsets, a.row_offsets_i64, 0) > r) return false;
     int lo = 0, hi = a.bs - 1;

@@ -2,7 +2,7 @@
 // residual resample, accepted-prefix compaction and KV-slot gather.
 //
 // Launches of one verify step (no host synchronisation):
-//   k_prep   (requests)         penalty bitmap of each request's token history
+//   k_prep   (spans x requests) penalty bitmap of each request's token history, 20480 ids a workgroup
 //   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 10240 fp32 values held in
 //                               registers: max/argmax, softmax partial sums, exact top-k
 //                               candidates, nucleus value counts -- one read of the logits
@@ -80,21 +80,34 @@ __device__ __forceinline__ bool pen_test(const KParams& P, int b, int64_t j) {
 // ---------------------------------------------------------------------------------------
 // k_prep: history bitmaps
 // ---------------------------------------------------------------------------------------
+constexpr int PREP_WORDS = 640;  // bitmap words of one k_prep workgroup (20480 token ids)
 __global__ __launch_bounds__(BCT) void k_prep(KParams P) {
-  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ uint32_t bm[PREP_WORDS];
   const dsv_verify_args& a = P.a;
-  const int b = blockIdx.x, tid = threadIdx.x;
-  uint32_t* bm = reinterpret_cast<uint32_t*>(dyn);
-  const int words = (int)P.pwords;
-  for (int i = tid; i < words; i += BCT) bm[i] = 0u;
-  __syncthreads();
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int64_t w0 = (int64_t)blockIdx.x * PREP_WORDS;  // this workgroup's words of request b's bitmap
+  const int64_t lo = w0 * 32;
+  const int words = (int)(P.pwords - w0 < PREP_WORDS ? P.pwords - w0 : PREP_WORDS);
   const int32_t* h = a.hist_ids + (int64_t)b * a.hist_len;
-  for (int i = tid; i < a.hist_len; i += BCT) {
-    const int64_t t = h[i];
-    if (t >= 0 && t < a.vocab) atomicOr(&bm[t >> 5], 1u << (t & 31));
+  const int H = a.hist_len;
+  int64_t t[4];  // the request's ids, read before the LDS is cleared
+  for (int i0 = 0; i0 < H; i0 += 4 * BCT) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) t[g] = i0 + g * BCT + tid < H ? (int64_t)h[i0 + g * BCT + tid] : -1;
+    if (i0 == 0) {
+      for (int i = tid; i < PREP_WORDS; i += BCT) bm[i] = 0u;
+      __syncthreads();
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (t[g] >= lo && t[g] < a.vocab && t[g] < lo + 32 * PREP_WORDS)
+        atomicOr(&bm[(t[g] - lo) >> 5], 1u << ((t[g] - lo) & 31));
+  }
+  if (H <= 0) {
+    for (int i = tid; i < PREP_WORDS; i += BCT) bm[i] = 0u;
   }
   __syncthreads();
-  uint32_t* dst = P.pbits + (int64_t)b * P.pwords;
+  uint32_t* dst = P.pbits + (int64_t)b * P.pwords + w0;
   for (int i = tid; i < words; i += BCT) dst[i] = bm[i];
 }
 
@@ -1043,7 +1056,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       if (lane == 0) {
         ds.cm[c] = mc;
         ds.ct[c] = tc;
-        P.rties[r * NCHK + c] = tc;
+        if (!a.candidates) P.rties[r * NCHK + c] = tc;  // (for k_dense_p; the step keeps them in LDS)
       }
     }
   } else {
@@ -1077,7 +1090,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     if (lane == 0) {
       ds.cm[c] = mc;
       ds.ct[c] = tc;
-      P.rties[r * NCHK + c] = tc;
+      if (!a.candidates) P.rties[r * NCHK + c] = tc;
     }
   }
   }
@@ -1816,14 +1829,37 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   // max and the first index attaining it
   float m_t = -INFINITY;
   int bu = -1;
+  bool done = false;
+  if constexpr (DT == DSV_BF16) {
+    // bf16 bits compared as signed 16-bit integers (two a packed max): the order of the values
+    // when the maximum is positive; a thread whose maximum is not takes the float path below
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    int best = INT_MIN;
 #pragma unroll
-  for (int u = 0; u < CV; ++u) {
-    float vm = vec_elem<DT>(v[u], 0);
+    for (int u = 0; u < CV; ++u) {
+      const s16x2 a = __builtin_elementwise_max(__builtin_bit_cast(s16x2, v[u].x), __builtin_bit_cast(s16x2, v[u].y));
+      const s16x2 c = __builtin_elementwise_max(__builtin_bit_cast(s16x2, v[u].z), __builtin_bit_cast(s16x2, v[u].w));
+      const s16x2 d = __builtin_elementwise_max(a, c);
+      const int vm = (int)d.x > (int)d.y ? (int)d.x : (int)d.y;
+      if (vm > best) {
+        best = vm;
+        bu = u;
+      }
+    }
+    done = best > 0;
+    if (done) m_t = __uint_as_float((uint32_t)best << 16);
+  }
+  if (!done) {
+    bu = -1;
 #pragma unroll
-    for (int e = 1; e < n; ++e) vm = fmaxf(vm, vec_elem<DT>(v[u], e));
-    if (vm > m_t) {
-      m_t = vm;
-      bu = u;
+    for (int u = 0; u < CV; ++u) {
+      float vm = vec_elem<DT>(v[u], 0);
+#pragma unroll
+      for (int e = 1; e < n; ++e) vm = fmaxf(vm, vec_elem<DT>(v[u], e));
+      if (vm > m_t) {
+        m_t = vm;
+        bu = u;
+      }
     }
   }
   uint64_t mine = 0ull;
@@ -2194,9 +2230,13 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   } else {
     // the chunk and threshold; k_final scans the chunk when this row is the accepted one
     dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, pre.pres, pre.rep, resid, pre.uf, ds, true);
+    // the plan, stored by waves 1 and 2: a wave's later waits cover only its own stores, so the
+    // row's stores (wave 0, below) do not queue behind these
+    static_assert(QMAX <= WAVE && CT >= 3 * WAVE, "plan stores by waves 1 and 2");
     DrawPlan* pl = P.plans + r;
-    if (threadIdx.x < QMAX) pl->qd[threadIdx.x] = ds.qd[threadIdx.x];
-    if (threadIdx.x == 0) {
+    const int lq = (int)threadIdx.x - WAVE;
+    if (lq >= 0 && lq < QMAX) pl->qd[lq] = ds.qd[lq];
+    if (threadIdx.x == 2 * WAVE) {
       pl->thr = ds.thr;
       pl->chunk_lo = ds.chunk_lo;
       pl->chunk = ds.chunk;
@@ -2671,8 +2711,6 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   if (a.workspace_bytes < w.total)
     DSV_FAIL(DSV_ERR_WORKSPACE, "%s: workspace %lld < %lld bytes", what, (long long)a.workspace_bytes,
              (long long)w.total);
-  if (history && (size_t)pen_words(a.vocab) * 4 > 64 * 1024)
-    DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab too large for the history bitmap", what);
   const size_t esize = a.logits_dtype == DSV_BF16 ? 2 : 4;
   memset(&P, 0, sizeof(P));
   P.a = a;
@@ -2703,9 +2741,8 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
 static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipStream_t stream) {
   const dsv_verify_args& a = P.a;
   if (P.pbits) {
-    const size_t prep_lds = (size_t)P.pwords * 4;
-    (void)hipFuncSetAttribute((const void*)k_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)prep_lds);
-    hipLaunchKernelGGL(k_prep, dim3(a.bs), dim3(BCT), prep_lds, stream, P);
+    const unsigned spans = (unsigned)((P.pwords + PREP_WORDS - 1) / PREP_WORDS);
+    hipLaunchKernelGGL(k_prep, dim3(spans, (unsigned)a.bs), dim3(BCT), 0, stream, P);
     DSV_CHECK_LAUNCH("k_prep");
   }
   if (profile && g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
