@@ -473,6 +473,17 @@ __device__ __forceinline__ bool topp_fails(int backend, double S_before, float p
 
 __device__ __forceinline__ float clamp01(float q) { return (q >= 0.f && q <= 1.f) ? q : 0.f; }
 
+// Whether a support-list (top-k) row of the verify step needs its softmax normaliser Z: only a
+// top-p test on the unrenormalised probabilities reads it.  Top-k and min-p compare p up to a
+// common factor, the flashinfer min-p branch renormalises over the top-k before its top-p test,
+// and with top_p >= 1 the test keeps every value (up to the float32 rounding of its running
+// sum).  The target-distribution entry reports p / Z and always needs it.
+__device__ __forceinline__ bool list_needs_z(const dsv_verify_args& a, float top_p) {
+  if (!a.candidates) return true;
+  if (a.backend == DSV_BACKEND_FLASHINFER && a.need_min_p) return false;
+  return top_p < 1.f;
+}
+
 // The first cut tie of a key held by cnt values of probability p each, with mass sb and cb values
 // ahead of it in (value desc, id asc) order: the top-k rank, the min-p floor and the top-p test
 // are each monotone along that order.  Returns cnt when none of the ties is cut.

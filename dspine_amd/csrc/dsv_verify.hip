@@ -698,7 +698,10 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     return;
   }
   const float c2 = log2e_over(T);
-  const double Z = wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0);
+  // (support-list rows whose filter does not read Z: p up to the factor 1/Z, renormalised below)
+  const bool nz = mode != M_LIST || list_needs_z(a, pre.top_p);
+  const double Z =
+      nz ? wave_sum(m_l > -INFINITY ? s_l * (double)__builtin_amdgcn_exp2f((m_l - M) * c2) : 0.0) : 1.0;
   const float m_f = M / T;
   const float invZ = (float)(1.0 / Z);
   rs.Z = Z;
@@ -732,7 +735,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     const double S_all = wave_tiles((double)p, lo_p, hi_p);
     const float top_p = pre.top_p;
     const float min_p = pre.min_p;
-    bool keep = live && lane < pre.top_k && !topp_fails(a.backend, lo_p, p, top_p);
+    bool keep = live && lane < pre.top_k && (!nz || !topp_fails(a.backend, lo_p, p, top_p));
     if (a.need_min_p) {
       if (a.backend == DSV_BACKEND_FLASHINFER) {
         // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
@@ -1887,7 +1890,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   out.xtok = 0.f;
   out.pad = 0;
 
-  if (P.softmax && mode != M_GREEDY && cbest) {
+  // the softmax partial sum (support-list rows of the step only when their top-p test needs Z)
+  if (P.softmax && mode != M_GREEDY && cbest && (mode != M_LIST || list_needs_z(a, top_p))) {
     const float c2 = log2e_over(T);
     const float mc2 = out.m * c2;
     float st_ = 0.f;
