@@ -960,50 +960,80 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     }
     m_total += sh.wm[i];
   }
-  uint64_t cut = ~0ull;
-  double cutS = 0.0;
-  for (int q0 = wid * SL; q0 < q_end && cut == ~0ull; q0 += WAVE) {
-    const int q = q0 + lane;
-    const uint32_t cnt = q < q_end ? sh.h[q] : 0u;
-    if (__ballot(cnt != 0u) == 0ull) continue;
-    const uint32_t k = kmax - (uint32_t)q;
-    const float p = cnt ? prob_of(value_of_key<DT>(k), T, m_f, invZ) : 0.f;
-    double lo_m, hi_m;
-    const double it_m = wave_tiles((double)cnt * (double)p, lo_m, hi_m);
-    int64_t c_excl = wave_incl_scan((int64_t)cnt);
-    const int64_t it_c = readlane<WAVE - 1>(c_excl);
-    c_excl -= cnt;
-    uint64_t f = ~0ull;
-    double fS = 0.0;
-    if (cnt) {
-      const double sb = run_S + lo_m;
-      const int64_t fail = cut_index(a.backend, cnt, p, sb, run_C + c_excl, topk, min_p, thr_minp, top_p);
-      if (fail < (int64_t)cnt) {
-        f = ((uint64_t)(uint32_t)fail << 32) | k;
-        fS = sb + (double)fail * (double)p;
+  // The first value (value desc, id asc) that the filter (rank < tk, p >= mp * max, mass
+  // ahead within tp) removes in the merged window: fc = its key | tie index << 32 (~0: none in
+  // the window), fS the mass kept before it.
+  auto find_cut = [&](int tk, float mp, float tp, uint64_t& fc, double& fS) {
+    double rS = run_S;
+    int64_t rC = run_C;
+    uint64_t cut = ~0ull;
+    double cutS = 0.0;
+    for (int q0 = wid * SL; q0 < q_end && cut == ~0ull; q0 += WAVE) {
+      const int q = q0 + lane;
+      const uint32_t cnt = q < q_end ? sh.h[q] : 0u;
+      if (__ballot(cnt != 0u) == 0ull) continue;
+      const uint32_t k = kmax - (uint32_t)q;
+      const float p = cnt ? prob_of(value_of_key<DT>(k), T, m_f, invZ) : 0.f;
+      double lo_m, hi_m;
+      const double it_m = wave_tiles((double)cnt * (double)p, lo_m, hi_m);
+      int64_t c_excl = wave_incl_scan((int64_t)cnt);
+      const int64_t it_c = readlane<WAVE - 1>(c_excl);
+      c_excl -= cnt;
+      uint64_t f = ~0ull;
+      double fSl = 0.0;
+      if (cnt) {
+        const double sb = rS + lo_m;
+        const int64_t fail = cut_index(a.backend, cnt, p, sb, rC + c_excl, tk, mp, thr_minp, tp);
+        if (fail < (int64_t)cnt) {
+          f = ((uint64_t)(uint32_t)fail << 32) | k;
+          fSl = sb + (double)fail * (double)p;
+        }
       }
+      const uint64_t who = __ballot(f != ~0ull);
+      if (who) {
+        const int src = __ffsll((long long)who) - 1;
+        cut = readlane_at(f, src);
+        cutS = readlane_at(fSl, src);
+      }
+      rS += it_m;
+      rC += it_c;
     }
-    const uint64_t who = __ballot(f != ~0ull);
-    if (who) {
-      const int src = __ffsll((long long)who) - 1;
-      cut = readlane_at(f, src);
-      cutS = readlane_at(fS, src);
+    __syncthreads();  // (readers of an earlier call's results)
+    if (lane == 0) {
+      sh.cut[wid] = cut;
+      sh.cutS[wid] = cutS;
     }
-    run_S += it_m;
-    run_C += it_c;
-  }
-  if (lane == 0) {
-    sh.cut[wid] = cut;
-    sh.cutS[wid] = cutS;
-  }
-  __syncthreads();
-  uint64_t fc = ~0ull;
-  double fS = 0.0;
-  for (int i = 0; i < NW && fc == ~0ull; ++i) {
-    fc = sh.cut[i];
-    fS = sh.cutS[i];
-  }
+    __syncthreads();
+    fc = ~0ull;
+    fS = 0.0;
+    for (int i = 0; i < NW && fc == ~0ull; ++i) {
+      fc = sh.cut[i];
+      fS = sh.cutS[i];
+    }
+  };
   const bool x_untracked = __ballot(lane < C && x_l == KX_UNKNOWN) != 0ull;
+  float top_p_eff = top_p;
+  if (a.backend == DSV_BACKEND_FLASHINFER && min_p > 0.f) {
+    // flashinfer's min-p branch renormalises over the top-k before its top-p test: a value is
+    // kept while (mass ahead) / S_k <= top_p, S_k the top-k's mass (a rank-only cut first)
+    uint64_t kc;
+    double kS;
+    find_cut(topk, 0.f, INFINITY, kc, kS);
+    if (kc == ~0ull && (int64_t)topk < a.vocab) {
+      // the top-k reaches below the window: the full histogram decides the row
+      if (tid == 0) {
+        rs.flags = FLAG_FULL_HIST;
+        ro->rs = rs;
+        ro->ok = 0;
+        ro->nuc = 1;
+      }
+      return;
+    }
+    top_p_eff = (float)((double)top_p * (kc != ~0ull ? kS : Z * (double)invZ));
+  }
+  uint64_t fc;
+  double fS;
+  find_cut(topk, min_p, top_p_eff, fc, fS);
   if (fc == ~0ull && (kcov > sh.kb_row || x_untracked)) {
     // the cut lies below a chunk's window (or below every window, where a chunk did not
     // track its largest value): the full histogram decides it
@@ -1275,64 +1305,83 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   const float top_p = a.top_ps[b];
   const float min_p = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;
   const float thr_minp = prob_of(M, T, m_f, invZ) * min_p;
-  uint64_t cut = ~0ull;
-  double cutS = 0.0;
-  for (int i = 0; i < NUC_ITERS && cut == ~0ull; ++i) {
-    const int wd = nuc_word(wid, i, lane);
-    const uint2 g = gsum[wd];
-    const uint32_t c_hi = g.y, c_lo = g.x;
-    if (__ballot((c_hi | c_lo) != 0u) == 0ull) continue;
-    const uint32_t k_hi = 2u * (uint32_t)wd + 1u, k_lo = 2u * (uint32_t)wd;
-    const float p_hi = c_hi ? prob_of(value_of_key<DT>(k_hi), T, m_f, invZ) : 0.f;
-    const float p_lo = c_lo ? prob_of(value_of_key<DT>(k_lo), T, m_f, invZ) : 0.f;
-    double lo_m, hi_m;
-    const double it_m = wave_tiles((double)c_hi * (double)p_hi + (double)c_lo * (double)p_lo, lo_m, hi_m);
-    const int64_t c_word = (int64_t)c_hi + c_lo;
-    int64_t c_excl = wave_incl_scan(c_word);
-    const int64_t it_c = readlane<WAVE - 1>(c_excl);
-    c_excl -= c_word;
-    uint64_t f = ~0ull;
-    double fS = 0.0;
-    double sb = run_S + lo_m;
-    int64_t cb = run_C + c_excl;
-    if (c_hi) {
-      const int64_t fail = cut_index(a.backend, c_hi, p_hi, sb, cb, topk, min_p, thr_minp, top_p);
-      if (fail < (int64_t)c_hi) {
-        f = ((uint64_t)(uint32_t)fail << 32) | k_hi;
-        fS = sb + (double)fail * (double)p_hi;
-      } else {
-        sb += (double)c_hi * (double)p_hi;
-        cb += c_hi;
+  // The first value (value desc, id asc) that the filter (rank < tk, p >= mp * max, mass ahead
+  // within tp) removes: fc = its key | tie index << 32 (~0: none), fS the mass kept before it.
+  auto find_cut = [&](int tk, float mp, float tp, uint64_t& fc, double& fS) {
+    double rS = run_S;
+    int64_t rC = run_C;
+    uint64_t cut = ~0ull;
+    double cutS = 0.0;
+    for (int i = 0; i < NUC_ITERS && cut == ~0ull; ++i) {
+      const int wd = nuc_word(wid, i, lane);
+      const uint2 g = gsum[wd];
+      const uint32_t c_hi = g.y, c_lo = g.x;
+      if (__ballot((c_hi | c_lo) != 0u) == 0ull) continue;
+      const uint32_t k_hi = 2u * (uint32_t)wd + 1u, k_lo = 2u * (uint32_t)wd;
+      const float p_hi = c_hi ? prob_of(value_of_key<DT>(k_hi), T, m_f, invZ) : 0.f;
+      const float p_lo = c_lo ? prob_of(value_of_key<DT>(k_lo), T, m_f, invZ) : 0.f;
+      double lo_m, hi_m;
+      const double it_m = wave_tiles((double)c_hi * (double)p_hi + (double)c_lo * (double)p_lo, lo_m, hi_m);
+      const int64_t c_word = (int64_t)c_hi + c_lo;
+      int64_t c_excl = wave_incl_scan(c_word);
+      const int64_t it_c = readlane<WAVE - 1>(c_excl);
+      c_excl -= c_word;
+      uint64_t f = ~0ull;
+      double fSl = 0.0;
+      double sb = rS + lo_m;
+      int64_t cb = rC + c_excl;
+      if (c_hi) {
+        const int64_t fail = cut_index(a.backend, c_hi, p_hi, sb, cb, tk, mp, thr_minp, tp);
+        if (fail < (int64_t)c_hi) {
+          f = ((uint64_t)(uint32_t)fail << 32) | k_hi;
+          fSl = sb + (double)fail * (double)p_hi;
+        } else {
+          sb += (double)c_hi * (double)p_hi;
+          cb += c_hi;
+        }
       }
-    }
-    if (c_lo && f == ~0ull) {
-      const int64_t fail = cut_index(a.backend, c_lo, p_lo, sb, cb, topk, min_p, thr_minp, top_p);
-      if (fail < (int64_t)c_lo) {
-        f = ((uint64_t)(uint32_t)fail << 32) | k_lo;
-        fS = sb + (double)fail * (double)p_lo;
+      if (c_lo && f == ~0ull) {
+        const int64_t fail = cut_index(a.backend, c_lo, p_lo, sb, cb, tk, mp, thr_minp, tp);
+        if (fail < (int64_t)c_lo) {
+          f = ((uint64_t)(uint32_t)fail << 32) | k_lo;
+          fSl = sb + (double)fail * (double)p_lo;
+        }
       }
+      const uint64_t who = __ballot(f != ~0ull);
+      if (who) {
+        const int src = __ffsll((long long)who) - 1;
+        cut = readlane_at(f, src);
+        cutS = readlane_at(fSl, src);
+      }
+      rS += it_m;
+      rC += it_c;
     }
-    const uint64_t who = __ballot(f != ~0ull);
-    if (who) {
-      const int src = __ffsll((long long)who) - 1;
-      cut = readlane_at(f, src);
-      cutS = readlane_at(fS, src);
+    __syncthreads();  // (readers of an earlier call's results)
+    if (lane == 0) {
+      sh.cut[wid] = cut;
+      sh.cutS[wid] = cutS;
     }
-    run_S += it_m;
-    run_C += it_c;
-  }
-  if (lane == 0) {
-    sh.cut[wid] = cut;
-    sh.cutS[wid] = cutS;
-  }
-  __syncthreads();
-  if (tid < WAVE) {
-    uint64_t fc = ~0ull;
-    double fS = 0.0;
+    __syncthreads();
+    fc = ~0ull;
+    fS = 0.0;
     for (int i = 0; i < NUC_WAVES && fc == ~0ull; ++i) {
       fc = sh.cut[i];
       fS = sh.cutS[i];
     }
+  };
+  float top_p_eff = top_p;
+  if (a.backend == DSV_BACKEND_FLASHINFER && min_p > 0.f) {
+    // flashinfer's min-p branch: top-p on the mass renormalised over the top-k (S_k from a
+    // rank-only cut; no rank cut: the whole mass)
+    uint64_t kc;
+    double kS;
+    find_cut(topk, 0.f, INFINITY, kc, kS);
+    top_p_eff = (float)((double)top_p * (kc != ~0ull ? kS : m_total));
+  }
+  uint64_t fc;
+  double fS;
+  find_cut(topk, min_p, top_p_eff, fc, fS);
+  if (tid < WAVE) {
     if (fc == ~0ull) {
       rs.vcut = 0u;
       rs.ktie = INT_MAX;
@@ -1592,28 +1641,44 @@ __device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucL
   f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 0, 0u, L, ktok, tok, tie_before);
   f32_prefix(L, 0, sh);
   const int64_t tie_tok = (int64_t)block_sum<NUC_WAVES>((uint64_t)tie_before, sh.u);
-  bool found = false;
-  int b0 = f32_next(L, 0, -1, true, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, topk, min_p, thr_minp, top_p, sh);
-  // the first bin that can hold the cut, else the next non-empty one (a margin of rounding may
-  // need one more)
-  for (int t0 = 0; t0 < 3 && b0 >= 0 && !found; ++t0) {
-    const uint64_t c0 = L.pcnt[0][b0], m0 = L.pmass[0][b0];
-    f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 1, (uint32_t)b0, L, ktok, tok, unused);
-    f32_prefix(L, 1, sh);
-    int b1 = f32_next(L, 1, -1, true, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, topk, min_p, thr_minp, top_p, sh);
-    for (int t1 = 0; t1 < 3 && b1 >= 0 && !found; ++t1) {
-      const uint32_t prefix = ((uint32_t)b0 << 11) | (uint32_t)b1;
-      f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 2, prefix, L, ktok, tok, unused);
-      found = f32_walk(L, prefix, c0 + L.pcnt[1][b1], m0 + L.pmass[1][b1], T, m_f, invZ, a.backend, topk, min_p,
-                       thr_minp, top_p, sh);
+  // The first value (value desc, id asc) that the filter (rank < tk, p >= mp * max, mass ahead
+  // within tp) removes, into sh.cut_key / cut_tie / cut_S; false when it keeps every value.
+  // The level-0 bins serve every call.
+  auto descend = [&](int tk, float mp, float tp) -> bool {
+    bool found = false;
+    int b0 = f32_next(L, 0, -1, true, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, tk, mp, thr_minp, tp, sh);
+    // the first bin that can hold the cut, else the next non-empty one (a margin of rounding
+    // may need one more)
+    for (int t0 = 0; t0 < 3 && b0 >= 0 && !found; ++t0) {
+      const uint64_t c0 = L.pcnt[0][b0], m0 = L.pmass[0][b0];
+      f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 1, (uint32_t)b0, L, ktok, tok, unused);
+      f32_prefix(L, 1, sh);
+      int b1 = f32_next(L, 1, -1, true, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, tk, mp, thr_minp, tp, sh);
+      for (int t1 = 0; t1 < 3 && b1 >= 0 && !found; ++t1) {
+        const uint32_t prefix = ((uint32_t)b0 << 11) | (uint32_t)b1;
+        f32_pass<ALIGNED>(P, b, rowp, pres, rep, T, m_f, invZ, 2, prefix, L, ktok, tok, unused);
+        found = f32_walk(L, prefix, c0 + L.pcnt[1][b1], m0 + L.pmass[1][b1], T, m_f, invZ, a.backend, tk, mp,
+                         thr_minp, tp, sh);
+        if (!found)
+          b1 = f32_next(L, 1, F32_BINS - 1 - b1, false, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, tk, mp,
+                        thr_minp, tp, sh);
+      }
       if (!found)
-        b1 = f32_next(L, 1, F32_BINS - 1 - b1, false, (uint32_t)b0, c0, m0, T, m_f, invZ, a.backend, topk, min_p,
-                      thr_minp, top_p, sh);
+        b0 = f32_next(L, 0, F32_BINS - 1 - b0, false, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, tk, mp, thr_minp,
+                      tp, sh);
     }
-    if (!found)
-      b0 = f32_next(L, 0, F32_BINS - 1 - b0, false, 0u, 0ull, 0ull, T, m_f, invZ, a.backend, topk, min_p, thr_minp,
-                    top_p, sh);
+    return found;
+  };
+  float top_p_eff = top_p;
+  if (a.backend == DSV_BACKEND_FLASHINFER && min_p > 0.f) {
+    // flashinfer's min-p branch: top-p on the mass renormalised over the top-k (S_k from a
+    // rank-only descent; no rank cut: the whole mass)
+    const bool kf = descend(topk, 0.f, INFINITY);
+    const double Sk = kf ? sh.cut_S : (double)(L.pmass[0][0] + L.mass[0][0]) / FX_ONE;
+    top_p_eff = (float)((double)top_p * Sk);
+    __syncthreads();  // (sh.cut_S read before the next descent)
   }
+  const bool found = descend(topk, min_p, top_p_eff);
   if (tid < WAVE) {
     if (found) {
       rs.vcut = sh.cut_key;
@@ -2705,8 +2770,6 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   if (a.backend != DSV_BACKEND_PYTORCH && a.backend != DSV_BACKEND_FLASHINFER)
     DSV_FAIL(DSV_ERR_INVALID, "%s: unknown backend %d", what, a.backend);
   hist_possible = a.filter && a.max_top_k > DSV_LIST_K;
-  if (hist_possible && a.backend == DSV_BACKEND_FLASHINFER && a.need_min_p)
-    DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: flashinfer min-p branch with top_k > %d is not implemented", what, DSV_LIST_K);
   const int C = chunks_per_row(a.vocab, a.logits_dtype);
   if (C > NCHK)
     DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: vocab %lld needs %d chunks (> %d)", what, (long long)a.vocab, C, NCHK);

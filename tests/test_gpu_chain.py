@@ -291,6 +291,25 @@ def test_build_target_probs_nucleus(device, dtype):
     torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_build_target_probs_flashinfer_min_p(device, dtype):
+    """flashinfer's min-p branch on nucleus rows (top-k off or > 64): top-p on the mass
+    renormalised over the top-k, then min-p against the max (tests/ref_utils.py:79-108)."""
+    from dspine_amd.runtime.worker import build_dspine_target_probs
+
+    O = _O()
+    bs, T, V = 6, 2, 50021
+    g = torch.Generator().manual_seed(33)
+    logits = (torch.randn(bs * T, V, generator=g) * 2.5).to(dtype)
+    info = W.sampling_info([1.0, 0.7, 1.0, 1.3, 1.0, 0.9], [0, 100, 1000, 0, 200, 0],
+                           [0.9, 0.5, 0.95, 0.8, 0.99, 1.0], [0.05, 1e-4, 0.1, 3e-4, 0.01, 1e-5])
+    got = build_dspine_target_probs(next_token_logits=logits.to(device), sampling_info=W.info_to(info, device),
+                                    block_size=T, bs=bs, sampling_backend="flashinfer")
+    torch.cuda.synchronize()
+    ref = O.build_target_probs(logits, info, T, bs, "flashinfer", exact_softmax=True)
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
+
+
 @pytest.mark.parametrize("normalize", [True, False])
 def test_filter_target_probs(device, normalize):
     from dspine_amd.runtime.worker import filter_target_probs

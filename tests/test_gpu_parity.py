@@ -342,6 +342,31 @@ def test_verify_nucleus_paths(device, case, dtype):
     assert len(compare_outputs(gpu, ref, range(bs), f"nucleus {case}")) <= 1
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", ["windows", "flat"])
+def test_verify_flashinfer_min_p_nucleus(device, case, dtype):
+    # flashinfer's min-p branch (tests/ref_utils.py:79-108): renormalise over the top-k, top-p
+    # on that mass, then min-p against the max -- on nucleus rows (top-k off or > 64, one
+    # support-list row beside them), min-p both dominating and negligible; "flat" (temperature
+    # 40) sends the bf16 rows to the full histogram
+    V = 151936
+    bs, T = 6, 3
+    batch = _small_batch(31, bs=bs, T=T, V=V, K=4, dtype=dtype, mixed=False, penalties=True)
+    g = torch.Generator().manual_seed(32)
+    batch["logits"] = (torch.randn(bs * T, V, generator=g) * 2.0).to(dtype)
+    temps = [40.0] * bs if case == "flat" else [1.0, 0.7, 1.0, 0.7, 1.0, 0.7]
+    batch["info"] = W.sampling_info(temps, [0, 100, 1000, 20, 5000, 0], [0.9, 0.8, 0.95, 0.5, 0.9, 1.0],
+                                    min_ps=[0.05, 1e-4, 0.1, 3e-4, 0.01, 1e-5])
+    base = batch["logits"].float()
+    for b in range(bs):  # a likely token as a q lane, so some drafts are accepted
+        for s_ in range(T - 1):
+            batch["q_ids"][b, s_, 0] = int(base[b * T + s_].argmax())
+    batch["q_ids"], _ = batch["q_ids"].sort(-1)
+    gpu = run_gpu_verify(batch, device, backend="flashinfer")
+    ref = run_oracle(batch, list(range(bs)), backend="flashinfer", exact_softmax=True)
+    assert len(compare_outputs(gpu, ref, range(bs), f"flashinfer min-p {case}")) <= 1
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_verify_large_vocab(device, dtype):
     """262144-wide rows (26 float32 / 13 bf16 chunks a row), ragged, mixed list / nucleus /
