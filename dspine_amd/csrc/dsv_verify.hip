@@ -1821,61 +1821,57 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     int hv = 0;
 #pragma unroll
     for (int u = 0; u < CV; ++u) hv += bits[u] != 0u;
-    int pre = 0, tot = 0;  // exclusive prefix and total of the hit vectors over the wave
-    for (int k = 1;; ++k) {
-      const uint64_t bal = __ballot(hv >= k);
-      if (!bal) break;
-      pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-      tot += __popcll(bal);
-    }
+    // exclusive prefix and total of the hit vectors over the wave (a DPP scan)
+    const int incl = wave_incl_scan(hv);
+    const int tot = readlane<WAVE - 1>(incl);
     uint4* wv = s_hv + wid * WHITV;
     uint32_t* wm = s_hm + wid * WHITV;
-    int slot = pre;
+    // rounds of the wave's LDS slots (one unless the history is long): the round's hit vectors
+    // are copied out, one lane per vector penalises their elements, the owners read them back
+    for (int r0 = 0; r0 < tot; r0 += WHITV) {
+      int slot = incl - hv - r0;
 #pragma unroll
-    for (int u = 0; u < CV; ++u) {
-      if (bits[u]) {
-        if (slot < WHITV) {
-          wv[slot] = v[u];
-          wm[slot] = bits[u];
-        } else {  // beyond the wave's LDS slots: in place
-          uint32_t bu = bits[u];
-          while (bu) {
-            const int e = __ffs(bu) - 1;
-            bu &= bu - 1u;
-            vec_set_dyn<DT>(v[u], e, penalize<DT>(vec_elem_dyn<DT>(v[u], e), pres, rep));
+      for (int u = 0; u < CV; ++u) {
+        if (bits[u]) {
+          if ((unsigned)slot < (unsigned)WHITV) {
+            wv[slot] = v[u];
+            wm[slot] = bits[u];
+          }
+          ++slot;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int nv = tot - r0 < WHITV ? tot - r0 : WHITV;
+      for (int i = lane; i < nv; i += WAVE) {
+        uint32_t m = wm[i];
+        while (m) {
+          const int e = __ffs(m) - 1;
+          m &= m - 1u;
+          if constexpr (DT == DSV_BF16) {
+            uint16_t* el = reinterpret_cast<uint16_t*>(&wv[i]) + e;
+            *el = (uint16_t)(__float_as_uint(penalize<DT>(bf16_bits_to_f32(*el), pres, rep)) >> 16);
+          } else {
+            float* el = reinterpret_cast<float*>(&wv[i]) + e;
+            *el = penalize<DT>(*el, pres, rep);
           }
         }
-        ++slot;
       }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int nv = tot < WHITV ? tot : WHITV;
-    for (int i = lane; i < nv; i += WAVE) {
-      uint32_t m = wm[i];
-      while (m) {
-        const int e = __ffs(m) - 1;
-        m &= m - 1u;
-        if constexpr (DT == DSV_BF16) {
-          uint16_t* el = reinterpret_cast<uint16_t*>(&wv[i]) + e;
-          *el = (uint16_t)(__float_as_uint(penalize<DT>(bf16_bits_to_f32(*el), pres, rep)) >> 16);
-        } else {
-          float* el = reinterpret_cast<float*>(&wv[i]) + e;
-          *el = penalize<DT>(*el, pres, rep);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      slot = incl - hv - r0;
+#pragma unroll
+      for (int u = 0; u < CV; ++u) {
+        if (bits[u]) {
+          if ((unsigned)slot < (unsigned)WHITV) v[u] = wv[slot];
+          ++slot;
         }
       }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    slot = pre;
-#pragma unroll
-    for (int u = 0; u < CV; ++u) {
-      if (bits[u]) {
-        if (slot < WHITV) v[u] = wv[slot];
-        ++slot;
-      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 

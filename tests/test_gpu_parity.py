@@ -277,6 +277,19 @@ def test_verify_row_layouts(device, dtype, V, stride):
     assert len(compare_outputs(gpu, ref, range(bs), f"layout V={V} stride={stride}")) <= 1
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_long_history(device, dtype):
+    # a history of 6000 tokens over 20483 ids: more vectors hold a penalised value than a
+    # wave's LDS slots, so every lane penalises its own elements in place
+    batch = _small_batch(13, bs=8, T=5, V=20483, K=4, dtype=dtype, mixed=True, penalties=True)
+    g = torch.Generator().manual_seed(14)
+    bs = batch["candidates"].shape[0]
+    batch["hist_ids"] = torch.randint(-1, 20483, (bs, 6000), generator=g, dtype=torch.int64).to(torch.int32)
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    assert len(compare_outputs(gpu, ref, range(bs), f"long history {dtype}")) <= 1
+
+
 @pytest.mark.parametrize("V,stride", [(997, 1000), (70001, 70008)])
 def test_greedy_and_topk_row_layouts(device, V, stride):
     from dspine_amd.kernels.dspine import topk
