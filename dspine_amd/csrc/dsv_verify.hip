@@ -2023,6 +2023,10 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
           // tracked here (the merge takes the full-histogram path if it needs it).
           const uint32_t cb = wlo - 0x8000u;
           const uint32_t cb2 = cb | (cb << 16);
+          // the increment and the byte-offset shift held in registers for the whole loop (the
+          // compiler would otherwise materialise both for every element)
+          uint32_t one = 1u, two = 2u;
+          asm volatile("" : "+v"(one), "+v"(two));
 #pragma unroll
           for (int u = 0; u < CV; ++u) {
             reg_fence1(v[u]);
@@ -2031,8 +2035,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
             for (int q = 0; q < 4; ++q) {
               const uint32_t o2 = sub_u16x2(w4[q], cb2);
               const uint32_t o0 = o2 & 0xffffu, o1 = o2 >> 16;
-              if (o0 < W) atomicAdd(&cnt[o0], 1u);
-              if (o1 < W) atomicAdd(&cnt[o1], 1u);
+              if (o0 < W) __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(cnt) + (o0 << two)), one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+              if (o1 < W) __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(cnt) + (o1 << two)), one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
           }
           kx = KX_UNKNOWN;
@@ -2108,19 +2112,14 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 #pragma unroll
         for (int e = 0; e < n; ++e)
           am |= (uint32_t)(key_of<DT>(vec_elem<DT>(w, e)) >= thr && j0 + e < hi) << e;
-        // slots: a prefix over the wave and one LDS atomic a wave
+        // slots: a prefix over the wave (DPP scan) and one LDS atomic a wave
         const int na = __popc(am);
-        int pre = 0, tot = 0;
-        for (int k = 1;; ++k) {
-          const uint64_t bal = __ballot(na >= k);
-          if (!bal) break;
-          pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          tot += __popcll(bal);
-        }
+        const int incl = wave_incl_scan(na);
+        const int tot = readlane<WAVE - 1>(incl);
         if (tot) {
           int base = 0;
           if (lane == 0) base = atomicAdd(&s_cnt, tot);
-          int at = __shfl(base, 0, WAVE) + pre;
+          int at = readlane<0>(base) + incl - na;
 #pragma unroll
           for (int e = 0; e < n; ++e) {
             if ((am >> e) & 1u) {
