@@ -159,6 +159,12 @@ __device__ __forceinline__ float vec_elem(const uint4& v, int e) {
     return __uint_as_float(w);
 }
 
+// The 16 bits of bf16 element e (0..7, a compile-time index) of a 16-byte vector.
+__device__ __forceinline__ uint32_t bf16_bits(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (e & 1) ? w >> 16 : w & 0xffffu;
+}
+
 typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t FILL_BF16 = 0xFF80FF80u;  // two bf16 -inf
 constexpr uint32_t FILL_F32 = 0xFF800000u;   // float -inf

@@ -2098,6 +2098,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
     __syncthreads();
     const int nq = s_nq;
+    const bool pos_thr = DT == DSV_BF16 && thr > 0x8000u;  // (the usual case)
+    const int t0 = (int)thr - 0x8000;
     if (nq <= STAGE_MAX) {
       for (int vb = 0; vb < nq * CV; vb += CT) {
         const int vi = vb + tid;
@@ -2109,9 +2111,19 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
           j0 = (v0 + (int64_t)u * CT + s_qtid[slot]) * n;
         }
         uint32_t am = 0u;  // the vector's admitted elements
+        if (pos_thr) {
+          // a positive bf16 threshold: a value reaches it iff its bits, as a signed 16-bit
+          // integer, reach thr - 0x8000 (negative values are negative integers); its key is
+          // then bits | 0x8000
 #pragma unroll
-        for (int e = 0; e < n; ++e)
-          am |= (uint32_t)(key_of<DT>(vec_elem<DT>(w, e)) >= thr && j0 + e < hi) << e;
+          for (int e = 0; e < n; ++e) am |= (uint32_t)((int)(int16_t)bf16_bits(w, e) >= t0) << e;
+          const int64_t nval = hi - j0;  // elements of the vector inside the row
+          am &= nval >= n ? 0xFFu : (nval <= 0 ? 0u : (1u << (uint32_t)nval) - 1u);
+        } else {
+#pragma unroll
+          for (int e = 0; e < n; ++e)
+            am |= (uint32_t)(key_of<DT>(vec_elem<DT>(w, e)) >= thr && j0 + e < hi) << e;
+        }
         // slots: a prefix over the wave (DPP scan) and one LDS atomic a wave
         const int na = __popc(am);
         const int incl = wave_incl_scan(na);
@@ -2123,7 +2135,8 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 #pragma unroll
           for (int e = 0; e < n; ++e) {
             if ((am >> e) & 1u) {
-              if (at < CAND_CAP) cbuf[at] = pack(key_of<DT>(vec_elem<DT>(w, e)), j0 + e);
+              const uint32_t key = pos_thr ? (bf16_bits(w, e) | 0x8000u) : key_of<DT>(vec_elem<DT>(w, e));
+              if (at < CAND_CAP) cbuf[at] = pack(key, j0 + e);
               ++at;
             }
           }
