@@ -156,7 +156,8 @@ __device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char*
 constexpr int FCT = 512;      // threads of k_final
 constexpr int DNW_MAX = FCT / WAVE;
 constexpr int64_t BONUS_LATER = -2;  // rbonus: the row is drawn in k_final
-constexpr int64_t BONUS_PLAN = -3;   // rbonus: k_final scans the row's planned chunk
+// rbonus <= BONUS_PLAN: k_final scans the row's planned chunk BONUS_PLAN - 1 - rbonus (-1: none)
+constexpr int64_t BONUS_PLAN = -3;
 
 struct DrawShared {
   double red_d[DNW_MAX];
@@ -282,46 +283,63 @@ struct RowPre {
 };
 
 // Thread t's span of chunk c in id order (NT threads tile the chunk: ids c*chunk + t*FE + [0,
-// FE)), penalised and handed to f(i, x) in id order; -inf past the row.
-template <int DT, bool ALIGNED, int NT, class F>
-__device__ __forceinline__ void for_span(const KParams& P, int b, const char* rowp, int c, float pres, float rep,
-                                         F&& f) {
+// FE)): its vectors and history bits, loaded by span_load and handed out penalised, in id
+// order, by span_each as f(i, x); -inf past the row.
+template <int DT, int NT>
+struct Span {
+  static constexpr int SV = CT * CV / NT, FE = SV * Elems<DT>::n;  // vectors and ids a thread
+  uint4 v[SV];
+  uint64_t blo, bhi;  // the span's history bits (tokens >= vocab have none)
+};
+template <int DT, bool ALIGNED, int NT>
+__device__ __forceinline__ void span_load(const KParams& P, int b, const char* rowp, int c, Span<DT, NT>& sp) {
   constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
-  constexpr int SV = CT * CV / NT, FE = SV * n;  // vectors and ids a thread
-  static_assert(SV * NT == CT * CV && FE <= 96, "spans tile a chunk");
+  constexpr int SV = Span<DT, NT>::SV;
+  static_assert(SV * NT == CT * CV && Span<DT, NT>::FE <= 96, "spans tile a chunk");
   const int64_t V = P.a.vocab;
   const int64_t clo = (int64_t)c * CHE, chi = clo + CHE < V ? clo + CHE : V;
-  const int64_t jlo = clo + (int64_t)threadIdx.x * FE;
-  uint4 v[SV];
+  const int64_t jlo = clo + (int64_t)threadIdx.x * Span<DT, NT>::FE;
   if constexpr (ALIGNED) {
     const auto rsr = buf_rsrc(rowp + clo * (16 / n), (uint32_t)((chi - clo) * (16 / n)));
 #pragma unroll
-    for (int u = 0; u < SV; ++u) v[u] = buf_load16(rsr, (uint32_t)threadIdx.x * (SV * 16u), (uint32_t)(u * 16));
+    for (int u = 0; u < SV; ++u) sp.v[u] = buf_load16(rsr, (uint32_t)threadIdx.x * (SV * 16u), (uint32_t)(u * 16));
 #pragma unroll
     for (int u = 0; u < SV; ++u)  // past the row: the buffer reads zeros; -inf and the partial last vector
-      if (jlo + u * n + n > chi) v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
+      if (jlo + u * n + n > chi) sp.v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
   } else {
 #pragma unroll
-    for (int u = 0; u < SV; ++u) v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
+    for (int u = 0; u < SV; ++u) sp.v[u] = load_vec<DT>(rowp, jlo / n + u, chi, false);
   }
-  uint64_t blo = 0, bhi = 0;  // the span's history bits (tokens >= vocab have none)
+  sp.blo = 0;
+  sp.bhi = 0;
   if (P.pbits) {
     const auto rb = buf_rsrc(P.pbits + (int64_t)b * P.pwords, (uint32_t)(P.pwords * 4));
     const uint32_t w0 = (uint32_t)(jlo >> 5) * 4u, sh = (uint32_t)(jlo & 31);
     const uint64_t A = (uint64_t)buf_load4(rb, w0, 0) | ((uint64_t)buf_load4(rb, w0, 4) << 32);
     const uint64_t B = (uint64_t)buf_load4(rb, w0, 8) | ((uint64_t)buf_load4(rb, w0, 12) << 32);
-    blo = (A >> sh) | (sh ? B << (64 - sh) : 0ull);
-    bhi = B >> sh;
+    sp.blo = (A >> sh) | (sh ? B << (64 - sh) : 0ull);
+    sp.bhi = B >> sh;
   }
+}
+template <int DT, int NT, class F>
+__device__ __forceinline__ void span_each(const Span<DT, NT>& sp, float pres, float rep, F&& f) {
+  constexpr int n = Elems<DT>::n;
 #pragma unroll
-  for (int u = 0; u < SV; ++u)
+  for (int u = 0; u < Span<DT, NT>::SV; ++u)
 #pragma unroll
     for (int e = 0; e < n; ++e) {
       const int i = u * n + e;
-      float x = vec_elem<DT>(v[u], e);
-      if (((i < 64 ? blo >> i : bhi >> (i - 64)) & 1ull)) x = penalize<DT>(x, pres, rep);
+      float x = vec_elem<DT>(sp.v[u], e);
+      if (((i < 64 ? sp.blo >> i : sp.bhi >> (i - 64)) & 1ull)) x = penalize<DT>(x, pres, rep);
       f(i, x);
     }
+}
+template <int DT, bool ALIGNED, int NT, class F>
+__device__ __forceinline__ void for_span(const KParams& P, int b, const char* rowp, int c, float pres, float rep,
+                                         F&& f) {
+  Span<DT, NT> sp;
+  span_load<DT, ALIGNED, NT>(P, b, rowp, c, sp);
+  span_each<DT, NT>(sp, pres, rep, f);
 }
 
 // Support-list draw (wave 0): entries sh.lst[0, sh.nlist) sorted by id; q staged when resid.
@@ -480,9 +498,10 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
 
 // Dense draw, second part: the planned chunk in id order -- per-thread masses, the thread whose
 // mass holds the threshold, then its ids.  Returns the token (every thread).
-template <int DT, bool ALIGNED, int NT>
+// PRE: the planned chunk's span is already loaded into `pre` (else loaded here).
+template <int DT, bool ALIGNED, int NT, bool PRE = false>
 __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
-                                              float pres, float rep, DrawShared& sh) {
+                                              float pres, float rep, DrawShared& sh, const Span<DT, NT>& pre) {
   constexpr int NW = NT / WAVE;
   constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
   static_assert(FE <= 64, "a thread's span fits a 64-bit mask");
@@ -506,7 +525,7 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
   uint64_t tmask = 0;  // span positions holding the cut key
   double mt = 0.0;
   int32_t tt = 0;
-  for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, [&](int i, float x) {
+  auto weigh = [&](int i, float x) {
     const uint32_t k = key_of<DT>(x);
     float wi = 0.f;
     if (!hist || k > rs.vcut) {
@@ -517,7 +536,11 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
     }
     w[i] = wi;
     mt += (double)wi;
-  });
+  };
+  if constexpr (PRE)  // the planned chunk's span, loaded by the caller (cstar is that chunk)
+    span_each<DT, NT>(pre, pres, rep, weigh);
+  else
+    for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, weigh);
   int32_t tie_tot = 0;
   const int32_t tbefore = sh.tieq + block_excl_scan<NW>(tt, sh.red_i, &tie_tot);
   int32_t kept_t = 0;
@@ -2321,7 +2344,7 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
       pl->use_r = ds.use_r;
       pl->pad = 0;
     }
-    bonus = BONUS_PLAN;
+    bonus = BONUS_PLAN - 1 - ds.chunk;  // (the chunk, for k_final's early loads)
   }
   if (threadIdx.x == 0) {
     P.rowsum[r] = rs;
@@ -2421,10 +2444,14 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   __syncthreads();
   const int acc = sh.acc;
   int64_t bonus = sh.bonus;
-  if (bonus == BONUS_PLAN) {  // the row merge planned the draw: scan the chunk
+  if (bonus <= BONUS_PLAN) {  // the row merge planned the draw: scan the chunk
     const int64_t rstar = row0 + acc;
     const bool resid = acc < cap - 1;
     const DrawPlan* pl = P.plans + rstar;
+    // the planned chunk's loads go out first, beside the plan's
+    const int cpl = (int)(BONUS_PLAN - 1 - bonus);  // (-1: no mass anywhere, no scan)
+    Span<DT, FCT> sp;
+    if (cpl >= 0) span_load<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), cpl, sp);
     if (tid < WAVE) {
       // the plan and the q lanes of the rejected draft in one round (dense_pick's first barrier
       // publishes them): ids, clamped values, whether the lane is the last with its id
@@ -2450,7 +2477,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       if (lane == 0) sh.qmask = qm;
     }
     const RowSum rs = P.rowsum[rstar];
-    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh);
+    bonus = dense_pick<DT, ALIGNED, FCT, true>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh, sp);
   } else if (bonus == BONUS_LATER) {
     const int64_t rstar = row0 + acc;
     const RowSum rs = P.rowsum[rstar];
@@ -2477,7 +2504,8 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     }
     __syncthreads();
     dense_plan<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, resid, uf, sh);
-    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh);
+    Span<DT, FCT> unused;
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh, unused);
     (void)CHE;
   }
   write_outputs(a, b, acc, bonus);
