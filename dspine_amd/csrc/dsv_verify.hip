@@ -42,7 +42,7 @@ struct KParams {
   int32_t* step_ok;       // [rows]: 1 when the draft token verified by the row is accepted
   uint32_t* pbits;        // [bs, pwords]: history bitmap of each request, NULL without history
   uint32_t* hpart;        // [rows, C, HWIN / 2]: nucleus rows' per-chunk window counts (16-bit pairs)
-  uint32_t* nhist;        // [NUC_GRID, 65536]: full-histogram counts, one area per k_nuc workgroup
+  uint32_t* nhist;        // [max(NUC_GRID, bs), 65536]: full-histogram counts, one area per workgroup
   int32_t* nuc_rows;      // [rows + 1]: the number of full-histogram rows, then their ids
   int64_t pwords;
   int32_t C;              // chunks per row
@@ -51,6 +51,7 @@ struct KParams {
   int32_t force_greedy;   // greedy-verify entry: every row is GREEDY
   int32_t softmax;        // chunk pass computes softmax partial sums (the verify entry)
   int32_t raw_p;          // dense target writer: the filtered p, not renormalised
+  int32_t final_nuc;      // k_final resolves the full-histogram rows (no k_nuc launch)
 };
 
 __device__ __forceinline__ const char* row_ptr(const dsv_verify_args& a, int64_t r) {
@@ -1203,7 +1204,10 @@ __device__ __forceinline__ int nuc_word(int wid, int i, int lane) {
 }
 
 template <int DT, bool ALIGNED>
-__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh) {
+// area: the workgroup's 65536-key accumulation area in P.nhist; ro: the row's result into LDS
+// (nullptr: RowSum and step decision stored to their arrays).
+__device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* hist, NucShared& sh, int area,
+                                        RowOut* ro) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   int b = 0, s = 0;
@@ -1229,7 +1233,7 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
   __syncthreads();
   const uint32_t ktok = sh.ktok;
   // 32-bit counts of key pairs, this workgroup's own area: (key 2wd, key 2wd + 1) at index wd
-  uint2* gsum = reinterpret_cast<uint2*>(P.nhist) + (int64_t)blockIdx.x * HIST_WORDS;
+  uint2* gsum = reinterpret_cast<uint2*>(P.nhist) + (int64_t)area * HIST_WORDS;
   uint32_t tie_before = 0;
   auto count = [&](float x, int64_t j) {
     const uint32_t k = key_of<DT>(x);
@@ -1415,7 +1419,7 @@ __device__ __forceinline__ void nuc_row(const KParams& P, int64_t r, uint32_t* h
       rs.S_kept = fS;
     }
     rs.S_f = (float)rs.S_kept;
-    nucleus_finish<DT>(P, r, b, s, rs, T, sh.xtok, tok, tie_tok, nullptr);
+    nucleus_finish<DT>(P, r, b, s, rs, T, sh.xtok, tok, tie_tok, ro);
   }
   __syncthreads();
 }
@@ -1636,7 +1640,8 @@ __device__ __forceinline__ bool f32_walk(const F32NucLds& L, uint32_t prefix, ui
 }
 
 template <bool ALIGNED>
-__device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucLds& L, F32NucShared& sh) {
+__device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucLds& L, F32NucShared& sh,
+                                            RowOut* ro) {
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x;
   int b = 0, s = 0;
@@ -1713,7 +1718,7 @@ __device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucL
       rs.S_kept = (double)(L.pmass[0][0] + L.mass[0][0]) / FX_ONE;
     }
     rs.S_f = (float)rs.S_kept;
-    nucleus_finish<DSV_F32>(P, r, b, s, rs, T, xt, tok, tie_tok, nullptr);
+    nucleus_finish<DSV_F32>(P, r, b, s, rs, T, xt, tok, tie_tok, ro);
   }
   __syncthreads();
 }
@@ -1732,10 +1737,10 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
     const int32_t row = P.nuc_rows[1 + i];
     if (row < 0 || row >= a.rows) continue;
     if constexpr (DT == DSV_BF16) {
-      nuc_row<DT, ALIGNED>(P, row, hist, sh);
+      nuc_row<DT, ALIGNED>(P, row, hist, sh, blockIdx.x, nullptr);
     } else {
       __shared__ F32NucShared fsh;
-      nuc_row_f32<ALIGNED>(P, row, *reinterpret_cast<F32NucLds*>(dyn), fsh);
+      nuc_row_f32<ALIGNED>(P, row, *reinterpret_cast<F32NucLds*>(dyn), fsh, nullptr);
     }
   }
 }
@@ -2400,7 +2405,10 @@ __device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, i
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   constexpr int CHE = Elems<DT>::chunk;
+  static_assert(FCT == NUC_THREADS, "k_final resolves full-histogram rows with the nucleus code");
+  extern __shared__ __align__(16) unsigned char dyn[];  // (final_nuc: the full-histogram LDS)
   __shared__ DrawShared sh;
+  __shared__ RowOut fro;  // a full-histogram row resolved here
   const dsv_verify_args& a = P.a;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
@@ -2419,31 +2427,58 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   const float pres = pen && a.presence ? a.presence[b] : 0.f;
   const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
   const float uf = a.uniform_final[b];
-  if (tid < WAVE) {
-    // the first rejected step (the last row ends every prefix) and the bonus its row drew, read
-    // together
-    int acc = cap - 1;
-    int64_t drawn = 0;
-    for (int s0 = 0; s0 < cap; s0 += WAVE) {
-      const int s = s0 + lane;
-      const int32_t ok = s < cap - 1 ? P.step_ok[row0 + s] : 0;
-      const int64_t rb = s < cap ? P.rbonus[row0 + s] : 0;
-      const uint64_t end = __ballot(s < cap && ok == 0);
-      if (end) {
-        const int l = __ffsll((long long)end) - 1;
-        acc = s0 + l;
-        drawn = readlane_at(rb, l);
-        break;
+  // the first step from s_from on that ends the prefix (a rejected draft; the last row ends every
+  // prefix) and the bonus its row's merge drew or planned, read together by wave 0
+  auto scan = [&](int s_from) {
+    if (tid < WAVE) {
+      int acc = cap - 1;
+      int64_t drawn = 0;
+      for (int s0 = s_from; s0 < cap; s0 += WAVE) {
+        const int s = s0 + lane;
+        const int32_t ok = s < cap - 1 ? P.step_ok[row0 + s] : 0;
+        const int64_t rb = s < cap ? P.rbonus[row0 + s] : 0;
+        const uint64_t end = __ballot(s < cap && ok == 0);
+        if (end) {
+          const int l = __ffsll((long long)end) - 1;
+          acc = s0 + l;
+          drawn = readlane_at(rb, l);
+          break;
+        }
+      }
+      if (tid == 0) {
+        sh.acc = acc;
+        sh.bonus = drawn;
       }
     }
-    if (tid == 0) {
-      sh.acc = acc;
-      sh.bonus = drawn;
+    __syncthreads();
+  };
+  scan(0);
+  int acc = sh.acc;
+  int64_t bonus = sh.bonus;
+  bool own = false;  // the accepted row's RowSum is fro.rs (resolved here)
+  if (P.final_nuc) {
+    // A row whose cut the merge's windows did not settle carries a placeholder decision (0):
+    // its full histogram decides it here, and the scan resumes after it when it accepts.
+    while (bonus == BONUS_LATER) {
+      const int64_t r = row0 + acc;
+      if constexpr (DT == DSV_BF16) {
+        __shared__ NucShared nsh;
+        nuc_row<DT, ALIGNED>(P, r, reinterpret_cast<uint32_t*>(dyn), nsh, b, &fro);
+      } else {
+        __shared__ F32NucShared fsh;
+        nuc_row_f32<ALIGNED>(P, r, *reinterpret_cast<F32NucLds*>(dyn), fsh, &fro);
+      }
+      __syncthreads();
+      if (acc < cap - 1 && fro.ok) {
+        scan(acc + 1);
+        acc = sh.acc;
+        bonus = sh.bonus;
+        continue;
+      }
+      own = true;
+      break;
     }
   }
-  __syncthreads();
-  const int acc = sh.acc;
-  int64_t bonus = sh.bonus;
   if (bonus <= BONUS_PLAN) {  // the row merge planned the draw: scan the chunk
     const int64_t rstar = row0 + acc;
     const bool resid = acc < cap - 1;
@@ -2480,7 +2515,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     bonus = dense_pick<DT, ALIGNED, FCT, true>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh, sp);
   } else if (bonus == BONUS_LATER) {
     const int64_t rstar = row0 + acc;
-    const RowSum rs = P.rowsum[rstar];
+    const RowSum rs = own ? fro.rs : P.rowsum[rstar];
     const bool resid = acc < cap - 1;
     stage_q(a, b, acc, resid, sh);
     const char* rowp = row_ptr(a, rstar);
@@ -2750,7 +2785,7 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.cstat, rows * C * (int64_t)sizeof(ChunkStat));
   take(w.cand, rows * C * (int64_t)kcand * 8);
   take(w.hpart, kcand ? rows * C * (int64_t)(HWIN / 2) * 4 : 0);
-  take(w.nhist, kcand ? (int64_t)NUC_GRID * 65536 * 4 : 0);
+  take(w.nhist, kcand ? (int64_t)(bs > NUC_GRID ? bs : NUC_GRID) * 65536 * 4 : 0);
   take(w.nuc, (rows + 1) * 4);
   take(w.rbonus, rows * 8);
   take(w.rties, rows * NCHK * 4);
@@ -2865,7 +2900,7 @@ static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipSt
       hipLaunchKernelGGL((k_merge<DSV_F32, false>), dim3((unsigned)a.rows), dim3(CT), 0, stream, P);
   }
   DSV_CHECK_LAUNCH("k_chunk / k_merge");
-  if (hist_possible) {  // nucleus rows the merge listed: the full histogram (bf16) or radix descent (fp32)
+  if (hist_possible && !P.final_nuc) {  // rows the merge listed: the full histogram (bf16) or radix descent (fp32)
     const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
     if (a.logits_dtype == DSV_BF16) {
       const size_t nuc_lds = (size_t)HIST_WORDS * 4;
@@ -2905,21 +2940,29 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   if (rc != DSV_OK) return rc;
   if (a.rows == 0) return DSV_OK;
   const int stages = a.stages ? a.stages : 7;
+  // with k_final in the launch, each request's workgroup resolves its own full-histogram rows
+  // (usually none: the merge's windows settle the cut) and no k_nuc launch is needed
+  P.final_nuc = (stages & 4) && hist_possible ? 1 : 0;
   if (stages & 1) {
     const int rc2 = launch_rows(P, hist_possible, true, stream);
     if (rc2 != DSV_OK) return rc2;
   }
   if (stages & 4) {
+    const size_t lds = !P.final_nuc ? 0 : a.logits_dtype == DSV_BF16 ? (size_t)HIST_WORDS * 4 : sizeof(F32NucLds);
+    auto go = [&](const void* fn, auto kernel) {
+      if (lds) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      hipLaunchKernelGGL(kernel, dim3(a.bs), dim3(FCT), lds, stream, P);
+    };
     if (a.logits_dtype == DSV_BF16) {
       if (P.aligned)
-        hipLaunchKernelGGL((k_final<DSV_BF16, true>), dim3(a.bs), dim3(FCT), 0, stream, P);
+        go((const void*)k_final<DSV_BF16, true>, k_final<DSV_BF16, true>);
       else
-        hipLaunchKernelGGL((k_final<DSV_BF16, false>), dim3(a.bs), dim3(FCT), 0, stream, P);
+        go((const void*)k_final<DSV_BF16, false>, k_final<DSV_BF16, false>);
     } else {
       if (P.aligned)
-        hipLaunchKernelGGL((k_final<DSV_F32, true>), dim3(a.bs), dim3(FCT), 0, stream, P);
+        go((const void*)k_final<DSV_F32, true>, k_final<DSV_F32, true>);
       else
-        hipLaunchKernelGGL((k_final<DSV_F32, false>), dim3(a.bs), dim3(FCT), 0, stream, P);
+        go((const void*)k_final<DSV_F32, false>, k_final<DSV_F32, false>);
     }
     DSV_CHECK_LAUNCH("k_final");
   }
