@@ -2,21 +2,24 @@
 // residual resample, accepted-prefix compaction and KV-slot gather.
 //
 // Launches of one verify step (no host synchronisation):
-//   k_prep   (spans x requests) penalty bitmap of each request's token history, 20480 ids a workgroup
+//   k_prep   (spans x requests) penalty bitmap of each request's token history, 20480 ids a
+//                               workgroup
 //   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 10240 fp32 values held in
-//                               registers: max/argmax, softmax partial sums, exact top-k
-//                               candidates, nucleus value counts -- one read of the logits
+//                               registers: penalties, max/argmax, softmax partial sums, exact
+//                               top-k candidates, nucleus value counts -- one read of the logits
 //   k_merge  (rows)             per row: Z, the filtered top-k support (id, P), P at the draft
 //                               token and the step's accept/reject decision; nucleus rows (a
 //                               top-p / min-p cut with top-k > 64) find their cut from the chunk
 //                               pass's value counts.  Then the bonus draw the row would give as
 //                               the accepted length: drawn for support-list rows, planned (the
 //                               chunk and threshold) for dense rows
-//   k_nuc    (<= 64 workgroups) nucleus rows those counts do not settle: the full 65536-key
-//                               value histogram of the row
-//   k_final  (requests)         accepted length from the row decisions, the bonus token of that
-//                               row (a dense row's planned chunk scanned here), outputs and KV
-//                               slots
+//   k_final  (requests)         rows those counts did not settle first (the full 65536-key
+//                               histogram, or the float32 radix descent, in the workgroup's LDS),
+//                               then the accepted length from the row decisions, the bonus token
+//                               of that row (a dense row's planned chunk scanned here), outputs
+//                               and KV slots
+// The target-distribution entry runs k_prep, k_chunk, k_merge, then k_nuc over the rows the
+// merge listed and k_dense_p.
 // Workgroups never wait on one another inside a kernel: on this multi-XCD part a device-scope
 // fence writes back and invalidates the whole L2, so every hand-off is a kernel boundary.
 //
