@@ -2057,10 +2057,12 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
           // the increment and the byte-offset shift held in registers for the whole loop (the
           // compiler would otherwise materialise both for every element)
           uint32_t one = 1u, two = 2u;
-          asm volatile("" : "+v"(one), "+v"(two));
 #pragma unroll
           for (int u = 0; u < CV; ++u) {
-            reg_fence1(v[u]);
+            // (redefines the two constants after vector u is read, which orders this vector's
+            // counts after the previous one's without redefining the vector itself: a copy of
+            // every vector at the branch's join otherwise)
+            asm volatile("" : "+v"(one), "+v"(two) : "v"(v[u].x), "v"(v[u].y), "v"(v[u].z), "v"(v[u].w));
             const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -2401,6 +2403,41 @@ __device__ __forceinline__ void write_outputs(const dsv_verify_args& a, int b, i
   }
 }
 
+// The gathers behind a request's outputs -- the draft token after position i and the KV slot of
+// position i -- for the positions i = threadIdx.x - WAVE of waves 1 on, issued before the accepted
+// length is known; write_outputs_at then only picks among them.
+struct OutGather {
+  int64_t tok = 0;
+  int32_t slot = -1;
+};
+__device__ __forceinline__ OutGather gather_outputs(const dsv_verify_args& a, int b, int i, int32_t plen) {
+  OutGather g;
+  if (i < 0 || i >= a.T) return g;
+  if (i + 1 < a.T) g.tok = a.candidates[(int64_t)b * a.T + i + 1];
+  if (a.kv_slots && a.page_table) {
+    const int64_t pos = (int64_t)plen + i;
+    if (pos >= 0 && pos < a.page_cols) g.slot = a.page_table[(int64_t)b * a.page_stride + pos];
+  }
+  return g;
+}
+// write_outputs with the gathers of gather_outputs (positions past the first FCT - WAVE gather here)
+__device__ __forceinline__ void write_outputs_at(const dsv_verify_args& a, int b, int acc, int64_t bonus,
+                                                 const OutGather& g, int stride, int32_t plen) {
+  const int T = a.T;
+  const int i0 = (int)threadIdx.x - WAVE;
+  for (int i = i0; i0 >= 0 && i < T; i += stride) {
+    const OutGather o = i == i0 ? g : gather_outputs(a, b, i, plen);
+    a.output[(int64_t)b * T + i] = i < acc ? o.tok : (i == acc ? bonus : 0);
+    if (a.kv_slots) a.kv_slots[(int64_t)b * T + i] = i <= acc ? o.slot : -1;
+  }
+  if (threadIdx.x == 0) {
+    a.accept[b] = acc;
+    a.commit[b] = acc + 1;
+    a.bonus[b] = bonus;
+    a.new_seq[b] = plen + acc + 1;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // k_final: outputs, one workgroup per request -- the accepted length a, and the bonus token of
 // row a (drawn by the row merge, or here for rows the full histogram settled)
@@ -2424,6 +2461,8 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     return;
   }
   if (row0 + cap > a.rows) cap = (int)(a.rows - row0);
+  const int32_t plen = a.prefix_lens[b];
+  const OutGather og = gather_outputs(a, b, tid - WAVE, plen);
   // the request's parameters for a dense draw, read with the step decisions
   const float T = a.temperatures[b];
   const bool pen = P.pbits != nullptr;
@@ -2546,7 +2585,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh, unused);
     (void)CHE;
   }
-  write_outputs(a, b, acc, bonus);
+  write_outputs_at(a, b, acc, bonus, og, FCT - WAVE, plen);
 }
 
 // ---------------------------------------------------------------------------------------
