@@ -241,6 +241,30 @@ __device__ __forceinline__ uint32_t wave_kth_key(uint32_t k, int J) {
   return pre;
 }
 
+// The smallest key k in [lo, hi] with pred(k), for a pred that is false and then true as the key
+// grows (hi is taken to hold it, untested): a 64-way search, one key a lane a round -- three rounds
+// for 16-bit keys -- where a bisection by one thread takes sixteen dependent steps.  Wave-wide
+// (every lane active); the result in every lane.
+template <class F>
+__device__ __forceinline__ uint32_t wave_first_key(uint32_t lo, uint32_t hi, F&& pred) {
+  const uint32_t lane = threadIdx.x & (WAVE - 1);
+  while (lo < hi) {
+    const uint32_t step = (hi - lo + WAVE - 1) / WAVE;
+    const uint32_t k = lo + lane * step;
+    const bool valid = k < hi;
+    const uint64_t yes = __ballot(valid && pred(k));
+    if (yes) {
+      const uint32_t f = (uint32_t)(__ffsll((long long)yes) - 1);
+      const uint32_t kf = lo + f * step;
+      lo = f == 0 ? lo : kf - step + 1;  // lane f - 1's key fails
+      hi = kf;
+    } else {
+      lo = lo + (uint32_t)(63 - __clzll((long long)__ballot(valid))) * step + 1;  // past the last key tried
+    }
+  }
+  return lo;
+}
+
 // Element e (a run-time index) of a vector, and its replacement: branch-free, through the two
 // 64-bit halves of the vector.
 template <int DT>

@@ -887,22 +887,17 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   const float min_p = a.need_min_p ? pre.min_p : 0.f;
   const int topk = pre.top_k;
   const int64_t tok = pre.tok;
-  if (tid == 0) {
+  if (tid < WAVE) {
     const double eps = (Z * (double)invZ - (double)top_p - 1e-6) / (double)a.vocab;
     uint32_t kb = 0x80u;  // the lowest finite key: no floor
-    if (eps > 0.0 && kmax >= 0x80u) {
-      uint32_t lo = 0x80u, hi = kmax;  // smallest key with p >= eps (p is non-decreasing in the key)
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if ((double)prob_of(value_of_key<DT>(mid), T, m_f, invZ) >= eps)
-          hi = mid;
-        else
-          lo = mid + 1;
-      }
-      kb = lo;
+    if (eps > 0.0 && kmax >= 0x80u)  // smallest key with p >= eps (p is non-decreasing in the key)
+      kb = wave_first_key(0x80u, kmax, [&](uint32_t k) {
+        return (double)prob_of(value_of_key<DT>(k), T, m_f, invZ) >= eps;
+      });
+    if (lane == 0) {
+      sh.kb_row = kb;
+      sh.xtok = (tok >= 0 && tok < a.vocab) ? cs[tok / Elems<DT>::chunk].xtok : -INFINITY;
     }
-    sh.kb_row = kb;
-    sh.xtok = (tok >= 0 && tok < a.vocab) ? cs[tok / Elems<DT>::chunk].xtok : -INFINITY;
   }
   __syncthreads();
   RowSum rs;
@@ -2005,7 +2000,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
       // reaches 2 (1 - top_p) / V.  The row merge takes the cut from the counts when it lies
       // in every chunk's window, and the full-histogram path otherwise.
       uint32_t* cnt = reinterpret_cast<uint32_t*>(big);
-      if (tid == 0) {
+      if (wid == 0) {
         uint32_t wlo = WIN_EMPTY;
         if (cbest) {
           const uint32_t kmax = unpack_key(cbest);
@@ -2013,20 +2008,14 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
           const float floor_e = 2.f * (1.f - top_p) / (float)V * (float)(out.s * (double)C);
           if (floor_e > 0.f && kmax > 0x80u) {
             const float c2 = log2e_over(T);
-            uint32_t l0 = 0x80u, l1 = kmax;
-            while (l0 < l1) {
-              const uint32_t mid = (l0 + l1) >> 1;
-              if (__builtin_amdgcn_exp2f((value_of_key<DT>(mid) - out.m) * c2) >= floor_e)
-                l1 = mid;
-              else
-                l0 = mid + 1;
-            }
-            kb = l0;
+            kb = wave_first_key(0x80u, kmax, [&](uint32_t k) {
+              return __builtin_amdgcn_exp2f((value_of_key<DT>(k) - out.m) * c2) >= floor_e;
+            });
           }
           const uint32_t wfloor = kmax >= (uint32_t)HWIN - 1u ? kmax - ((uint32_t)HWIN - 1u) : 0u;
           wlo = kb > wfloor ? kb : wfloor;
         }
-        s_wlo = wlo;
+        if (lane == 0) s_wlo = wlo;
       }
 #pragma unroll
       for (int i = tid; i < HWIN / 4; i += CT) big[i] = make_uint4(0u, 0u, 0u, 0u);
