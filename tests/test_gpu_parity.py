@@ -254,6 +254,27 @@ def test_verify_small_mixed(device, seed, dtype, penalties):
     assert len(near) <= 1
 
 
+@pytest.mark.parametrize("seed", [5, 6])
+def test_verify_page_table_edges(device, seed):
+    """KV slots where the committed positions run past the page table's columns (-1 there, as
+    the oracle's kv_slots), from prefix 0 and from the last column."""
+    batch = _small_batch(seed, dtype=torch.bfloat16, penalties=True)
+    bs, T = batch["candidates"].shape
+    g = torch.Generator().manual_seed(100 + seed)
+    cols = 24
+    batch["page_table"] = torch.randperm(bs * cols, generator=g).view(bs, cols).to(torch.int32)
+    prefix = torch.randint(cols - T, cols + 2, (bs,), generator=g, dtype=torch.int64)
+    prefix[0] = 0
+    prefix[1] = cols - 1
+    batch["prefix_lens"] = prefix.to(torch.int32)
+    batch["verify_lens"] = torch.full((bs,), T, dtype=torch.int32)
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    assert (ref["kv_slots"] == -1).any() and (ref["kv_slots"] >= 0).any()
+    near = compare_outputs(gpu, ref, range(bs), f"page edges seed={seed}")
+    assert len(near) <= 1
+
+
 @pytest.mark.parametrize("seed", [3, 4])
 def test_verify_small_ragged(device, seed):
     batch = _small_batch(seed, dtype=torch.bfloat16, ragged=True, penalties=True)
