@@ -1,23 +1,34 @@
 #!/usr/bin/env python3
-"""Benchmark of the full verify step at serving shape on one MI355X.
+"""Benchmark of the verification hot path on one MI355X.
 
-Workload (the headline configuration): 64 requests x 17 rows x 151936 vocab bf16 logits,
-per-request temperature {0, 0.6, 1.0}, top-k {off, 20}, top-p {1.0, 0.95}, presence/repetition
-penalties over a 512-token history, sparse draft q [64, 16, 16], int32 page table.  One step =
-logit adjustments -> target distribution -> chain rejection -> residual resample -> accepted-prefix
-compaction + KV-slot gather, on inputs already resident in HBM.  K steps are timed as plain stream
-launches and as HIP-graph replays (each bracketed by device synchronisation); the faster is the
-step time.
+Default workload (the headline configuration, ``--config 4``): the full verify step at serving
+shape -- 64 requests x 17 rows x 151936 vocab bf16 logits, per-request temperature {0, 0.6,
+1.0}, top-k {off, 20}, top-p {1.0, 0.95}, presence/repetition penalties over a 512-token
+history, sparse draft q [64, 16, 16], int32 page table.  One step = logit adjustments -> target
+distribution -> chain rejection -> residual resample -> accepted-prefix compaction + KV-slot
+gather, on inputs already resident in HBM.
+
+Other workloads (parity cases of the same path, timed the same way):
+  --config 2   top-k only: [1088, 151936] bf16 with planted peaks and duplicates, --k {1,20,64}
+  --config 3   rejection: 32 x 17 x 151936 fp32, top-k 20, top-p 0.95, sparse q (--sigma)
+  --config 5   ragged: 32 requests x U{4..16} rows x 262144 bf16 Student-t, top-p 0.9
+
+The logits of each step come from one of several identical copies in turn (together >= 661 MB,
+so no step reads data the previous steps left in the 256 MB Infinity Cache).  K steps are
+timed as plain stream launches and as HIP-graph replays, each bracketed by device
+synchronisation; the faster is the step time.
 
 Prints ONE JSON line (metric: verified rows/s) with the roofline of the dominant kernel -- the
 chunk pass k_chunk, which reads every logit once; its launches are bracketed by HIP events on
-their stream (dsv_profile_events) over a run of full steps -- and the CPU oracle timed on the
-host.  The HBM traffic figure comes from the committed rocprofv3 counter summary of that kernel
-(profiles/k_chunk_serving_traffic.txt) when it is present.
+their stream (dsv_profile_events) over a run of full steps -- the step's own fraction of peak
+(``step_frac``) and the CPU oracle timed on the host.  The HBM traffic figure comes from the
+committed rocprofv3 counter summary of that kernel (profiles/k_chunk_<workload>_traffic.txt)
+when one is present.
 """
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -27,25 +38,27 @@ sys.path.insert(0, ROOT)
 
 METRIC = "verify rows/sec at B=64x17x151936 bf16; achieved HBM GB/s vs peak"
 PEAK_GBPS = 8000.0  # MI355X HBM3E
+ROTATE_BYTES = 661 << 20  # logits copies read in turn: more than twice the 256 MB Infinity Cache
 
 
-def algorithmic_bytes(bs, T, V, K, hist_len):
-    """(whole step, chunk pass) algorithmic HBM bytes.  The step: one read of every verified
-    logit row plus the small per-request inputs and outputs.  The chunk pass k_chunk: the
-    logits (2 bytes per value) and each request's history bitmap (V/8 bytes, read once per
+def verify_bytes(bs, T, V, K, hist_len, esize, rows=None):
+    """(whole step, chunk pass) algorithmic HBM bytes of a fused verify step.  The step: one
+    read of every verified logit row plus the small per-request inputs and outputs.  The chunk
+    pass k_chunk: the logits and each request's history bitmap (V/8 bytes, read once per
     request; its rows find it in L2) -- its per-chunk statistics, candidates and value counts
     are workspace it writes for the merge (counted in the traffic figure, not here)."""
-    logits = bs * T * V * 2
+    rows = bs * T if rows is None else rows
+    logits = rows * V * esize
     small_in = (bs * hist_len * 4 + bs * (T - 1) * K * (8 + 4) + bs * T * 8 + bs * (T - 1) * 4 + bs * 4
                 + bs * 4 * 4 + bs * 4 + bs * T * 4)
     outputs = bs * (4 + 4 + 8 + 4) + bs * T * 8 + bs * T * 4
-    chunk_pass = logits + bs * ((V + 31) // 32) * 4
+    chunk_pass = logits + (bs * ((V + 31) // 32) * 4 if hist_len else 0)
     return logits + small_in + outputs, chunk_pass
 
 
-def committed_traffic():
+def committed_traffic(workload):
     """HBM bytes per k_chunk launch from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "k_chunk_serving_traffic.txt")
+    path = os.path.join(ROOT, "profiles", f"k_chunk_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -58,38 +71,60 @@ def time_kernel_events(step, steps, lib, torch):
     """Average k_chunk duration over `steps` eager steps: HIP events recorded by the library right
     before and after the kernel launch, on the stream it is launched on."""
     pairs = []
-    for _ in range(steps):
+    for i in range(steps):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         e.record()  # creates both events; the library re-records them around the kernel
         lib.dsv_profile_events(s.cuda_event, e.cuda_event)
-        step()
+        step(i)
         pairs.append((s, e))
     lib.dsv_profile_events(None, None)
     torch.cuda.synchronize()
     return sum(s.elapsed_time(e) for s, e in pairs) / steps
 
 
-def time_graph(step, steps, warmup, torch):
-    for _ in range(warmup):
-        step()
+def time_eager(step, steps, warmup, torch):
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_graph(step, steps, warmup, nbuf, torch):
+    """One graph holds one step on each logits copy; it is replayed until `steps` steps ran."""
+    for i in range(warmup):
+        step(i)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        step()
-    for _ in range(3):
+        for i in range(nbuf):
+            step(i)
+    for _ in range(2):
         g.replay()
     torch.cuda.synchronize()
+    replays = max(1, math.ceil(steps / nbuf))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
+    for _ in range(replays):
         g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, g
+    return start.elapsed_time(end) / (replays * nbuf), g
 
 
-def cpu_baseline(batch, min_seconds=10.0, max_seconds=30.0):
+def copies(t, torch):
+    """Identical copies of `t` at distinct addresses, together >= ROTATE_BYTES."""
+    n = max(2, math.ceil(ROTATE_BYTES / (t.numel() * t.element_size())))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+def cpu_verify_baseline(batch, min_seconds=10.0, max_seconds=30.0):
     """The CPU oracle (torch on the host) on a bounded sample of the same workload: passes over
     the requests, one request per call, until at least ``min_seconds`` of work (capped at
     ``max_seconds``)."""
@@ -101,19 +136,24 @@ def cpu_baseline(batch, min_seconds=10.0, max_seconds=30.0):
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     bs, T = batch["candidates"].shape
+    lens = batch.get("verify_lens")
+    lens = np.full(bs, T) if lens is None else lens.numpy()
+    offs = batch.get("row_offsets")
+    V = batch["logits"].shape[1]
     calls, rows, t0 = 0, 0, time.perf_counter()
     done = False
     while not done:
         for b in range(bs):
             O.verify_step(
                 batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
-                q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(),
-                verify_lens=np.full(bs, T), uniforms=batch["uniforms"].numpy(),
-                uniform_final=batch["uniform_final"].numpy(), prefix_lens=batch["prefix_lens"].numpy(),
-                hist_ids=batch["hist_ids"], presence=batch["presence"], repetition=batch["repetition"],
-                page_table=batch["page_table"], requests=[b])
+                q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(), verify_lens=lens,
+                uniforms=batch["uniforms"].numpy(), uniform_final=batch["uniform_final"].numpy(),
+                prefix_lens=batch["prefix_lens"].numpy(), hist_ids=batch.get("hist_ids"),
+                presence=batch.get("presence"), repetition=batch.get("repetition"),
+                page_table=batch.get("page_table"), row_offsets=None if offs is None else offs.numpy(),
+                requests=[b])
             calls += 1
-            rows += T
+            rows += int(lens[b])
             if time.perf_counter() - t0 > max_seconds:
                 done = True
                 break
@@ -122,7 +162,103 @@ def cpu_baseline(batch, min_seconds=10.0, max_seconds=30.0):
     dt = time.perf_counter() - t0
     return {"value": rows / dt, "unit": "rows/s", "cores": n, "kind": "port",
             "sample": f"{calls} request verifications ({calls / bs:.2f} passes over the {bs} requests, "
-                      f"{rows} rows x 151936) of the same workload, one request per oracle call, {dt:.1f} s"}
+                      f"{rows} rows x {V}) of the same workload, one request per oracle call, {dt:.1f} s"}
+
+
+def cpu_topk_baseline(x, k, min_seconds=10.0, max_seconds=30.0):
+    """The CPU oracle's top-k (stable descending sort) on bounded 64-row slices of the rows."""
+    import torch
+
+    import oracle.verify_oracle as O
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    rows, t0, i = 0, time.perf_counter(), 0
+    while time.perf_counter() - t0 < min_seconds:
+        sl = x[(i * 64) % x.shape[0]: (i * 64) % x.shape[0] + 64]
+        O.topk(sl.float(), k)
+        rows += sl.shape[0]
+        i += 1
+        if time.perf_counter() - t0 > max_seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": rows / dt, "unit": "rows/s", "cores": n, "kind": "port",
+            "sample": f"{rows} rows x {x.shape[1]} (64-row slices of the same rows), k={k}, {dt:.1f} s"}
+
+
+def setup_verify(config, args, torch, dev):
+    """(step(i), workload facts) of a fused verify workload."""
+    from dspine_amd import workloads as W
+    from dspine_amd.verify import History, Workspace, new_outputs, verify_step
+
+    if config == 4:
+        batch = W.serving_round()
+        name, workload = "serving", ("full verify step (penalties, temperature softmax, top-k/top-p filter, "
+                                     "chain rejection with sparse q, residual resample, compaction + KV slots)")
+    elif config == 3:
+        batch = W.rejection_round(sigma_draft=args.sigma)
+        name, workload = "rejection", (f"verify step, fp32 target, T=1, top-k 20, top-p 0.95, sparse q from "
+                                       f"draft logits + N(0, {args.sigma}^2)")
+    else:
+        batch = W.ragged_round()
+        name, workload = "ragged", ("ragged verify step, compact rows (verify lengths U{4..16}), T=1, top-p 0.9, "
+                                    "heavy-tailed logits")
+    d = W.to_device(batch, dev)
+    bs, T = batch["candidates"].shape
+    V = batch["logits"].shape[1]
+    K = batch["q_ids"].shape[2]
+    H = batch["hist_ids"].shape[1] if "hist_ids" in batch else 0
+    rows = batch["logits"].shape[0]
+    esize = batch["logits"].element_size()
+    outs, kv = new_outputs(bs, T, dev)
+    ws = Workspace()
+    hist = History(d["hist_ids"], d["presence"], d["repetition"]) if H else None
+    info = d["info"]
+    info.temperatures = info.temperatures.reshape(-1).contiguous()
+    bufs = copies(d["logits"], torch)
+
+    def step(i):
+        verify_step(logits=bufs[i % len(bufs)], sampling_info=info, candidates=d["candidates"],
+                    q_ids=d["q_ids"], q_values=d["q_values"], uniforms=d["uniforms"],
+                    uniform_final=d["uniform_final"], prefix_lens=d["prefix_lens"],
+                    verify_lens=d.get("verify_lens"), row_offsets=d.get("row_offsets"), history=hist,
+                    page_table=d.get("page_table"), outputs=outs, kv_slots=kv if "page_table" in d else None,
+                    workspace=ws)
+
+    total, chunk = verify_bytes(bs, T, V, K, H, esize, rows=rows)
+    C = math.ceil(V / (20480 if esize == 2 else 10240))
+    facts = dict(name=name, batch=batch, rows=rows, total=total, chunk=chunk, dtype="bf16" if esize == 2 else "f32",
+                 kernel=f"k_chunk (chunk pass: {rows} rows x {C} chunks of {20480 if esize == 2 else 10240} "
+                        f"{'bf16' if esize == 2 else 'fp32'})",
+                 config={"workload": workload, "requests": bs, "rows_per_request": T, "rows": rows, "vocab": V,
+                         "q_width": K, "history": H, "logits_dtype": "bf16" if esize == 2 else "fp32",
+                         "logits_copies": len(bufs)},
+                 accept=lambda: outs[0].float().mean().item())
+    return step, facts
+
+
+def setup_topk(args, torch, dev):
+    from dspine_amd import workloads as W
+    from dspine_amd.kernels.dspine import topk
+
+    x = W.topk_rows()["logits"]
+    rows, V = x.shape
+    k = args.k
+    vals = torch.empty((rows, k), dtype=torch.float32, device=dev)
+    ids = torch.empty((rows, k), dtype=torch.int64, device=dev)
+    bufs = copies(x.to(dev), torch)
+
+    def step(i):
+        topk(bufs[i % len(bufs)], k, vals, ids)
+
+    logits = rows * V * 2
+    facts = dict(name="topk", x=x, rows=rows, total=logits + rows * k * 12, chunk=logits, dtype="bf16",
+                 kernel=f"k_chunk (candidate pass: {rows} rows x {math.ceil(V / 20480)} chunks of 20480 bf16)",
+                 config={"workload": f"top-k only, k={k}, (value desc, id asc) order, planted peaks and ~1% "
+                                     f"duplicates", "rows": rows, "vocab": V, "k": k, "logits_dtype": "bf16",
+                         "logits_copies": len(bufs)},
+                 accept=None)
+    return step, facts
 
 
 def main():
@@ -130,6 +266,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5),
+                    help="workload: 4 = the serving verify step (default); 2 top-k, 3 rejection, 5 ragged")
+    ap.add_argument("--k", type=int, default=64, choices=(1, 20, 64), help="top-k of --config 2")
+    ap.add_argument("--sigma", type=float, default=0.5, choices=(0.5, 1.5), help="draft noise of --config 3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (the reference for HBM byte counters)")
@@ -152,59 +292,37 @@ def main():
         print(json.dumps({"calibrate_copy_bytes_read": n, "calibrate_copy_bytes_written": n, "launches": 5}))
         return
 
-    from dspine_amd import workloads as W
-    from dspine_amd.verify import History, Workspace, new_outputs, verify_step
+    from dspine_amd import _lib
 
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
-    batch = W.serving_round()
-    d = W.to_device(batch, dev)
-    print(f"[bench] workload ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    bs, T = batch["candidates"].shape
-    V = batch["logits"].shape[1]
-    K = batch["q_ids"].shape[2]
-    H = batch["hist_ids"].shape[1]
-    outs, kv = new_outputs(bs, T, dev)
-    ws = Workspace()
-    hist = History(d["hist_ids"], d["presence"], d["repetition"])
-    info = d["info"]
-    info.temperatures = info.temperatures.reshape(-1).contiguous()
+    if args.config == 2:
+        step, f = setup_topk(args, torch, dev)
+    else:
+        step, f = setup_verify(args.config, args, torch, dev)
+    nbuf = f["config"]["logits_copies"]
+    print(f"[bench] config {args.config} ready in {time.perf_counter() - t0:.1f} s ({nbuf} logits copies)",
+          file=sys.stderr, flush=True)
 
-    def step(stages=0):
-        verify_step(logits=d["logits"], sampling_info=info, candidates=d["candidates"],
-                    q_ids=d["q_ids"], q_values=d["q_values"], uniforms=d["uniforms"],
-                    uniform_final=d["uniform_final"], prefix_lens=d["prefix_lens"], history=hist,
-                    page_table=d["page_table"], outputs=outs, kv_slots=kv, workspace=ws,
-                    _stages=stages)
-
-    # eager timing: K steps bracketed by device synchronisation
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms = e0.elapsed_time(e1) / args.steps
-    # graph replay; the step's time is the faster of the two launch modes (the same work either way)
-    graph_ms, _g = time_graph(step, args.steps, args.warmup, torch)
+    eager_ms = time_eager(step, args.steps, args.warmup, torch)
+    graph_ms, _g = time_graph(step, args.steps, args.warmup, nbuf, torch)
     ms = min(graph_ms, eager_ms)
     mode = "graph" if graph_ms <= eager_ms else "eager"
-    # the dominant kernel: k_chunk inside full steps, HIP events on its launch stream
-    from dspine_amd import _lib
-
     kern_ms = time_kernel_events(step, args.steps, _lib.load(), torch)
-    total_bytes, chunk_bytes = algorithmic_bytes(bs, T, V, K, H)
-    acc = outs[0].float().mean().item()
-    print(f"[bench] graph {graph_ms * 1e3:.1f} us/step, eager {eager_ms * 1e3:.1f} us/step, k_chunk "
-          f"{kern_ms * 1e3:.1f} us, mean accept {acc:.2f}, step {total_bytes / (ms * 1e-3) / 1e9:.0f} GB/s",
-          file=sys.stderr, flush=True)
+    total_bytes, chunk_bytes = f["total"], f["chunk"]
     achieved = chunk_bytes / (kern_ms * 1e-3) / 1e9
+    step_gbps = total_bytes / (ms * 1e-3) / 1e9
+    acc = f["accept"]() if f["accept"] else None
+    print(f"[bench] graph {graph_ms * 1e3:.1f} us/step, eager {eager_ms * 1e3:.1f} us/step, k_chunk "
+          f"{kern_ms * 1e3:.1f} us ({achieved / PEAK_GBPS:.3f} of peak), step {step_gbps:.0f} GB/s "
+          f"({step_gbps / PEAK_GBPS:.3f} of peak)" + (f", mean accept {acc:.2f}" if acc is not None else ""),
+          file=sys.stderr, flush=True)
+    cfg = dict(f["config"])
+    cfg.update({"timed_launch": mode, "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms,
+                "step_GBps_algorithmic": step_gbps, "step_algorithmic_bytes": total_bytes})
     line = {
         "metric": METRIC,
-        "value": bs * T / (ms * 1e-3),
+        "value": f["rows"] / (ms * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -213,25 +331,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": f["dtype"],
         "data": "synthetic",
-        "config": {
-            "workload": "full verify step (penalties, temperature softmax, top-k/top-p filter, chain "
-                        "rejection with sparse q, residual resample, compaction + KV slots)",
-            "requests": bs, "rows_per_request": T, "vocab": V, "q_width": K, "history": H,
-            "logits_dtype": "bf16", "timed_launch": mode, "eager_ms_per_step": eager_ms,
-            "graph_ms_per_step": graph_ms,
-            "step_GBps_algorithmic": total_bytes / (ms * 1e-3) / 1e9,
-        },
+        "config": cfg,
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": PEAK_GBPS, "unit": "GB/s",
-            "frac": achieved / PEAK_GBPS, "traffic": committed_traffic(),
-            "kernel": "k_chunk (chunk pass: 1088 rows x 8 chunks of 20480 bf16)",
-            "kernel_us": kern_ms * 1e3, "algorithmic_bytes": chunk_bytes,
+            "frac": achieved / PEAK_GBPS, "traffic": committed_traffic(f["name"]),
+            "kernel": f["kernel"], "kernel_us": kern_ms * 1e3, "algorithmic_bytes": chunk_bytes,
+            "step_frac": step_gbps / PEAK_GBPS,
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(batch)
+        if args.config == 2:
+            line["cpu_baseline"] = cpu_topk_baseline(f["x"], args.k)
+        else:
+            line["cpu_baseline"] = cpu_verify_baseline(f["batch"])
     print(json.dumps(line), flush=True)
 
 

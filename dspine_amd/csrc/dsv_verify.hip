@@ -1056,7 +1056,13 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   uint64_t fc;
   double fS;
   find_cut(topk, min_p, top_p_eff, fc, fS);
-  if (fc == ~0ull && (kcov > sh.kb_row || x_untracked)) {
+  // No value at or above kscan is removed.  When their mass (all of it counted: each chunk
+  // counted every key >= kcov) already exceeds the top-p bound by more than the probabilities'
+  // rounding, every value below kscan has at least that mass ahead and is removed as well: the
+  // cut sits just below kscan, whatever values lie there (peaked rows, whose nucleus is a few
+  // tokens far above the other chunks' windows).
+  const bool cut_below = fc == ~0ull && m_total > (double)top_p_eff + 1e-5;
+  if (fc == ~0ull && !cut_below && (kcov > sh.kb_row || x_untracked)) {
     // the cut lies below a chunk's window (or below every window, where a chunk did not
     // track its largest value): the full histogram decides it
     if (tid == 0) {
@@ -1071,6 +1077,10 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
     rs.vcut = (uint32_t)fc;
     rs.ktie = (int32_t)(fc >> 32);
     rs.S_kept = fS;
+  } else if (cut_below) {
+    rs.vcut = kscan - 1u;  // (kscan >= 0x80, the lowest finite key)
+    rs.ktie = 0;
+    rs.S_kept = m_total;
   } else {
     // every value at or above kscan is kept: the cut is the first value below kscan (tie 0)
     uint64_t below = 0;
@@ -3031,27 +3041,28 @@ extern "C" int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t
   return DSV_OK;
 }
 
-extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t row_stride,
-                                 int32_t bs, int32_t T, const int64_t* candidates, const int32_t* verify_lens,
-                                 int32_t cap, const int32_t* prefix_lens, int32_t* accept, int32_t* commit,
-                                 int64_t* bonus, int64_t* output, int32_t* new_seq, int64_t* top1_out,
-                                 void* workspace, int64_t workspace_bytes, dsv_stream_t stream_) {
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (dtype != DSV_BF16 && dtype != DSV_F32)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: logits must be float32 or bfloat16");
+// Argument checks shared by the greedy-verify entry points (what: the entry point's name).
+static int greedy_check(const char* what, const void* logits, int32_t dtype, int64_t rows, int64_t vocab,
+                        int64_t row_stride, int32_t bs, int32_t T, const int64_t* candidates,
+                        const int32_t* verify_lens, int32_t cap, const int32_t* prefix_lens, int32_t* accept,
+                        int32_t* commit, int64_t* bonus, int64_t* output, int32_t* new_seq) {
+  if (dtype != DSV_BF16 && dtype != DSV_F32) DSV_FAIL(DSV_ERR_INVALID, "%s: logits must be float32 or bfloat16", what);
   if (bs <= 0 || T < 1 || vocab < 1 || row_stride < vocab || rows != (int64_t)bs * T)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: logits must be [bs*T, V] (rows %lld, bs %d, T %d)",
-             (long long)rows, bs, T);
-  if (vocab >= (1ll << 31) || rows >= (1ll << 31))
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: vocab and rows must be < 2^31");
-  if (!verify_lens && (cap < 1 || cap > T))
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: cap %d outside [1, %d]", cap, T);
-  if (!logits || !candidates || !prefix_lens || !accept || !commit || !bonus || !output || !new_seq || !workspace)
-    DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: required pointer is null");
-  const WsLayout w = ws_layout(rows, 1, vocab, dtype, 0, false);
-  if (workspace_bytes < w.total)
-    DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_greedy_verify: workspace %lld < %lld", (long long)workspace_bytes,
-             (long long)w.total);
+    DSV_FAIL(DSV_ERR_INVALID, "%s: logits must be [bs*T, V] (rows %lld, bs %d, T %d)", what, (long long)rows, bs, T);
+  if (vocab >= (1ll << 31) || rows >= (1ll << 31)) DSV_FAIL(DSV_ERR_INVALID, "%s: vocab and rows must be < 2^31", what);
+  if (!verify_lens && (cap < 1 || cap > T)) DSV_FAIL(DSV_ERR_INVALID, "%s: cap %d outside [1, %d]", what, cap, T);
+  if (!logits || !candidates || !prefix_lens || !accept || !commit || !bonus || !output || !new_seq)
+    DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
+  return DSV_OK;
+}
+
+// The greedy verify's two launches: the chunk pass (per-chunk max / first argmax into
+// cstat[rows * C], every entry written) and the per-request acceptance reading them.
+static int greedy_launch(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t row_stride,
+                         int32_t bs, int32_t T, const int64_t* candidates, const int32_t* verify_lens, int32_t cap,
+                         const int32_t* prefix_lens, int32_t* accept, int32_t* commit, int64_t* bonus,
+                         int64_t* output, int32_t* new_seq, int64_t* top1_out, ChunkStat* cstat,
+                         hipStream_t stream) {
   const size_t esize = dtype == DSV_BF16 ? 2 : 4;
   KParams P;
   memset(&P, 0, sizeof(P));
@@ -3063,8 +3074,7 @@ extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows
   P.a.bs = bs;
   P.a.T = T;
   P.a.candidates = candidates;
-  char* ws = reinterpret_cast<char*>(workspace);
-  P.cstat = reinterpret_cast<ChunkStat*>(ws + w.cstat);
+  P.cstat = cstat;
   P.C = chunks_per_row(vocab, dtype);
   P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0) &&
               vocab * (int64_t)esize >= 16;
@@ -3075,6 +3085,25 @@ extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows
                      verify_lens, cap, prefix_lens, bs, T, accept, commit, bonus, output, new_seq, top1_out);
   DSV_CHECK_LAUNCH("k_greedy_accept");
   return DSV_OK;
+}
+
+extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t row_stride,
+                                 int32_t bs, int32_t T, const int64_t* candidates, const int32_t* verify_lens,
+                                 int32_t cap, const int32_t* prefix_lens, int32_t* accept, int32_t* commit,
+                                 int64_t* bonus, int64_t* output, int32_t* new_seq, int64_t* top1_out,
+                                 void* workspace, int64_t workspace_bytes, dsv_stream_t stream_) {
+  const int rc = greedy_check("dsv_greedy_verify", logits, dtype, rows, vocab, row_stride, bs, T, candidates,
+                              verify_lens, cap, prefix_lens, accept, commit, bonus, output, new_seq);
+  if (rc != DSV_OK) return rc;
+  if (!workspace) DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify: required pointer is null");
+  const WsLayout w = ws_layout(rows, 1, vocab, dtype, 0, false);
+  if (workspace_bytes < w.total)
+    DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_greedy_verify: workspace %lld < %lld", (long long)workspace_bytes,
+             (long long)w.total);
+  ChunkStat* cstat = reinterpret_cast<ChunkStat*>(reinterpret_cast<char*>(workspace) + w.cstat);
+  return greedy_launch(logits, dtype, rows, vocab, row_stride, bs, T, candidates, verify_lens, cap, prefix_lens,
+                       accept, commit, bonus, output, new_seq, top1_out, cstat,
+                       reinterpret_cast<hipStream_t>(stream_));
 }
 
 extern "C" int64_t dsv_topk_workspace_bytes(int64_t rows, int64_t vocab, int32_t k) {
@@ -3112,7 +3141,11 @@ extern "C" int dsv_topk(const void* logits, int32_t dtype, int64_t rows, int64_t
   P.kcand = k;
   P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0) &&
               vocab * (int64_t)esize >= 16;
+  if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_topk: cannot record the profiling start event");
   launch_chunk(P, dtype, (unsigned)(rows * C), stream);
+  if (g_prof_start && g_prof_stop && hipEventRecord(g_prof_stop, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_topk: cannot record the profiling stop event");
   if (dtype == DSV_BF16) {
     (void)hipFuncSetAttribute((const void*)k_topk_merge<DSV_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)merge_lds);

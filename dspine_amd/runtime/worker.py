@@ -182,6 +182,7 @@ class VerifyWorker:
         self.sampling_backend = sampling_backend
         self._dspine_sampler = DraftRound(k, random)
         self.target_distribution = TargetDistribution(self) if use_target_distribution else None
+        self.verify_caps = None  # the verification controller (caps.active_controller reads it)
         self._buffers = [None, None]
         self._flip = 0
         self._lock = threading.Lock()

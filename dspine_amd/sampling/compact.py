@@ -119,15 +119,24 @@ def adjust_history(logits, hist_ids, presence=None, repetition=None, row_to_requ
             "dsv_adjust_history")
 
 
-def around_verify_logits_adjustments(original, *, next_token_logits, sampling_info, draft_token_num,
-                                     controller=None):
-    """The AROUND hook on SGLang's verify-logit adjustments (sampling/compact.py:82-116): compact
-    rounds adjust the packed rows of ``controller`` with its row_to_request; full blocks are
-    viewed as [bs, draft_token_num, V].  Without a controller the original runs."""
-    if controller is None:
+def around_verify_logits_adjustments(original, *, next_token_logits, sampling_info, draft_token_num):
+    """The AROUND hook on SGLang's verify-logit adjustments (sampling/compact.py:82-116).
+
+    Resolves the active worker's verification controller (``caps.active_controller``).  With
+    no DSpine worker at all the original SGLang adjustment runs.  A compact round adjusts the
+    packed rows of the controller with its ``row_to_request`` (the logits must be the round's
+    own packed tensor).  Otherwise full blocks [bs * draft_token_num, V] are adjusted as
+    [bs, draft_token_num, V]: first SGLang's custom logit processors when the batch has them
+    (``sglang.srt.layers.sampler.apply_custom_logit_processor``, imported only then, as the
+    reference does), then ``adjust_logits``."""
+    from dspine_amd.runtime import worker
+    from dspine_amd.verification.caps import active_controller
+
+    controller = active_controller()
+    if controller is None and worker._active_worker is None:
         return original(next_token_logits=next_token_logits, sampling_info=sampling_info,
                         draft_token_num=draft_token_num)
-    if getattr(controller, "compact_round", False):
+    if controller is not None and getattr(controller, "compact_round", False):
         if next_token_logits is not controller.compact_logits:
             raise RuntimeError("Packed verification logits do not belong to this round")
         return adjust_logits(next_token_logits, sampling_info, controller.row_to_request)
@@ -138,4 +147,8 @@ def around_verify_logits_adjustments(original, *, next_token_logits, sampling_in
     bs = len(sampling_info)
     if next_token_logits.shape[0] != bs * draft_token_num:
         raise ValueError("Verification logits do not match the request/block layout")
+    if getattr(sampling_info, "has_custom_logit_processor", False):
+        from sglang.srt.layers.sampler import apply_custom_logit_processor
+
+        apply_custom_logit_processor(next_token_logits, sampling_info, num_tokens_in_batch=draft_token_num)
     return adjust_logits(next_token_logits.view(bs, draft_token_num, -1), sampling_info, None)

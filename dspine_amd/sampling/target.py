@@ -40,8 +40,9 @@ class TargetDistribution:
                       row_offsets=None, row_to_request=None):
         """Verify one (possibly shortened) target call against this round's sampled q
         (sampling/target.py:34-122).  Rows are ``b*T + s`` or compact ``row_offsets[b] + s``.
-        Returns the worker's next output buffers, or None when compact rows come without
-        ``row_offsets`` (the caller then builds P densely)."""
+        Returns the worker's next output buffers.  Compact rows need their ``row_offsets``:
+        ``row_to_request`` without them raises ValueError (the reference would read the compact
+        rows as ``b*T + s`` there; its callers always pass both, verification/ragged.py:329-331)."""
         sampler = self.worker._dspine_sampler
         if not sampler.round_sampled or sampler.round_bs != bs:
             raise RuntimeError("Sparse rejection must consume this round's actual proposal q")
@@ -49,7 +50,7 @@ class TargetDistribution:
         if candidates.shape != (bs, width):
             raise ValueError("Proposal storage does not match this decode batch")
         if row_to_request is not None and row_offsets is None:
-            return None
+            raise ValueError("Compact verification rows (row_to_request) need their row_offsets")
         outputs = self.worker._next_accept_bonus_buffers(bs)
         uniforms, final = verification_uniforms(bs, width, candidates.device, sampler.random)
         q_ids = sampler.candidate_out[:bs]

@@ -57,3 +57,47 @@ def accept_greedy(*, candidates: torch.Tensor, next_token_logits: torch.Tensor,
         accept.data_ptr(), commit.data_ptr(), bonus.data_ptr(), output.data_ptr(), new_seq.data_ptr(),
         _lib.ptr(top1), ws.data_ptr(), ws.numel(), _lib.stream_of(dev)), "dsv_greedy_verify")
     return outputs
+
+
+def active_controller():
+    """The active worker's verification controller, or None (verification/caps.py:381-385)."""
+    from dspine_amd.runtime import worker as module
+
+    current = module._active_worker
+    return getattr(current, "verify_caps", None) if current is not None else None
+
+
+def _prefix_i32(prefix_lens):
+    return prefix_lens if prefix_lens.dtype == torch.int32 else prefix_lens.to(torch.int32)
+
+
+def accept(self, *, candidates, next_token_logits, sampling_info, draft_input, prefix_lens, bs):
+    """``VerifyCaps.accept`` (verification/caps.py:331-379), written as a plain function of the
+    controller so that it binds as the method (``VerifyCaps.accept = caps.accept``).
+
+    Reads the controller state the reference reads: ``executed_width`` and ``active`` (the
+    confirmed shortened target forward), ``sampled_round``, ``full``, ``worker`` (its
+    ``_next_accept_bonus_buffers``) and ``_sampled_cap_lens``.  Sampled rounds verify against
+    this round's q (``accept_sampled_prefix`` with every request's length = ``active``);
+    greedy rounds run the fused argmax + capped acceptance (``dsv_greedy_verify``) into the
+    worker's next output buffers.  Returns (accept i32, commit i32, bonus i64, output i64
+    [bs, full], new_seq i32)."""
+    if self.executed_width != self.active:
+        raise RuntimeError("Capped acceptance requires a confirmed shortened target forward")
+    if self.sampled_round:
+        from dspine_amd.sampling.rejection import accept_sampled_prefix
+
+        cache = getattr(self, "_sampled_cap_lens", None)
+        if cache is None:
+            cache = self._sampled_cap_lens = {}
+        key = (bs, self.active)
+        if key not in cache:
+            cache[key] = torch.full((bs,), self.active, device=candidates.device, dtype=torch.int32)
+        return accept_sampled_prefix(self, candidates=candidates, next_token_logits=next_token_logits,
+                                     sampling_info=sampling_info, prefix_lens=prefix_lens, bs=bs,
+                                     verify_lens=cache[key])
+    if candidates.shape != (bs, self.full):
+        raise ValueError(f"Capped acceptance requires full{self.full} proposal storage")
+    outputs = self.worker._next_accept_bonus_buffers(bs)
+    return accept_greedy(candidates=candidates, next_token_logits=next_token_logits,
+                         prefix_lens=_prefix_i32(prefix_lens), cap=self.active, outputs=outputs)

@@ -32,6 +32,8 @@
  *                         build_sparse_target)
  *   dsv_sample_chain      kernels/dspine.py:616-772 (serial_sample_chain)
  *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices)
+ *   dsv_sps_plan          verification/sps.py:35-58 (allocate_verify_lens) and :61-99
+ *                         (device_plan: lengths, layout row pointer, _indices)
  */
 #ifndef DSPINE_VERIFY_H
 #define DSPINE_VERIFY_H
@@ -122,8 +124,9 @@ int64_t dsv_verify_workspace_bytes(int64_t rows, int32_t bs, int32_t T, int64_t 
 int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream);
 
 /* Profiling aid with no counterpart in the reference: the calling thread's later dsv_verify   */
-/* calls record `start` / `stop` (hipEvent_t, timing enabled) on their stream right before and */
-/* after the chunk-pass kernel, so a benchmark can time that kernel alone.  NULL, NULL: off.   */
+/* and dsv_topk calls record `start` / `stop` (hipEvent_t, timing enabled) on their stream     */
+/* right before and after the chunk-pass kernel, so a benchmark can time that kernel alone.    */
+/* NULL, NULL: off.                                                                            */
 int dsv_profile_events(void* start, void* stop);
 
 /* Greedy verify (argmax acceptance): top1 = first argmax of each row, a = first mismatch   */
@@ -243,6 +246,23 @@ int dsv_sample_chain(const float* table, int64_t n, int32_t K, int32_t block_siz
                      const int32_t* top_k, const float* top_p, const float* min_p, const int32_t* greedy,
                      const float* u, const int64_t* cand, const int64_t* greedy_tok, int64_t* out_tok,
                      float* out_q, float* confidence, dsv_stream_t stream);
+
+/* SPS verify-length plan (verification/sps.py:35-99: allocate_verify_lens, the calibration   */
+/* table lookup it does, the ragged layout's row pointer and _indices), one launch.           */
+/* raw [bs, gamma] float32 confidences (row stride raw_stride), probabilities [prob_rows,     */
+/* n_bins] float32 (row stride prob_stride), depth [gamma] int64 (rows of the table), optional */
+/* boundaries [n_boundaries <= n_bins - 1] float64 ascending (torch.bucketize; NULL: bin =    */
+/* trunc(raw * n_bins) clamped).  Survival = running minimum of the running product (float64, */
+/* each prefix rounded to float32) of table[depth[d], bin]; the budget - bs positions of      */
+/* highest survival (position-major order d * bs + b on ties) are verified beyond each        */
+/* request's root: verify_lens [bs] int32 (1 + selected positions), qo_indptr [bs + 1] int32  */
+/* (exclusive prefix, may be NULL), window_index [budget] int64 (b * (gamma + 1) + d, may be  */
+/* NULL).  bs <= budget <= bs * (gamma + 1).  raw == NULL: verify_lens is an input and only   */
+/* the layout (qo_indptr, window_index) is written.  bs * gamma + bs <= 38912.               */
+int dsv_sps_plan(const float* raw, int64_t raw_stride, int32_t bs, int32_t gamma, const float* probabilities,
+                 int64_t prob_stride, int32_t n_bins, int64_t prob_rows, const int64_t* depth,
+                 const double* boundaries, int32_t n_boundaries, int32_t budget, int32_t* verify_lens,
+                 int32_t* qo_indptr, int64_t* window_index, dsv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,9 @@ PINNED = {
     "topk": "tests/test_topk_compat.py:70-84 known answer, tests/test_tp_head.py:49-53",
     "compress": "invariants of tests/test_p_distribution_reference.py:156-175",
     "window_index": "closed form tests/test_sps.py:446-448",
+    "allocate_verify_lens": "the reference's brute-force order (-survival, depth, request) of "
+    "tests/test_sps.py:360-384 and its fp32 extreme rows :387-417; bucketize boundaries of :420-448",
+    "sps_layout": "closed form (exclusive prefix; tests/test_sps.py:446-448)",
     "logits_padding": "tests/test_release.py:45-67",
     "sample_chain": "ties-to-lower-lane known answer tests/test_cuda.py:213-232, brute force; "
     "confidence known answers tests/test_sampled_confidence.py:124-196",
@@ -560,6 +563,40 @@ def window_index(lens, T: int) -> np.ndarray:
     """verification/sps.py:27-32 and :94-98: [b*T + d for each b, for d < lens[b]]."""
     return np.array([b * T + d for b, n in enumerate(np.asarray(lens).tolist()) for d in range(n)],
                     dtype=np.int64)
+
+
+def allocate_verify_lens(raw, probabilities, depth, budget, boundaries=None) -> torch.Tensor:
+    """verification/sps.py:35-58 on CPU torch: bins by ``bucketize`` against the float64
+    boundaries (else ``(raw * bins).to(int64).clamp(0, bins-1)``), conditional =
+    ``probabilities[depth, bins]``, survival = ``cumprod`` (CPU: float64 accumulation, each
+    prefix rounded to float32) then ``cummin``; the first ``budget - bs`` positions of a stable
+    descending argsort of the position-major survival; lengths = 1 + positions per request."""
+    raw = torch.as_tensor(raw, dtype=torch.float32)
+    bs, gamma = raw.shape
+    if not bs <= budget <= bs * (gamma + 1):
+        raise ValueError("SPS budget must include every root and fit the draft block")
+    probabilities = torch.as_tensor(probabilities, dtype=torch.float32)
+    n_bins = probabilities.shape[-1]
+    if boundaries is not None:
+        bins = torch.bucketize(raw.contiguous(), torch.as_tensor(boundaries, dtype=torch.float64))
+    else:
+        bins = (raw * n_bins).to(torch.int64).clamp_(0, n_bins - 1)
+    conditional = probabilities[torch.as_tensor(depth, dtype=torch.int64), bins]
+    survival = conditional.cumprod(dim=-1).cummin(dim=-1).values
+    survival = survival.transpose(0, 1).contiguous().view(-1)
+    selected = torch.argsort(survival, descending=True, stable=True)[: budget - bs]
+    lens = torch.ones((bs,), dtype=torch.int32)
+    lens.scatter_add_(0, selected.remainder(bs), torch.ones_like(selected, dtype=torch.int32))
+    return lens
+
+
+def sps_layout(lens, T: int):
+    """The ragged layout of verify lengths: (qo_indptr int32 [bs + 1] = exclusive prefix,
+    window index int64 = [b*T + d for d < lens[b]]) (verification/sps.py:86-98)."""
+    lens = np.asarray(lens, dtype=np.int64).reshape(-1)
+    qo = np.zeros(lens.size + 1, dtype=np.int32)
+    qo[1:] = np.cumsum(lens)
+    return qo, window_index(lens, T)
 
 
 def kv_slots(page_table, prefix_lens, accept, T: int) -> np.ndarray:

@@ -12,6 +12,23 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP library)")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """The near-margin table of every parity comparison of the run (tests/parity.py)."""
+    import parity
+
+    if not parity.RECORDS:
+        return
+    tr = terminalreporter
+    tr.section(f"parity vs oracle (near-margin: oracle margin < {parity.MARGIN:g})")
+    total = [0, 0, 0]
+    for tag, compared, near, differing in parity.RECORDS:
+        tr.write_line(f"{tag}: compared {compared}, near-margin {near}, differing {len(differing)} {differing}")
+        total[0] += compared
+        total[1] += near
+        total[2] += len(differing)
+    tr.write_line(f"TOTAL: compared {total[0]}, near-margin {total[1]}, differing {total[2]}")
+
+
 @pytest.fixture(scope="session")
 def device():
     import torch

@@ -11,9 +11,11 @@ import numpy as np
 import pytest
 import torch
 
+import parity
+from parity import MARGIN
+
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 CASES = sorted(os.path.basename(f)[:-4] for f in glob.glob(os.path.join(HERE, "*.npz")))
-MARGIN = 1e-4
 
 
 def load(name):
@@ -79,11 +81,16 @@ def test_oracle_reproduces_golden(name):
 
 def _compare(name, z, got, names):
     margins = z.get("expect_margins")
-    for b in range(z["expect_" + names[0]].shape[0]):
-        same = all(np.array_equal(got[n][b], z["expect_" + n][b]) for n in names)
+    n = z["expect_" + names[0]].shape[0]
+    differing = []
+    for b in range(n):
+        same = all(np.array_equal(got[k][b], z["expect_" + k][b]) for k in names)
         if not same:
-            assert margins is not None and margins[b] < MARGIN, (name, b, {n: got[n][b] for n in names},
-                                                                 {n: z["expect_" + n][b] for n in names})
+            assert margins is not None and margins[b] < MARGIN, (name, b, {k: got[k][b] for k in names},
+                                                                 {k: z["expect_" + k][b] for k in names})
+            differing.append(b)
+    near = 0 if margins is None else int((margins < MARGIN).sum())
+    parity.record(f"golden {name}", n, near, differing)
 
 
 @pytest.mark.gpu

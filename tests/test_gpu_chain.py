@@ -11,11 +11,11 @@ import numpy as np
 import pytest
 import torch
 
+import parity
 from dspine_amd import workloads as W
+from parity import MARGIN
 
 pytestmark = pytest.mark.gpu
-
-MARGIN = 1e-4
 
 
 def _O():
@@ -42,6 +42,7 @@ def _check_chain(outs, ref, tag, max_near=0):
             assert ref[5][b] < MARGIN, (tag, b, {n: g[b] for n, g in zip(names, got)},
                                         {n: r[b] for n, r in zip(names, ref)}, ref[5][b])
             near.append(b)
+    parity.record(tag, got[0].shape[0], int((np.asarray(ref[5]) < MARGIN).sum()), near)
     assert len(near) <= max_near, (tag, near)
 
 
@@ -662,12 +663,16 @@ def test_worker_seam_fused_equals_explicit(device):
     u_fin = O.seeded_uniforms(seeds.numpy(), positions.numpy(), 1, O.BONUS).reshape(-1)
     ref = O.verify_step(logits, info, candidates=cand.numpy(), q_ids=q_ids.numpy(), q_values=q.numpy(),
                         verify_lens=np.full(bs, T), uniforms=u_acc, uniform_final=u_fin,
-                        prefix_lens=np.zeros(bs, np.int32))
+                        prefix_lens=np.zeros(bs, np.int32), exact_softmax=True)
+    differing = set()
     for name, a, b in (("accept", acc, acc2), ("bonus", bonus, bonus2)):
         a, b = a.cpu().numpy(), b.cpu().numpy()
         for i in range(bs):
             if a[i] != ref[name][i] or b[i] != ref[name][i]:
                 assert ref["margins"][i] < MARGIN, (name, i, a[i], b[i], ref[name][i])
+                differing.add(i)
+    parity.record("worker seam (fused, explicit P)", bs, int((ref["margins"] < MARGIN).sum()), sorted(differing))
+    assert len(differing) <= 1, differing
     Wk.set_active_worker(None)
 
 

@@ -1,19 +1,22 @@
 """Parity of the HIP path (through the C ABI) with the CPU oracle on identical inputs.
 
 Integer outputs must match bit-exactly.  A request may differ only when the oracle itself
-reports a decision margin below MARGIN (an accept test u*q vs p or a bonus CDF boundary within
-rounding of the reference's own float32 softmax); such requests are counted and must be rare.
+reports a decision margin below MARGIN (tests/parity.py: an accept test u*q vs p or a bonus CDF
+boundary within the measured probability error); every comparison records how many requests
+were near such a margin and how many differed, and the run prints the table at its end.
+The benchmark workloads (top-k rows, rejection, serving and ragged rounds) are compared in
+full: every row or request.
 """
 
 import numpy as np
 import pytest
 import torch
 
+import parity
 from dspine_amd import workloads as W
+from parity import MARGIN
 
 pytestmark = pytest.mark.gpu
-
-MARGIN = 1e-4  # relative: well above the ~1e-5 error of CPU torch's float32 softmax
 
 
 def _oracle():
@@ -25,20 +28,7 @@ def _oracle():
 def compare_outputs(gpu, ref, requests, tag):
     """gpu/ref: dicts of numpy arrays (accept, bonus, output, new_seq, [kv_slots]); returns the
     list of near-margin requests that differ (asserts every other request is identical)."""
-    near = []
-    for b in requests:
-        same = (int(gpu["accept"][b]) == int(ref["accept"][b])
-                and int(gpu["bonus"][b]) == int(ref["bonus"][b])
-                and np.array_equal(gpu["output"][b], ref["output"][b])
-                and int(gpu["new_seq"][b]) == int(ref["new_seq"][b]))
-        if same and ref.get("kv_slots") is not None and gpu.get("kv_slots") is not None:
-            same = np.array_equal(gpu["kv_slots"][b], ref["kv_slots"][b])
-        if not same:
-            m = float(ref["margins"][b])
-            assert m < MARGIN, (tag, b, {k: gpu[k][b] for k in ("accept", "bonus")},
-                                {k: ref[k][b] for k in ("accept", "bonus")}, m)
-            near.append(b)
-    return near
+    return parity.compare_requests(gpu, ref, requests, tag)
 
 
 def _padded(x, device, width):
@@ -71,7 +61,7 @@ def run_gpu_verify(batch, device, backend="pytorch", row_stride=None):
     return res
 
 
-def run_oracle(batch, requests, backend="pytorch", exact_softmax=False):
+def run_oracle(batch, requests, backend="pytorch", exact_softmax=True):
     O = _oracle()
     bs, T = batch["candidates"].shape
     lens = batch.get("verify_lens")
@@ -377,6 +367,26 @@ def test_verify_nucleus_paths(device, case, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_verify_full_histogram_rows_accepted(device, dtype):
+    """Flat nucleus rows (temperature 40: the bf16 rows need the full histogram, the float32
+    rows the radix descent) whose drafts are accepted: every q lane is 1e-7, below the ~7e-6
+    of a kept token, so the chain runs through several such rows and the bonus of a later one
+    is drawn after the accepted ones (the resumed scan of the request's rows)."""
+    V = 151936
+    bs, T = 4, 5
+    batch = _small_batch(23, bs=bs, T=T, V=V, K=4, dtype=dtype, mixed=False, penalties=True)
+    g = torch.Generator().manual_seed(24)
+    batch["logits"] = (torch.randn(bs * T, V, generator=g) * 2.0).to(dtype)
+    batch["info"] = W.sampling_info([40.0] * bs, [0] * bs, [0.9, 0.5, 0.95, 0.8])
+    batch["q_values"] = torch.full_like(batch["q_values"], 1e-7)
+    batch["verify_lens"] = torch.tensor([5, 3, 4, 5], dtype=torch.int32)
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)), exact_softmax=True)
+    assert (ref["accept"] >= 2).any(), ref["accept"]
+    assert len(compare_outputs(gpu, ref, range(bs), f"full-histogram rows accepted {dtype}")) <= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("case", ["windows", "flat"])
 def test_verify_flashinfer_min_p_nucleus(device, case, dtype):
     # flashinfer's min-p branch (tests/ref_utils.py:79-108): renormalise over the top-k, top-p
@@ -421,29 +431,89 @@ def test_verify_unfiltered(device):
     assert len(compare_outputs(gpu, ref, range(bs), "unfiltered")) <= 1
 
 
-SERVING_SUBSET = [0, 1, 2, 3, 5, 8, 13, 21, 34, 55, 63]
-
-
-def test_verify_serving_round_subset(device):
+def test_verify_serving_round_full(device):
+    """The benchmark's serving workload (64 x 17 x 151936 bf16, penalties, mixed modes, KV
+    slots): every request against the oracle."""
     batch = W.serving_round()
+    bs = batch["candidates"].shape[0]
     gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, SERVING_SUBSET)
-    near = compare_outputs(gpu, ref, SERVING_SUBSET, "serving")
-    assert len(near) <= 1
+    ref = run_oracle(batch, list(range(bs)))
+    compare_outputs(gpu, ref, range(bs), "serving 64x17x151936 bf16")
 
 
 @pytest.mark.parametrize("sigma", [0.5, 1.5])
-def test_verify_rejection_round_subset(device, sigma):
+def test_verify_rejection_round_full(device, sigma):
+    """The rejection workload (32 x 17 x 151936 fp32, top-k 20, top-p 0.95): every request."""
     batch = W.rejection_round(sigma_draft=sigma)
-    subset = [0, 3, 7, 12, 19, 31]
+    bs = batch["candidates"].shape[0]
     gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, subset)
-    assert len(compare_outputs(gpu, ref, subset, f"rejection sigma={sigma}")) <= 1
+    ref = run_oracle(batch, list(range(bs)))
+    compare_outputs(gpu, ref, range(bs), f"rejection 32x17x151936 fp32 sigma={sigma}")
 
 
-def test_verify_ragged_round_subset(device):
+def test_verify_ragged_round_full(device):
+    """The ragged workload (32 requests x U{4..16} rows x 262144 bf16, Student-t): every request."""
     batch = W.ragged_round()
-    subset = [0, 1, 9, 17, 31]
+    bs = batch["candidates"].shape[0]
     gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, subset)
-    assert len(compare_outputs(gpu, ref, subset, "ragged")) <= 1
+    ref = run_oracle(batch, list(range(bs)))
+    compare_outputs(gpu, ref, range(bs), "ragged 32x(4..16)x262144 bf16")
+
+
+def test_topk_rows_full(device):
+    """The top-k workload ([1088, 151936] bf16, planted peaks, ~1% duplicates): all rows for
+    k in {1, 20, 64}, ids and values bit-exact in (value desc, id asc) order."""
+    from dspine_amd.kernels.dspine import topk, topk_ids
+
+    O = _oracle()
+    x = W.topk_rows()["logits"]
+    rv, ri = O.topk(x.float(), 64)  # the first k of one stable order are the top-k for every k
+    xd = x.to(device)
+    for k in (1, 20, 64):
+        vals, ids = topk(xd, k)
+        srt = topk_ids(xd, k)
+        torch.cuda.synchronize()
+        bad = (ids.cpu() != ri[:, :k]).any(-1) | (vals.cpu() != rv[:, :k]).any(-1)
+        assert int(bad.sum()) == 0, (k, torch.nonzero(bad).view(-1)[:10].tolist())
+        assert torch.equal(srt.cpu(), ri[:, :k].sort(-1).values)
+        parity.record(f"topk [1088, 151936] bf16 k={k} (rows)", x.shape[0], 0, [])
+
+
+def test_target_p_error_bounds_margin(device):
+    """The dense target P of the HIP path against the float64 softmax (rounded once) and
+    against CPU torch's float32 softmax on the serving workload's rows (all four modes): the
+    largest relative error against the exact softmax on entries >= 1e-6 of the row max stays
+    below a quarter of MARGIN, so a decision further than MARGIN from its boundary (as the
+    oracle's exact softmax places it) cannot come out differently."""
+    from dspine_amd.runtime.worker import build_dspine_target_probs
+
+    O = _oracle()
+    batch = W.serving_round()
+    T = batch["candidates"].shape[1]
+    reqs = 16
+    x = batch["logits"][: reqs * T]
+    info = batch["info"]
+    sub = W.sampling_info(info.temperatures.view(-1)[:reqs].clone(), info.top_ks[:reqs].clone(),
+                          info.top_ps[:reqs].clone())
+    sub.temperatures = info.temperatures[:reqs].clone()
+    gp = build_dspine_target_probs(next_token_logits=x.to(device), sampling_info=W.info_to(sub, device),
+                                   block_size=T, bs=reqs, sampling_backend="pytorch")
+    got = gp.reshape(reqs * T, -1).double().cpu()
+    errs = {}
+    for exact in (True, False):
+        ref = O.build_target_probs(x, sub, T, reqs, "pytorch", exact_softmax=exact).reshape(reqs * T, -1).double()
+        both = (ref > 0) & (got > 0) & (ref >= ref.amax(-1, keepdim=True) * 1e-6)
+        rel = ((got - ref).abs() / ref.clamp_min(1e-300))[both]
+        # rows whose kept support differs (a top-p cut within the error of its boundary)
+        cut_rows = int(((got > 0) != (ref > 0)).any(-1).sum())
+        errs[exact] = (float(rel.max()), cut_rows)
+    print(f"[p-error] vs float64 softmax {errs[True][0]:.3g} ({errs[True][1]} rows with another cut), "
+          f"vs CPU torch float32 {errs[False][0]:.3g} ({errs[False][1]} rows with another cut)", flush=True)
+    # the parity tests compare against the exact softmax: the HIP path's P must sit well inside
+    # MARGIN of it, with the same cut on every row
+    assert errs[True][0] < MARGIN / 4, errs
+    assert errs[True][1] == 0, errs
+    # CPU torch's float32 normaliser is itself ~1e-5 off on these 151936-wide rows and cuts
+    # some top-p rows inside a bf16 tie group elsewhere (the reason the oracle's exact softmax
+    # is the parity reference); bounded here only to keep the figure on record
+    assert errs[False][0] < 1e-4, errs

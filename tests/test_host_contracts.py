@@ -187,3 +187,162 @@ def test_compress_and_padding_need_device_tensors():
         compress_probs(torch, torch.zeros(2, 5))
     with pytest.raises(ValueError, match="device"):
         logits_padding(None, torch.zeros(1), (2, 5))
+
+
+# ------------------------------------------------------------------------------------------
+# the AROUND hook on the verify-logit adjustments (sampling/compact.py:82-116)
+# ------------------------------------------------------------------------------------------
+class _Info(list):
+    """A sampling_info with no adjustment tensors (adjust_logits is then a no-op) and
+    len() = batch size."""
+
+    def __init__(self, bs, custom=False):
+        super().__init__(range(bs))
+        self.has_custom_logit_processor = custom
+
+
+@pytest.fixture
+def hook_env(monkeypatch):
+    import sys
+    import types
+
+    from dspine_amd.runtime import worker as Wk
+
+    calls = []
+    sampler_mod = types.ModuleType("sglang.srt.layers.sampler")
+    sampler_mod.apply_custom_logit_processor = lambda logits, info, num_tokens_in_batch: calls.append(
+        ("custom", logits.shape, num_tokens_in_batch))
+    for name in ("sglang", "sglang.srt", "sglang.srt.layers"):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    monkeypatch.setitem(sys.modules, "sglang.srt.layers.sampler", sampler_mod)
+    monkeypatch.setattr(Wk, "_active_worker", None)
+
+    def original(**kw):
+        calls.append(("original", kw["next_token_logits"].shape, kw["draft_token_num"]))
+        return "original"
+
+    return Wk, calls, original
+
+
+def test_hook_without_worker_runs_original(hook_env):
+    from dspine_amd.sampling.compact import around_verify_logits_adjustments
+
+    Wk, calls, original = hook_env
+    logits = torch.zeros(6, 5)
+    assert around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=_Info(2),
+                                            draft_token_num=3) == "original"
+    assert calls == [("original", (6, 5), 3)]
+
+
+def test_hook_worker_without_controller_adjusts_full_block(hook_env):
+    from dspine_amd.sampling.compact import around_verify_logits_adjustments
+
+    Wk, calls, original = hook_env
+    Wk._active_worker = SimpleNamespace(verify_caps=None)
+    logits = torch.zeros(6, 5)
+    assert around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=_Info(2),
+                                            draft_token_num=3) is None
+    assert calls == []  # neither the original nor a custom processor
+    # custom logit processors run before the DSpine adjustments, over the [bs*T, V] rows
+    around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=_Info(2, custom=True),
+                                     draft_token_num=3)
+    assert calls == [("custom", (6, 5), 3)]
+    assert around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=None,
+                                            draft_token_num=3) is None
+    with pytest.raises(ValueError, match="request/block layout"):
+        around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=_Info(3),
+                                         draft_token_num=3)
+    with pytest.raises(ValueError, match="positive draft width"):
+        around_verify_logits_adjustments(original, next_token_logits=logits, sampling_info=_Info(2),
+                                         draft_token_num=0)
+
+
+def test_hook_compact_round(hook_env):
+    from dspine_amd.sampling.compact import around_verify_logits_adjustments
+
+    Wk, calls, original = hook_env
+    packed = torch.zeros(4, 5)
+    ctl = SimpleNamespace(compact_round=True, compact_logits=packed, row_to_request=torch.tensor([0, 0, 1, 1]))
+    Wk._active_worker = SimpleNamespace(verify_caps=ctl)
+    with pytest.raises(RuntimeError, match="do not belong to this round"):
+        around_verify_logits_adjustments(original, next_token_logits=packed.clone(), sampling_info=_Info(2),
+                                         draft_token_num=3)
+    # the round's own packed rows: adjusted with the controller's row map (no custom step)
+    assert around_verify_logits_adjustments(original, next_token_logits=packed,
+                                            sampling_info=_Info(2, custom=True), draft_token_num=3) is None
+    assert calls == []
+    # a controller outside a compact round: the full-block branch
+    ctl.compact_round = False
+    around_verify_logits_adjustments(original, next_token_logits=torch.zeros(6, 5),
+                                     sampling_info=_Info(2, custom=True), draft_token_num=3)
+    assert calls == [("custom", (6, 5), 3)]
+
+
+# ------------------------------------------------------------------------------------------
+# controller acceptance state checks (verification/caps.py:331-379, ragged.py:282-335)
+# ------------------------------------------------------------------------------------------
+def _accept_kwargs(bs=2, T=4):
+    return dict(candidates=torch.zeros(bs, T, dtype=torch.int64), next_token_logits=torch.zeros(bs * T, 8),
+                sampling_info=None, draft_input=None, prefix_lens=torch.zeros(bs, dtype=torch.int32), bs=bs)
+
+
+def test_capped_accept_requires_confirmed_forward():
+    from dspine_amd.verification import caps
+
+    ctl = SimpleNamespace(executed_width=3, active=2, sampled_round=False, full=4)
+    with pytest.raises(RuntimeError, match="confirmed shortened target forward"):
+        caps.accept(ctl, **_accept_kwargs())
+
+
+def test_ragged_accept_requires_confirmed_packed_verification():
+    from dspine_amd.verification import ragged
+
+    ctl = SimpleNamespace(ragged_round=True, batch_size=2, executed_tokens=5, tokens=6, sampled_round=False,
+                          full=4)
+    with pytest.raises(RuntimeError, match="confirmed packed verification"):
+        ragged.accept(ctl, **_accept_kwargs())
+    ctl.executed_tokens = 6
+    with pytest.raises(RuntimeError, match="confirmed packed verification"):
+        ragged.accept(ctl, **_accept_kwargs(bs=3))
+    # not a ragged round: the capped controller's checks apply
+    ctl = SimpleNamespace(ragged_round=False, executed_width=4, active=3, sampled_round=False, full=4)
+    with pytest.raises(RuntimeError, match="confirmed shortened target forward"):
+        ragged.accept(ctl, **_accept_kwargs())
+
+
+def test_sample_prefix_compact_rows_need_offsets():
+    from dspine_amd.sampling.target import TargetDistribution
+
+    sampler = SimpleNamespace(round_sampled=True, round_bs=2)
+    td = TargetDistribution(SimpleNamespace(block_size=4, _dspine_sampler=sampler))
+    with pytest.raises(ValueError, match="need their row_offsets"):
+        td.sample_prefix(candidates=torch.zeros(2, 4, dtype=torch.int64), next_token_logits=torch.zeros(5, 8),
+                         sampling_info=None, prefix_lens=torch.zeros(2, dtype=torch.int32), bs=2,
+                         verify_lens=torch.tensor([2, 3], dtype=torch.int32),
+                         row_to_request=torch.tensor([0, 0, 1, 1, 1]))
+
+
+# ------------------------------------------------------------------------------------------
+# SPS planner contracts (verification/sps.py:35-70)
+# ------------------------------------------------------------------------------------------
+def test_sps_plan_contracts():
+    from dspine_amd.verification.sps import allocate_verify_lens, device_plan
+
+    raw, table, depth = torch.rand(3, 15), torch.rand(15, 8), torch.arange(15)
+    cfg = SimpleNamespace(min_verify_len=1, survival_eps=0.0)
+    with pytest.raises(ValueError, match="SPS budget"):
+        allocate_verify_lens(raw, table, depth, 2)
+    with pytest.raises(ValueError, match="SPS budget"):
+        device_plan(raw, table, depth, 49, cfg)
+    with pytest.raises(ValueError, match="one root per request"):
+        device_plan(raw, table, depth, 10, SimpleNamespace(min_verify_len=2, survival_eps=0.0))
+    with pytest.raises(ValueError, match="one root per request"):
+        device_plan(raw, table, depth, 10, SimpleNamespace(min_verify_len=1, survival_eps=0.1))
+    with pytest.raises(ValueError, match="graph tier"):
+        device_plan(raw, table, depth, 10, cfg, graph_tokens=12)
+    with pytest.raises(ValueError, match="one table row per draft position"):
+        allocate_verify_lens(raw, table, depth[:-1], 10)
+    with pytest.raises(ValueError, match="at most bins - 1"):
+        allocate_verify_lens(raw, table, depth, 10, torch.linspace(0.1, 0.9, 8, dtype=torch.float64))
+    with pytest.raises(ValueError, match="device"):  # CPU tensors never reach the HIP library
+        allocate_verify_lens(raw, table, depth, 10)

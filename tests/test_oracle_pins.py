@@ -529,3 +529,88 @@ def test_sample_chain_confidence_known_answers():
     O.sample_chain(table, [1 / temperature] * 2, [5, 5], [0.8, 0.8], [0.05, 0.05], [0, 1], np.array([0.2, 0.8]),
                    np.arange(k)[None].repeat(2, 0), np.zeros(2, np.int64), width, confidence=conf2)
     assert conf2[1] == -1.0 and conf2[0] == conf[0]
+
+
+# ------------------------------------------------------------------------------------------
+# SPS planner (verification/sps.py:35-99)
+# ------------------------------------------------------------------------------------------
+def _order_lens(survival, bs, gamma, budget):
+    """The reference's brute-force rule (tests/test_sps.py:369-384): positions ordered by
+    (-survival, depth, request), the first budget - bs taken, lengths 1 + taken per request."""
+    order = sorted(((b, d) for b in range(bs) for d in range(gamma)),
+                   key=lambda pair: (-float(survival[pair]), pair[1], pair[0]))
+    selected = set(order[:budget - bs])
+    return [1 + sum((b, d) in selected for d in range(gamma)) for b in range(bs)], selected
+
+
+@pytest.mark.parametrize("bs", [1, 3, 9, 17, 65])
+def test_allocation_matches_global_survival_order(bs):
+    """tests/test_sps.py:360-384: equal confidences tie across rows and depths; the selection
+    is the global (-survival, depth, request) order and never takes a descendant without its
+    ancestors."""
+    generator = torch.Generator().manual_seed(714)
+    raw = torch.rand((bs, 15), generator=generator)
+    raw[::2] = 1
+    table = torch.linspace(0.1, 1.0, 16).expand(15, 16)
+    conditional = table[torch.arange(15), (raw * 16).long().clamp(0, 15)]
+    survival = conditional.cumprod(-1)
+    for budget in (bs, bs * 7 + (bs > 1), bs * 16):
+        lens = O.allocate_verify_lens(raw, table, torch.arange(15), budget)
+        expected, selected = _order_lens(survival, bs, 15, budget)
+        assert lens.tolist() == expected and int(lens.sum()) == budget
+        assert all((b, d) in selected for b, n in enumerate(expected) for d in range(n - 1))
+
+
+def test_allocation_fp32_extreme_survival():
+    """tests/test_sps.py:387-417: survival values at the float32 extremes (1 - 2^-24, tiny,
+    1e-30) keep ancestor order at every budget, lengths only grow with the budget."""
+    bs, gamma = 4, 15
+    conditional = torch.tensor([
+        [1.0] * gamma,
+        [1.0, 1.0 - 2**-24, 1.0 - 2**-23] * 5,
+        [1e-30, 1.0, 1e-30] + [1.0] * 12,
+        [1.0, torch.finfo(torch.float32).tiny, 1.0, 1e-10] + [1.0] * 11,
+    ], dtype=torch.float32)
+    table = conditional.T.contiguous()
+    raw = torch.tensor([0.125, 0.375, 0.625, 0.875])[:, None].expand(bs, gamma)
+    survival = conditional.cumprod(-1).cummin(-1).values
+    previous = [1] * bs
+    for budget in range(bs, bs * (gamma + 1) + 1):
+        lens = O.allocate_verify_lens(raw, table, torch.arange(gamma), budget).tolist()
+        expected, selected = _order_lens(survival, bs, gamma, budget)
+        assert lens == expected and sum(lens) == budget
+        assert all(1 <= n <= gamma + 1 and n >= old for n, old in zip(lens, previous))
+        previous = lens
+
+
+def test_allocation_bucketize_boundaries():
+    """Bins from float64 boundaries (tests/test_sps.py:420-448's logit grid): each confidence's
+    bin is the count of boundaries strictly below it in float64 (np.searchsorted, left), and the
+    lengths follow the brute-force order of the looked-up survival."""
+    logits = torch.linspace(-13.815509557963773, 13.815509557963773, 1024, dtype=torch.float64)
+    boundaries = ((logits[1:] + logits[:-1]) / 2).sigmoid()
+    table = (0.216 * logits + 0.3).sigmoid().float().repeat(15, 1)
+    g = torch.Generator().manual_seed(3)
+    raw = torch.rand((5, 15), generator=g)
+    raw[0] = 1.0
+    raw[1, :3] = 0.0
+    raw[2, 4] = float(boundaries[500])  # a confidence equal to a boundary (rounded to float32)
+    bins = np.searchsorted(boundaries.numpy(), raw.double().numpy(), side="left")
+    conditional = table[torch.arange(15), torch.as_tensor(bins)]
+    survival = conditional.double().cumprod(-1).float().cummin(-1).values
+    for budget in (5, 17, 40, 80):
+        lens = O.allocate_verify_lens(raw, table, torch.arange(15), budget, boundaries)
+        assert lens.tolist() == _order_lens(survival, 5, 15, budget)[0]
+
+
+def test_allocation_rejects_budget_outside_block():
+    with pytest.raises(ValueError, match="SPS budget"):
+        O.allocate_verify_lens(torch.rand(3, 15), torch.rand(15, 4), torch.arange(15), 2)
+    with pytest.raises(ValueError, match="SPS budget"):
+        O.allocate_verify_lens(torch.rand(3, 15), torch.rand(15, 4), torch.arange(15), 49)
+
+
+def test_sps_layout_closed_form():
+    qo, idx = O.sps_layout([1, 3, 2], 16)
+    assert qo.tolist() == [0, 1, 4, 6]
+    assert idx.tolist() == [0, 16, 17, 18, 32, 33]
