@@ -26,6 +26,7 @@ EXPORTS = (
     "dsv_uniforms", "dsv_profile_events", "dsv_adjust_logits", "dsv_adjust_history",
     "dsv_logits_padding", "dsv_window_index", "dsv_target_probs", "dsv_compress",
     "dsv_accept_chain", "dsv_sample_chain", "dsv_pack_joint", "dsv_sps_plan",
+    "dsv_greedy_verify_noalloc",
 )
 DSV_ADJ_ADD, DSV_ADJ_SCALE = 0, 1
 
@@ -106,6 +107,9 @@ def load():
         lib.dsv_greedy_verify.restype = i32
         lib.dsv_greedy_verify.argtypes = [vp, i32, i64, i64, i64, i32, i32, vp, vp, i32, vp,
                                           vp, vp, vp, vp, vp, vp, vp, i64, vp]
+        lib.dsv_greedy_verify_noalloc.restype = i32
+        lib.dsv_greedy_verify_noalloc.argtypes = [vp, i32, i64, i64, i64, i32, i32, vp, vp, i32, vp,
+                                                  vp, vp, vp, vp, vp, vp, vp]
         lib.dsv_topk.restype = i32
         lib.dsv_topk.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, i32, vp, i64, vp]
         lib.dsv_uniforms.restype = i32

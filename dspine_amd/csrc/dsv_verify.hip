@@ -28,6 +28,8 @@
 #include <float.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "dsv_device.h"
 
 namespace dsv {
@@ -3104,6 +3106,68 @@ extern "C" int dsv_greedy_verify(const void* logits, int32_t dtype, int64_t rows
   return greedy_launch(logits, dtype, rows, vocab, row_stride, bs, T, candidates, verify_lens, cap, prefix_lens,
                        accept, commit, bonus, output, new_seq, top1_out, cstat,
                        reinterpret_cast<hipStream_t>(stream_));
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free greedy verify: the per-chunk statistics go to a static device array instead
+// of a caller workspace.  Each device holds its own copy for the life of the process; its
+// address is looked up once per device (hipGetSymbolAddress, the device current) and only that
+// address is handed to kernels -- the array's name in host code is not a device address.
+// ---------------------------------------------------------------------------------------
+constexpr int64_t NOALLOC_CHUNK_STATS = 65536;  // (row, chunk) statistics: 65536 x 40 B = 2.5 MiB
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) ChunkStat scratch[NOALLOC_CHUNK_STATS];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// The scratch address on the current device (looked up on the first call there).
+static int noalloc_scratch(hipStream_t stream, ChunkStat** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_greedy_verify_noalloc: no usable current device");
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess)
+      DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify_noalloc: cannot query the stream's device");
+    if (sdev != dev)
+      DSV_FAIL(DSV_ERR_INVALID, "dsv_greedy_verify_noalloc: the stream belongs to device %d, device %d is current",
+               (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      DSV_FAIL(DSV_ERR_LAUNCH, "dsv_greedy_verify_noalloc: scratch address lookup failed on device %d: %s", dev,
+               hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = reinterpret_cast<ChunkStat*>(g_scratch_ptr[dev]);
+  return DSV_OK;
+}
+
+extern "C" int dsv_greedy_verify_noalloc(const void* logits, int32_t dtype, int64_t rows, int64_t vocab,
+                                         int64_t row_stride, int32_t bs, int32_t T, const int64_t* candidates,
+                                         const int32_t* verify_lens, int32_t cap, const int32_t* prefix_lens,
+                                         int32_t* accept, int32_t* commit, int64_t* bonus, int64_t* output,
+                                         int32_t* new_seq, int64_t* top1_out, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int rc = greedy_check("dsv_greedy_verify_noalloc", logits, dtype, rows, vocab, row_stride, bs, T,
+                              candidates, verify_lens, cap, prefix_lens, accept, commit, bonus, output, new_seq);
+  if (rc != DSV_OK) return rc;
+  const int64_t need = rows * chunks_per_row(vocab, dtype);
+  if (need > NOALLOC_CHUNK_STATS)
+    DSV_FAIL(DSV_ERR_INVALID,
+             "dsv_greedy_verify_noalloc: %lld rows x %d chunks exceed the %lld chunk statistics of the static "
+             "scratch (use dsv_greedy_verify with a workspace)",
+             (long long)rows, chunks_per_row(vocab, dtype), (long long)NOALLOC_CHUNK_STATS);
+  ChunkStat* cstat = nullptr;
+  const int rc2 = noalloc_scratch(stream, &cstat);
+  if (rc2 != DSV_OK) return rc2;
+  // every (row, chunk) statistic is written by the chunk pass before the acceptance reads it:
+  // nothing in the scratch needs clearing
+  return greedy_launch(logits, dtype, rows, vocab, row_stride, bs, T, candidates, verify_lens, cap, prefix_lens,
+                       accept, commit, bonus, output, new_seq, top1_out, cstat, stream);
 }
 
 extern "C" int64_t dsv_topk_workspace_bytes(int64_t rows, int64_t vocab, int32_t k) {

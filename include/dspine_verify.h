@@ -140,6 +140,20 @@ int dsv_greedy_verify(const void* logits, int32_t logits_dtype, int64_t rows, in
                       int64_t workspace_bytes, dsv_stream_t stream);
 int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab);
 
+/* dsv_greedy_verify without a workspace argument and without any allocation.  No counterpart */
+/* in the reference: it is for callers that cannot allocate device memory (code under HIP      */
+/* graph capture, serving loops or harnesses that forbid hipMalloc).  The per-chunk statistics */
+/* live in a static device array of the library (2.5 MiB a device, held until the process     */
+/* ends): rows * ceil(vocab / 20480) (bf16) or rows * ceil(vocab / 10240) (float32) must not   */
+/* exceed 65536 (DSV_ERR_INVALID otherwise; e.g. 8192 bf16 rows of 151936).  Calls that        */
+/* overlap on one device share that array and race; the stream must belong to the current     */
+/* device.  Same arguments and outputs as dsv_greedy_verify otherwise.                         */
+int dsv_greedy_verify_noalloc(const void* logits, int32_t logits_dtype, int64_t rows, int64_t vocab,
+                              int64_t row_stride, int32_t bs, int32_t T, const int64_t* candidates,
+                              const int32_t* verify_lens, int32_t cap, const int32_t* prefix_lens,
+                              int32_t* accept, int32_t* commit, int64_t* bonus, int64_t* output,
+                              int32_t* new_seq, int64_t* top1_out, dsv_stream_t stream);
+
 /* Top-k per row in (value desc, id asc) order, k in [1, 256].  values_out [rows, k] float32 */
 /* (may be NULL), ids_out [rows, k] int64; sort_by_id != 0 re-sorts each row's ids ascending */
 /* (topk_ids).  workspace: dsv_topk_workspace_bytes(rows, vocab, k) bytes of device memory.  */
