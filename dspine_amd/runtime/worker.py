@@ -245,3 +245,59 @@ def accept_dspine_sampled_round(*, candidates, next_token_logits, sampling_info,
     return worker._accept_sampled_round(candidates=candidates, next_token_logits=next_token_logits,
                                         sampling_info=sampling_info, max_top_k=max_top_k,
                                         uniform_top_k_value=uniform_top_k_value)
+
+
+def commit_accept(outputs, *, prefix_lens, req_pool_indices, req_to_token, out_cache_loc=None,
+                  verify_lens=None, slot_offsets=None, seq_lens=None, free_slots=None, free_count=None):
+    """Commit one verified round (``dsv_commit_accept``): what SGLang's speculative worker does
+    with the accept / bonus buffers after verification (its ``_commit_accept``, which the
+    reference's tests/test_tp_accept.py:106-180 drive; SGLang itself is not part of the
+    reference, so this is the closed form).
+
+    ``outputs`` is the round's 5-tuple (only ``accept`` [bs] int32 is read; the caller keeps the
+    buffers, which the worker double-buffers).  Request b verified positions
+    ``prefix_lens[b] + i`` for ``i < verify_lens[b]`` (default: the block width T) and commits the
+    first ``accept[b] + 1``.  With ``out_cache_loc`` (int64 window slots, ``b*T + i`` or
+    ``slot_offsets[b] + i``) the committed slots are written into ``req_to_token[
+    req_pool_indices[b], prefix + i]``; without it the slots are already in the table.
+    ``seq_lens[req_pool_indices[b]]`` becomes ``prefix + accept + 1``; the slots of the rejected
+    positions are compacted into ``free_slots`` (int64, (b, i) order) and counted in
+    ``free_count[0]``.  Returns ``(free_slots, free_count)``."""
+    accept, output = outputs[0], outputs[3]
+    bs, T = output.shape
+    dev = _lib.require_cuda(accept, prefix_lens, req_pool_indices, req_to_token, out_cache_loc, verify_lens,
+                            slot_offsets, seq_lens, free_slots, free_count)
+    if accept.shape != (bs,) or accept.dtype != torch.int32 or not accept.is_contiguous():
+        raise ValueError("accept must be contiguous int32 [bs]")
+    for name, t in (("prefix_lens", prefix_lens), ("req_pool_indices", req_pool_indices)):
+        if t.shape != (bs,) or t.dtype not in (torch.int32, torch.int64) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32/int64 [bs] vector")
+    if req_to_token.ndim != 2 or req_to_token.dtype != torch.int32 or req_to_token.stride(1) != 1:
+        raise ValueError("req_to_token must be a row-contiguous int32 [pool, context] table")
+    if verify_lens is not None and (verify_lens.shape != (bs,) or verify_lens.dtype != torch.int32
+                                    or not verify_lens.is_contiguous()):
+        raise ValueError("verify_lens must be contiguous int32 [bs]")
+    if out_cache_loc is not None and (out_cache_loc.dtype != torch.int64 or not out_cache_loc.is_contiguous()):
+        raise ValueError("out_cache_loc must be contiguous int64")
+    if out_cache_loc is not None and slot_offsets is None and out_cache_loc.numel() < bs * T:
+        raise ValueError("out_cache_loc must hold the [bs*T] window slots")
+    if slot_offsets is not None and (slot_offsets.shape != (bs,) or slot_offsets.dtype != torch.int64
+                                     or out_cache_loc is None):
+        raise ValueError("slot_offsets must be int64 [bs] offsets into out_cache_loc")
+    if seq_lens is not None and (seq_lens.dtype not in (torch.int32, torch.int64) or not seq_lens.is_contiguous()):
+        raise ValueError("seq_lens must be a contiguous int32/int64 vector")
+    if free_slots is None:
+        free_slots = torch.empty(bs * T, device=dev, dtype=torch.int64)
+    elif free_slots.dtype != torch.int64 or free_slots.numel() < bs * T or not free_slots.is_contiguous():
+        raise ValueError("free_slots must be contiguous int64 with room for bs*T slots")
+    if free_count is None:
+        free_count = torch.empty(1, device=dev, dtype=torch.int32)
+    elif free_count.dtype != torch.int32 or free_count.numel() < 1:
+        raise ValueError("free_count must be int32 [1]")
+    _lib.check(_lib.load().dsv_commit_accept(
+        bs, T, accept.data_ptr(), _lib.ptr(verify_lens), prefix_lens.data_ptr(),
+        int(prefix_lens.dtype == torch.int64), req_pool_indices.data_ptr(), int(req_pool_indices.dtype == torch.int64),
+        req_to_token.data_ptr(), req_to_token.stride(0), req_to_token.shape[1], _lib.ptr(out_cache_loc),
+        _lib.ptr(slot_offsets), _lib.ptr(seq_lens), int(seq_lens is not None and seq_lens.dtype == torch.int64),
+        free_slots.data_ptr(), free_count.data_ptr(), _lib.stream_of(dev)), "dsv_commit_accept")
+    return free_slots, free_count

@@ -34,6 +34,9 @@
  *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices)
  *   dsv_sps_plan          verification/sps.py:35-58 (allocate_verify_lens) and :61-99
  *                         (device_plan: lengths, layout row pointer, _indices)
+ *   dsv_commit_accept     the commit after the accept buffers (SGLang's _commit_accept, not in
+ *                         the reference; its accept-buffer discipline tests/test_tp_accept.py
+ *                         :106-180)
  */
 #ifndef DSPINE_VERIFY_H
 #define DSPINE_VERIFY_H
@@ -277,6 +280,21 @@ int dsv_sps_plan(const float* raw, int64_t raw_stride, int32_t bs, int32_t gamma
                  int64_t prob_stride, int32_t n_bins, int64_t prob_rows, const int64_t* depth,
                  const double* boundaries, int32_t n_boundaries, int32_t budget, int32_t* verify_lens,
                  int32_t* qo_indptr, int64_t* window_index, dsv_stream_t stream);
+
+/* Commit of an accepted round (SGLang's _commit_accept after the accept / bonus buffers,      */
+/* tests/test_tp_accept.py:106-180 of the reference; SGLang is not in the reference, the      */
+/* closed form is this build's): request b verified n = verify_lens[b] (NULL: T) positions     */
+/* prefix_lens[b] + i with window slots out_cache_loc[slot_offsets[b] + i] (slot_offsets NULL: */
+/* b*T + i); the first c = accept[b] + 1 are committed.  out_cache_loc given: req_to_token[    */
+/* req_pool_indices[b], prefix + i] = slot for i < c; NULL: the slots are already in the table */
+/* and are read from it.  seq_lens[req_pool_indices[b]] = prefix + c (int32 / int64, may be   */
+/* NULL); the slots of positions c .. n-1 go to free_slots (int64, in (b, i) order, capacity   */
+/* sum(n - c) <= bs*T) and their count to free_count[0] (either may be NULL).                 */
+int dsv_commit_accept(int32_t bs, int32_t T, const int32_t* accept, const int32_t* verify_lens,
+                      const void* prefix_lens, int32_t prefix_i64, const void* req_pool_indices,
+                      int32_t req_pool_i64, int32_t* req_to_token, int64_t rt_stride, int64_t rt_cols,
+                      const int64_t* out_cache_loc, const int64_t* slot_offsets, void* seq_lens,
+                      int32_t seq_lens_i64, int64_t* free_slots, int32_t* free_count, dsv_stream_t stream);
 
 #ifdef __cplusplus
 }

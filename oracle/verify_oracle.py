@@ -50,6 +50,8 @@ PINNED = {
     "allocate_verify_lens": "the reference's brute-force order (-survival, depth, request) of "
     "tests/test_sps.py:360-384 and its fp32 extreme rows :387-417; bucketize boundaries of :420-448",
     "sps_layout": "closed form (exclusive prefix; tests/test_sps.py:446-448)",
+    "commit_accept": "hand-computed known answer and invariants (committed + freed = verified "
+    "slots); parity with SGLang's _commit_accept unpinned (SGLang is not in the reference)",
     "logits_padding": "tests/test_release.py:45-67",
     "sample_chain": "ties-to-lower-lane known answer tests/test_cuda.py:213-232, brute force; "
     "confidence known answers tests/test_sampled_confidence.py:124-196",
@@ -597,6 +599,41 @@ def sps_layout(lens, T: int):
     qo = np.zeros(lens.size + 1, dtype=np.int32)
     qo[1:] = np.cumsum(lens)
     return qo, window_index(lens, T)
+
+
+def commit_accept(accept, prefix_lens, req_pool_indices, req_to_token, T: int, out_cache_loc=None,
+                  verify_lens=None, slot_offsets=None, seq_lens=None):
+    """The commit after a verified round (SGLang's _commit_accept, which the reference's
+    tests/test_tp_accept.py:106-180 drive; SGLang is not part of the reference, so this is the
+    closed form -- parity with SGLang unpinned): request b verified n_b positions prefix_b + i
+    and commits c_b = accept_b + 1 of them.  With window slots, req_to_token[row_b, prefix_b + i]
+    = slot for i < c_b; seq_lens[row_b] = prefix_b + c_b; the slots of positions c_b .. n_b - 1
+    in (b, i) order are freed.  Mutates req_to_token / seq_lens (numpy) in place; returns the
+    freed slots (int64)."""
+    acc = np.asarray(accept, dtype=np.int64).reshape(-1)
+    bs = acc.size
+    prefix = np.asarray(prefix_lens, dtype=np.int64).reshape(-1)
+    rows = np.asarray(req_pool_indices, dtype=np.int64).reshape(-1)
+    lens = np.full(bs, T) if verify_lens is None else np.asarray(verify_lens, dtype=np.int64).reshape(-1)
+    freed = []
+    for b in range(bs):
+        n = int(min(max(lens[b], 1), T))
+        c = int(min(max(acc[b] + 1, 1), n))
+        base = int(slot_offsets[b]) if slot_offsets is not None else b * T
+        for i in range(n):
+            pos = int(prefix[b]) + i
+            in_table = 0 <= pos < req_to_token.shape[1]
+            if out_cache_loc is not None:
+                slot = int(out_cache_loc[base + i])
+                if i < c and in_table:
+                    req_to_token[rows[b], pos] = slot
+            else:
+                slot = int(req_to_token[rows[b], pos]) if in_table else -1
+            if i >= c:
+                freed.append(slot)
+        if seq_lens is not None:
+            seq_lens[rows[b]] = int(prefix[b]) + c
+    return np.asarray(freed, dtype=np.int64)
 
 
 def kv_slots(page_table, prefix_lens, accept, T: int) -> np.ndarray:

@@ -614,3 +614,43 @@ def test_sps_layout_closed_form():
     qo, idx = O.sps_layout([1, 3, 2], 16)
     assert qo.tolist() == [0, 1, 4, 6]
     assert idx.tolist() == [0, 16, 17, 18, 32, 33]
+
+
+# ------------------------------------------------------------------------------------------
+# commit of an accepted round (closed form; parity with SGLang's _commit_accept unpinned)
+# ------------------------------------------------------------------------------------------
+def test_commit_accept_known_answer():
+    """Two requests in pool rows 3 and 0, T = 4: request 0 (prefix 10) accepts 1 of its 4
+    positions (commits 2), request 1 (prefix 5, verify length 3) accepts 2 (commits 3)."""
+    table = np.full((4, 16), -9, np.int32)
+    seq = np.zeros(4, np.int64)
+    ocl = np.arange(100, 108, dtype=np.int64)  # window slots b*4 + i
+    freed = O.commit_accept([1, 2], [10, 5], [3, 0], table, 4, out_cache_loc=ocl, verify_lens=[4, 3], seq_lens=seq)
+    assert table[3, 10:12].tolist() == [100, 101] and (table[3, 12:] == -9).all()
+    assert table[0, 5:8].tolist() == [104, 105, 106] and table[0, 8] == -9
+    assert seq.tolist() == [8, 0, 0, 12]
+    assert freed.tolist() == [102, 103]  # request 1 committed all three verified positions
+
+
+def test_commit_accept_invariants():
+    """Committed + freed slots are exactly the verified window slots; slots already in the
+    table are read from it when no window slots are given."""
+    rng = np.random.default_rng(3)
+    bs, T = 9, 6
+    acc = rng.integers(0, T, bs)
+    lens = rng.integers(1, T + 1, bs)
+    prefix = rng.integers(0, 20, bs)
+    rows = rng.permutation(12)[:bs]
+    ocl = rng.permutation(1000)[: bs * T].astype(np.int64)
+    table = np.full((12, 40), -1, np.int32)
+    freed = O.commit_accept(acc, prefix, rows, table, T, out_cache_loc=ocl, verify_lens=lens)
+    committed = [int(table[rows[b], prefix[b] + i]) for b in range(bs)
+                 for i in range(min(acc[b] + 1, lens[b]))]
+    verified = [int(ocl[b * T + i]) for b in range(bs) for i in range(lens[b])]
+    assert sorted(committed + freed.tolist()) == sorted(verified)
+    # the same round with the slots already in the table
+    table2 = np.full((12, 40), -1, np.int32)
+    for b in range(bs):
+        table2[rows[b], prefix[b]: prefix[b] + T] = ocl[b * T: b * T + T]
+    freed2 = O.commit_accept(acc, prefix, rows, table2, T, verify_lens=lens)
+    assert freed2.tolist() == freed.tolist()
