@@ -26,7 +26,7 @@ EXPORTS = (
     "dsv_uniforms", "dsv_profile_events", "dsv_adjust_logits", "dsv_adjust_history",
     "dsv_logits_padding", "dsv_window_index", "dsv_target_probs", "dsv_compress",
     "dsv_accept_chain", "dsv_sample_chain", "dsv_pack_joint", "dsv_sps_plan",
-    "dsv_greedy_verify_noalloc", "dsv_commit_accept",
+    "dsv_greedy_verify_noalloc", "dsv_commit_accept", "dsv_rs_table", "dsv_rs_table_workspace_bytes",
 )
 DSV_ADJ_ADD, DSV_ADJ_SCALE = 0, 1
 
@@ -134,6 +134,11 @@ def load():
         lib.dsv_pack_joint.argtypes = [vp, vp, i64, i32, vp, vp, i32, vp, vp, vp, vp, vp, i64, i64, vp]
         lib.dsv_sample_chain.restype = i32
         lib.dsv_sample_chain.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.dsv_rs_table_workspace_bytes.restype = i64
+        lib.dsv_rs_table_workspace_bytes.argtypes = [i64, i32, i32, i32]
+        lib.dsv_rs_table.restype = i32
+        lib.dsv_rs_table.argtypes = [vp, i64, vp, vp, i64, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp, vp, i32, i32,
+                                     vp, vp, i32, vp, vp, i32, _c.c_float, vp, vp, i64, vp]
         lib.dsv_commit_accept.restype = i32
         lib.dsv_commit_accept.argtypes = [i32, i32, vp, vp, vp, i32, vp, i32, vp, i64, i64, vp, vp, vp, i32, vp, vp,
                                           vp]

@@ -121,3 +121,77 @@ def serial_sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, g
             uu.data_ptr(), cand.data_ptr(), gt.data_ptr(), out_tok.data_ptr(), out_q.data_ptr(),
             _lib.ptr(confidence_out), _lib.stream_of(dev)), "dsv_sample_chain")
     return (out_tok, out_q)
+
+
+_rs_ws: dict = {}
+
+
+def serial_rs_table(raw, rms, query, anchors, cand, codebook, pred_gate_w, prev_w, gate_b, write_w, norm_w, lm_head_w,
+                    eps: float, block_size: int, out: torch.Tensor = None, chunk_rows: int = 256,
+                    res_emb: torch.Tensor = None, res_proj: torch.Tensor = None,
+                    candidate_head: torch.Tensor = None):
+    """float32 [n, K, K] sampling table of the serial last-write refinement
+    (kernels/dspine.py:505-613), n = bs*(T-1) block rows:
+    ``table[n, j, c] = normalize(x + scale * ((gate * value) @ write_w^T)) * norm_w . head[n, c]``
+    with ``gate = sigmoid(q + e @ pred_gate_w^T + gate_b)``, ``value = e @ prev_w^T`` (plus
+    ``res_emb[s] @ res_proj^T``), ``e = sqrt(C) * codebook[s]`` for sender ``s`` (the anchor on a
+    request's first block row, else candidate j of the previous row), ``x``, ``scale``, ``q`` the
+    row's pre-write state, write scale and receiver query.  Float32 on the matrix cores in three
+    launches (``dsv_rs_table``); ``chunk_rows`` is accepted for the reference's signature (nothing
+    is chunked: no intermediate of the size it bounds is materialised).
+
+    raw [bs*T, H], query [bs*T, >= R], codebook [V, C], lm_head_w [V, H], candidate_head
+    [n, K, H] and res_emb [V, r] are bfloat16; the weights float32, as the reference requires."""
+    t = int(block_size)
+    m, h = raw.shape
+    bs = m // t
+    n, k = cand.shape
+    r = pred_gate_w.shape[0]
+    if candidate_head is not None and (candidate_head.shape != (n, k, h) or candidate_head.dtype != torch.bfloat16
+                                       or not candidate_head.is_contiguous()):
+        raise ValueError("serial_rs_table candidate head must be contiguous BF16 [N,K,H]")
+    if m % t or n != bs * (t - 1) or rms.shape != (m,) or query.shape[0] != m or query.shape[1] < r \
+            or anchors.shape != (bs,):
+        raise ValueError("serial_rs_table layout mismatch")
+    for name, w in (("pred_gate_w", pred_gate_w), ("prev_w", prev_w), ("gate_b", gate_b), ("write_w", write_w),
+                    ("norm_w", norm_w)):
+        if w.dtype != torch.float32:
+            raise ValueError(f"serial_rs_table: {name} must be fp32")
+    if (res_emb is None) != (res_proj is None):
+        raise ValueError("serial_rs_table: res_emb and res_proj go together")
+    if res_proj is not None and (res_proj.dtype != torch.float32 or res_proj.shape[0] != r
+                                 or res_emb.shape != (codebook.shape[0], res_proj.shape[1])):
+        raise ValueError("serial_rs_table: terminal residual layout mismatch")
+    if out is None:
+        out = torch.empty((n, k, k), dtype=torch.float32, device=raw.device)
+    elif tuple(out.shape) != (n, k, k) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("serial_rs_table: out must be a contiguous fp32 [n, K, K] tensor")
+    if n == 0:
+        return out
+    c = codebook.shape[1]
+    shapes_ok = (pred_gate_w.shape == (r, c) and prev_w.shape == (r, c) and gate_b.numel() == r
+                 and write_w.shape == (h, r) and norm_w.numel() == h and lm_head_w.shape[1] == h)
+    if not shapes_ok:
+        raise ValueError("serial_rs_table: weight shapes do not match the state, rank and codebook widths")
+    bf16 = [raw, query, codebook, lm_head_w] + [x for x in (res_emb, candidate_head) if x is not None]
+    if any(x.dtype != torch.bfloat16 or x.stride(-1) != 1 for x in bf16):
+        raise ValueError("serial_rs_table: raw, query, codebook, head and residual embeddings must be "
+                         "row-contiguous bfloat16")
+    if anchors.dtype != torch.int64 or cand.dtype != torch.int64 or not cand.is_contiguous():
+        raise ValueError("serial_rs_table: anchors and candidates must be (contiguous) int64")
+    dev = _lib.require_cuda(raw, rms, query, anchors, cand, codebook, pred_gate_w, prev_w, gate_b, write_w,
+                            norm_w, lm_head_w, out, res_emb, res_proj, candidate_head)
+    f32c = [x.contiguous() for x in (rms, pred_gate_w, prev_w, gate_b, write_w, norm_w)]
+    rp = None if res_proj is None else res_proj.contiguous()
+    codebook, lm_head_w = codebook.contiguous(), lm_head_w.contiguous()
+    res_emb = None if res_emb is None else res_emb.contiguous()
+    lib = _lib.load()
+    ws = _rs_ws.setdefault(dev, Workspace()).get(int(lib.dsv_rs_table_workspace_bytes(n, k, h, r)), dev)
+    head = lm_head_w if candidate_head is None else candidate_head
+    _lib.check(lib.dsv_rs_table(
+        raw.data_ptr(), raw.stride(0), f32c[0].data_ptr(), query.data_ptr(), query.stride(0),
+        anchors.contiguous().data_ptr(), cand.data_ptr(), n, k, t, codebook.data_ptr(), c, f32c[1].data_ptr(),
+        f32c[2].data_ptr(), f32c[3].data_ptr(), f32c[4].data_ptr(), h, r, f32c[5].data_ptr(), head.data_ptr(),
+        int(candidate_head is not None), _lib.ptr(res_emb), _lib.ptr(rp), 0 if res_emb is None else res_emb.shape[1],
+        float(eps), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev)), "dsv_rs_table")
+    return out

@@ -31,6 +31,7 @@
  *   dsv_pack_joint        sampling/sparse/target.py:22-66,95-178 (_pack_joint, _overflow_dense,
  *                         build_sparse_target)
  *   dsv_sample_chain      kernels/dspine.py:616-772 (serial_sample_chain)
+ *   dsv_rs_table          kernels/dspine.py:505-613 (serial_rs_table)
  *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices)
  *   dsv_sps_plan          verification/sps.py:35-58 (allocate_verify_lens) and :61-99
  *                         (device_plan: lengths, layout row pointer, _indices)
@@ -280,6 +281,23 @@ int dsv_sps_plan(const float* raw, int64_t raw_stride, int32_t bs, int32_t gamma
                  int64_t prob_stride, int32_t n_bins, int64_t prob_rows, const int64_t* depth,
                  const double* boundaries, int32_t n_boundaries, int32_t budget, int32_t* verify_lens,
                  int32_t* qo_indptr, int64_t* window_index, dsv_stream_t stream);
+
+/* Draft-side sampling table of the serial last-write refinement (kernels/dspine.py:505-613,  */
+/* serial_rs_table), float32 on the matrix cores: out [n, K, K] with n = bs * (T - 1) block    */
+/* rows, out[n, j, c] = normalize(raw[r] + rms[r] * ((sigmoid(query[r] + e_j pg^T + gb) *     */
+/* (e_j pv^T + res_j res_proj^T)) write_w^T)) * norm_w . head[n, c], r = the row's state row,  */
+/* e_j = sqrt(C) * codebook[sender j] (the anchor on a request's first block row, else        */
+/* candidate j of the previous row).  raw [bs*T, H], query [bs*T, >= R], codebook [V, C], head */
+/* (lm_head [V, H] gathered by cand, or the candidate head [n, K, H] when head_is_candidates)  */
+/* and res_emb [V, RR] are bfloat16; the weights float32.  K <= 64; C, H, RR multiples of 16; */
+/* R a multiple of 64 up to 512.  workspace: dsv_rs_table_workspace_bytes(n, K, H, R).        */
+int64_t dsv_rs_table_workspace_bytes(int64_t n, int32_t K, int32_t H, int32_t R);
+int dsv_rs_table(const void* raw, int64_t raw_stride, const float* rms, const void* query, int64_t query_stride,
+                 const int64_t* anchors, const int64_t* cand, int64_t n, int32_t K, int32_t T, const void* codebook,
+                 int32_t C, const float* pred_gate_w, const float* prev_w, const float* gate_b,
+                 const float* write_w, int32_t H, int32_t R, const float* norm_w, const void* head,
+                 int32_t head_is_candidates, const void* res_emb, const float* res_proj, int32_t RR, float eps,
+                 float* out, void* workspace, int64_t workspace_bytes, dsv_stream_t stream);
 
 /* Commit of an accepted round (SGLang's _commit_accept after the accept / bonus buffers,      */
 /* tests/test_tp_accept.py:106-180 of the reference; SGLang is not in the reference, the      */

@@ -50,6 +50,8 @@ PINNED = {
     "allocate_verify_lens": "the reference's brute-force order (-survival, depth, request) of "
     "tests/test_sps.py:360-384 and its fp32 extreme rows :387-417; bucketize boundaries of :420-448",
     "sps_layout": "closed form (exclusive prefix; tests/test_sps.py:446-448)",
+    "rs_table": "the reference's explicit-loop float64 restatement (tests/ref_utils.py:52-76, retold "
+    "as scalar loops in the pin); anchor rows identical across senders; write_w = 0 closed form",
     "commit_accept": "hand-computed known answer and invariants (committed + freed = verified "
     "slots); parity with SGLang's _commit_accept unpinned (SGLang is not in the reference)",
     "logits_padding": "tests/test_release.py:45-67",
@@ -759,6 +761,32 @@ def sample_chain(table, inv_temp, top_k, top_p, min_p, greedy, u, cand, greedy_t
 # ---------------------------------------------------------------------------------------
 # The full verify step (S9 -> S1 -> S3 -> S11)
 # ---------------------------------------------------------------------------------------
+
+def rs_table(raw, rms, query, anchors, cand, codebook, pg, pv, gb, w_last, norm_w, head, eps, T,
+             res_emb=None, res_proj=None, candidate_head=None) -> torch.Tensor:
+    """float64 [n, K, K] table of the redone last write (kernels/dspine.py:505-613, the float64
+    reference tests/ref_utils.py:52-76, vectorised): for block row n of request b (state row
+    b*T + 1 + i), sender lane j (the anchor on i == 0, else candidate j of row n-1) and candidate
+    c: e = sqrt(C) codebook[s]; msg = sigmoid(q + pg e + gb) * (pv e [+ res_proj res_emb[s]]);
+    ref = x + rms * (w_last msg); T[n, j, c] = head[c] . (ref / sqrt(mean(ref^2) + eps) * norm_w)."""
+    d = torch.float64
+    m, h = raw.shape
+    n, k = cand.shape
+    r = pg.shape[0]
+    bs = m // T
+    rows = torch.tensor([b * T + 1 + i for b in range(bs) for i in range(T - 1)])
+    prev = torch.cat((torch.as_tensor(anchors).view(bs, 1, 1).expand(bs, 1, k),
+                      torch.as_tensor(cand).view(bs, T - 1, k)[:, :-1, :]), 1).reshape(n, k)
+    e = math.sqrt(codebook.shape[1]) * codebook.to(d)[prev]                      # [n, K, C]
+    gate = torch.sigmoid(query[rows, :r].to(d)[:, None, :] + e @ pg.to(d).T + gb.to(d))
+    value = e @ pv.to(d).T
+    if res_emb is not None:
+        value = value + res_emb.to(d)[prev] @ res_proj.to(d).T
+    ref = raw.to(d)[rows][:, None, :] + rms.to(d)[rows][:, None, None] * ((gate * value) @ w_last.to(d).T)
+    normalized = ref / torch.sqrt(ref.square().mean(-1, keepdim=True) + eps) * norm_w.to(d)
+    hd = (head.to(d)[torch.as_tensor(cand)] if candidate_head is None else candidate_head.to(d))  # [n, K, H]
+    return torch.einsum("njh,nch->njc", normalized, hd)
+
 
 def make_info(temperatures, top_ks, top_ps, min_ps=None, *, need_top_k=None, need_top_p=None,
               need_min_p=None, is_any_greedy=None):

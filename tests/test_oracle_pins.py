@@ -654,3 +654,77 @@ def test_commit_accept_invariants():
         table2[rows[b], prefix[b]: prefix[b] + T] = ocl[b * T: b * T + T]
     freed2 = O.commit_accept(acc, prefix, rows, table2, T, verify_lens=lens)
     assert freed2.tolist() == freed.tolist()
+
+
+# ------------------------------------------------------------------------------------------
+# draft-side sampling table of the redone last write (kernels/dspine.py:505-613)
+# ------------------------------------------------------------------------------------------
+def _rs_inputs(seed, bs=2, T=4, H=32, R=16, C=8, V=50, k=4, residual=False):
+    g = torch.Generator().manual_seed(seed)
+    m, n = bs * T, bs * (T - 1)
+    d = dict(raw=torch.randn(m, H, generator=g), rms=torch.rand(m, generator=g) + 0.5,
+             query=torch.randn(m, 3 * R, generator=g), codebook=torch.randn(V, C, generator=g) / math.sqrt(C),
+             pg=torch.randn(R, C, generator=g) / math.sqrt(C), pv=torch.randn(R, C, generator=g) / math.sqrt(C),
+             gb=torch.randn(R, generator=g) * 0.1, w_last=torch.randn(H, R, generator=g) / math.sqrt(R),
+             norm_w=1 + 0.1 * torch.randn(H, generator=g), head=torch.randn(V, H, generator=g) / math.sqrt(H))
+    d["cand"] = torch.stack([torch.randperm(V, generator=g)[:k].sort().values for _ in range(n)])
+    d["anchors"] = torch.randint(0, V, (bs,), generator=g)
+    if residual:
+        d["res_emb"] = torch.randn(V, 8, generator=g)
+        d["res_proj"] = torch.randn(R, 8, generator=g) / math.sqrt(8)
+    return d
+
+
+def _rs_call(d, T, eps=1e-6):
+    return O.rs_table(d["raw"], d["rms"], d["query"], d["anchors"], d["cand"], d["codebook"], d["pg"], d["pv"],
+                      d["gb"], d["w_last"], d["norm_w"], d["head"], eps, T, res_emb=d.get("res_emb"),
+                      res_proj=d.get("res_proj"))
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_rs_table_matches_explicit_loops(residual):
+    """The explicit per-row, per-sender float64 loops of tests/ref_utils.py:52-76 (senders: the
+    anchor on a request's first block row, the previous row's candidates after), with the
+    terminal residual added to the value when given."""
+    T, eps = 4, 1e-6
+    d = _rs_inputs(7, T=T, residual=residual)
+    got = _rs_call(d, T, eps)
+    m, h = d["raw"].shape
+    n, k = d["cand"].shape
+    C = d["codebook"].shape[1]
+    R = d["pg"].shape[0]
+    for b in range(m // T):
+        for i in range(T - 1):
+            row, nn = b * T + 1 + i, b * (T - 1) + i
+            senders = [int(d["anchors"][b])] * k if i == 0 else d["cand"][nn - 1].tolist()
+            x = d["raw"][row].double()
+            for j, s in enumerate(senders):
+                e = math.sqrt(C) * d["codebook"][s].double()
+                gate = torch.sigmoid(d["query"][row, :R].double() + d["pg"].double() @ e + d["gb"].double())
+                value = d["pv"].double() @ e
+                if residual:
+                    value = value + d["res_proj"].double() @ d["res_emb"][s].double()
+                xr = x + d["rms"][row].double() * (d["w_last"].double() @ (gate * value))
+                normalized = xr / torch.sqrt(xr.square().mean() + eps) * d["norm_w"].double()
+                want = d["head"][d["cand"][nn]].double() @ normalized
+                torch.testing.assert_close(got[nn, j], want, rtol=1e-12, atol=1e-12)
+
+
+def test_rs_table_closed_forms():
+    """A request's first block row has one sender (the anchor) for every lane: all K table rows
+    agree; with write_w = 0 the refinement is the identity and T[n, j, c] is the normalised state
+    row dotted with the candidate's head row, whatever the sender."""
+    T = 5
+    d = _rs_inputs(11, T=T)
+    got = _rs_call(d, T)
+    for b in range(2):
+        first = got[b * (T - 1)]
+        assert torch.equal(first, first[:1].expand_as(first))
+    d["w_last"] = torch.zeros_like(d["w_last"])
+    got = _rs_call(d, T)
+    for nn in range(got.shape[0]):
+        x = d["raw"][nn // (T - 1) * T + 1 + nn % (T - 1)].double()
+        xn = x / torch.sqrt(x.square().mean() + 1e-6) * d["norm_w"].double()
+        want = d["head"][d["cand"][nn]].double() @ xn
+        for j in range(got.shape[1]):
+            torch.testing.assert_close(got[nn, j], want, rtol=1e-12, atol=1e-12)
