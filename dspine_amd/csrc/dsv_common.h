@@ -26,6 +26,26 @@ constexpr int WAVE = 64;
 constexpr uint32_t NEG_INF_BF16_KEY = 0x007Fu;  // key16 of bf16 -inf (0xFF80)
 
 // ---------------------------------------------------------------------------------------
+// Device-coherent accesses: what one workgroup hands to another inside a launch.  The L2 of an
+// XCD is not coherent with the others', so these are relaxed device-scope atomic accesses
+// (global_store / global_load with sc1: written through to, and read from, the device's
+// coherence point) -- no full-L2 writeback or invalidate.  A producer publishes with st_dev
+// stores, waits for them to complete (publish_wait), then bumps a device-scope counter; the
+// workgroup whose increment completes the count reads with ld_dev.
+// ---------------------------------------------------------------------------------------
+template <class T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's memory accesses have completed (s_waitcnt vmcnt(0); the other
+// counters are left at their maxima: expcnt 7, lgkmcnt 15).
+__device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------------------------------
 // Order-preserving keys.  -0.0 is folded onto +0.0 so that equal values share one key, as
 // torch's comparisons (sort, argmax) treat them as equal.  Larger value -> larger key.
 // ---------------------------------------------------------------------------------------

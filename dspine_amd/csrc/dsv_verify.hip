@@ -2,26 +2,28 @@
 // residual resample, accepted-prefix compaction and KV-slot gather.
 //
 // Launches of one verify step (no host synchronisation):
-//   k_prep   (spans x requests) penalty bitmap of each request's token history, 20480 ids a
-//                               workgroup
 //   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 10240 fp32 values held in
-//                               registers: penalties, max/argmax, softmax partial sums, exact
+//                               registers: penalties (the chunk's slice of the request's history
+//                               bitmap built in LDS), max/argmax, softmax partial sums, exact
 //                               top-k candidates, nucleus value counts -- one read of the logits
 //   k_merge  (rows)             per row: Z, the filtered top-k support (id, P), P at the draft
 //                               token and the step's accept/reject decision; nucleus rows (a
 //                               top-p / min-p cut with top-k > 64) find their cut from the chunk
 //                               pass's value counts.  Then the bonus draw the row would give as
 //                               the accepted length: drawn for support-list rows, planned (the
-//                               chunk and threshold) for dense rows
-//   k_final  (requests)         rows those counts did not settle first (the full 65536-key
-//                               histogram, or the float32 radix descent, in the workgroup's LDS),
-//                               then the accepted length from the row decisions, the bonus token
-//                               of that row (a dense row's planned chunk scanned here), outputs
-//                               and KV slots
-// The target-distribution entry runs k_prep, k_chunk, k_merge, then k_nuc over the rows the
-// merge listed and k_dense_p.
-// Workgroups never wait on one another inside a kernel: on this multi-XCD part a device-scope
-// fence writes back and invalidates the whole L2, so every hand-off is a kernel boundary.
+//                               chunk and threshold) for dense rows.  The workgroup that merges a
+//                               request's last row writes the request's outputs when its accepted
+//                               row drew the token.
+//   k_final  (requests)         the requests left (launched when a dense row can occur): rows
+//                               the counts did not settle first (the full 65536-key histogram, or
+//                               the float32 radix descent, in the workgroup's LDS), then the
+//                               accepted length, the bonus token of that row (a dense row's
+//                               planned chunk scanned here), outputs and KV slots
+// The target-distribution entry runs k_chunk, k_merge, then k_nuc over the rows the merge
+// listed and k_dense_p.
+// Hand-offs between workgroups: kernel boundaries, except the per-request count in k_merge,
+// which uses device-coherent stores and loads (no device-scope fence: on this multi-XCD part
+// that writes back and invalidates the whole L2).
 //
 // Semantics follow runtime/worker.py:440-508 (target P, pytorch backend), sampling/rejection.py
 // :36-98 and sampling/sparse/accept.py:239-307 (chain rejection and residual resample).
@@ -57,6 +59,9 @@ struct KParams {
   int32_t softmax;        // chunk pass computes softmax partial sums (the verify entry)
   int32_t raw_p;          // dense target writer: the filtered p, not renormalised
   int32_t final_nuc;      // k_final resolves the full-histogram rows (no k_nuc launch)
+  uint32_t* req_cnt;      // [bs]: rows merged per request (zeroed by the chunk pass)
+  uint32_t* deferred;     // [bs]: 1 until the row merge wrote the request's outputs (set by the chunk pass)
+  int32_t only_deferred;  // k_final skips the requests the row merge finished
 };
 
 __device__ __forceinline__ const char* row_ptr(const dsv_verify_args& a, int64_t r) {
@@ -84,48 +89,15 @@ __device__ __forceinline__ bool pen_test(const KParams& P, int b, int64_t j) {
 }
 
 // ---------------------------------------------------------------------------------------
-// k_prep: history bitmaps
-// ---------------------------------------------------------------------------------------
-constexpr int PREP_WORDS = 640;  // bitmap words of one k_prep workgroup (20480 token ids)
-__global__ __launch_bounds__(BCT) void k_prep(KParams P) {
-  __shared__ uint32_t bm[PREP_WORDS];
-  const dsv_verify_args& a = P.a;
-  const int b = blockIdx.y, tid = threadIdx.x;
-  const int64_t w0 = (int64_t)blockIdx.x * PREP_WORDS;  // this workgroup's words of request b's bitmap
-  const int64_t lo = w0 * 32;
-  const int words = (int)(P.pwords - w0 < PREP_WORDS ? P.pwords - w0 : PREP_WORDS);
-  const int32_t* h = a.hist_ids + (int64_t)b * a.hist_len;
-  const int H = a.hist_len;
-  int64_t t[4];  // the request's ids, read before the LDS is cleared
-  for (int i0 = 0; i0 < H; i0 += 4 * BCT) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) t[g] = i0 + g * BCT + tid < H ? (int64_t)h[i0 + g * BCT + tid] : -1;
-    if (i0 == 0) {
-      for (int i = tid; i < PREP_WORDS; i += BCT) bm[i] = 0u;
-      __syncthreads();
-    }
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      if (t[g] >= lo && t[g] < a.vocab && t[g] < lo + 32 * PREP_WORDS)
-        atomicOr(&bm[(t[g] - lo) >> 5], 1u << ((t[g] - lo) & 31));
-  }
-  if (H <= 0) {
-    for (int i = tid; i < PREP_WORDS; i += BCT) bm[i] = 0u;
-  }
-  __syncthreads();
-  uint32_t* dst = P.pbits + (int64_t)b * P.pwords + w0;
-  for (int i = tid; i < words; i += BCT) dst[i] = bm[i];
-}
-
-// ---------------------------------------------------------------------------------------
 // Candidate refill: the chunk holds more values at or above the admission bound than the
-// LDS buffer.  The K-th largest buffered value is a higher bound; re-read the chunk from
+// LDS buffer (cbits: the chunk's history bits, lo a multiple of 32).  The K-th largest buffered
+// value is a higher bound; re-read the chunk from
 // memory until the admitted values fit.  Each raise drops at least CAND_CAP - K >= 256 of the
 // buffered values, so a chunk of at most 20480 values needs at most 80 rounds.  With thr0
 // nonzero the buffer holds nothing yet and the first read admits the values >= thr0.
 // ---------------------------------------------------------------------------------------
 template <int DT>
-__device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char* rowp, int64_t lo, int64_t hi,
+__device__ __noinline__ int refill_candidates(const uint32_t* cbits, const char* rowp, int64_t lo, int64_t hi,
                                               int K, float pres, float rep, uint64_t* cbuf, uint32_t* hist256,
                                               uint64_t* su, int32_t* cnt, uint64_t thr0) {
   constexpr int TOP_SHIFT = DT == DSV_BF16 ? 40 : 56;
@@ -142,7 +114,7 @@ __device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char*
     const uint64_t thr = su[0];
     for (int64_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
       float x = load_elem<DT>(rowp, j);
-      if (pbits && ((pbits[j >> 5] >> (j & 31)) & 1u)) x = penalize<DT>(x, pres, rep);
+      if (cbits && ((cbits[(j - lo) >> 5] >> (j & 31)) & 1u)) x = penalize<DT>(x, pres, rep);
       const uint64_t pk = pack(key_of<DT>(x), j);
       if (pk >= thr) {
         const int slot = atomicAdd(cnt, 1);
@@ -162,8 +134,12 @@ __device__ __noinline__ int refill_candidates(const uint32_t* pbits, const char*
 constexpr int FCT = 512;      // threads of k_final
 constexpr int DNW_MAX = FCT / WAVE;
 constexpr int64_t BONUS_LATER = -2;  // rbonus: the row is drawn in k_final
-// rbonus <= BONUS_PLAN: k_final scans the row's planned chunk BONUS_PLAN - 1 - rbonus (-1: none)
+// rbonus <= BONUS_PLAN: the row's draw is planned; the request's final scans chunk
+// BONUS_PLAN - 1 - rbonus (-1: no mass anywhere, no scan)
 constexpr int64_t BONUS_PLAN = -3;
+// deferred[b]: 0 done, 1 k_final decides the request, else a planned draw at accepted length
+// (deferred & (DEFER_ACC - 1)) - 2 in chunk (deferred >> 24) - 1
+constexpr int DEFER_ACC = 1 << 24;
 
 struct DrawShared {
   double red_d[DNW_MAX];
@@ -183,10 +159,9 @@ struct DrawShared {
   int64_t bonus;
   double chunk_lo, thr, pick_lo;
   int32_t acc, chunk, tieq, use_r, pick_thread, ptb;
-  uint64_t ptmask;   // the picked thread's span positions at the cut key
   uint64_t rmask;    // q lanes that need their rank at a split cut key
   uint64_t qmask;    // residual q lanes whose id lies in the planned chunk
-  float pw[64];      // the picked thread's span weights
+  uint4 pv[CV];       // the picked thread's span (penalised)
 };
 
 // The draw's P at value x: exp2(x c2 - M c2) * scale, scale = 1/Z (over the kept mass S for a
@@ -288,6 +263,70 @@ struct RowPre {
   int32_t top_k;
 };
 
+// History hits of a thread's vectors, penalised in place (about 0.3% of the values): each lane
+// copies its vectors holding hits to the wave's LDS slots wv / wm (WHITV of them), one lane per
+// copied vector penalises the hit elements there, and the owners read the vectors back -- the
+// registers end up penalised without a run-time register index.  bits[u]: the hit elements of
+// v[u].  Called by every lane of the wave.
+template <int DT, int NV>
+__device__ __forceinline__ void penalize_hits(uint4 (&v)[NV], const uint32_t (&bits)[NV], float pres, float rep,
+                                              uint4* wv, uint32_t* wm) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  int hv = 0;
+#pragma unroll
+  for (int u = 0; u < NV; ++u) hv += bits[u] != 0u;
+  // exclusive prefix and total of the hit vectors over the wave (a DPP scan)
+  const int incl = wave_incl_scan(hv);
+  const int tot = readlane<WAVE - 1>(incl);
+  // rounds of the wave's LDS slots (one unless the history is long): the round's hit vectors
+  // are copied out, one lane per vector penalises their elements, the owners read them back
+  for (int r0 = 0; r0 < tot; r0 += WHITV) {
+    int slot = incl - hv - r0;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      if (bits[u]) {
+        if ((unsigned)slot < (unsigned)WHITV) {
+          wv[slot] = v[u];
+          wm[slot] = bits[u];
+        }
+        ++slot;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nv = tot - r0 < WHITV ? tot - r0 : WHITV;
+    for (int i = lane; i < nv; i += WAVE) {
+      uint32_t m = wm[i];
+      while (m) {
+        const int e = __ffs(m) - 1;
+        m &= m - 1u;
+        if constexpr (DT == DSV_BF16) {
+          uint16_t* el = reinterpret_cast<uint16_t*>(&wv[i]) + e;
+          *el = (uint16_t)(__float_as_uint(penalize<DT>(bf16_bits_to_f32(*el), pres, rep)) >> 16);
+        } else {
+          float* el = reinterpret_cast<float*>(&wv[i]) + e;
+          *el = penalize<DT>(*el, pres, rep);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    slot = incl - hv - r0;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      if (bits[u]) {
+        if ((unsigned)slot < (unsigned)WHITV) v[u] = wv[slot];
+        ++slot;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // Thread t's span of chunk c in id order (NT threads tile the chunk: ids c*chunk + t*FE + [0,
 // FE)): its vectors and history bits, loaded by span_load and handed out penalised, in id
 // order, by span_each as f(i, x); -inf past the row.
@@ -366,8 +405,8 @@ __device__ __forceinline__ int64_t list_draw(const dsv_verify_args& a, bool resi
   return hit ? readlane_at((int64_t)e.id, __ffsll((long long)hit) - 1) : a.vocab - 1;
 }
 
-// What a dense row's draw needs after the chunk is known (the row merge writes it; k_final
-// reads it for the accepted row).
+// What a dense row's draw needs after the chunk is known (the row merge writes it; the request's
+// final reads it for the accepted row).
 struct DrawPlan {
   double thr, chunk_lo;  // the threshold u * mass and the mass before the chunk
   int32_t chunk, tieq;   // the chunk (-1: no mass anywhere) and the cut-key values before it
@@ -503,14 +542,19 @@ __device__ __forceinline__ void dense_plan(const KParams& P, int b, const char* 
 }
 
 // Dense draw, second part: the planned chunk in id order -- per-thread masses, the thread whose
-// mass holds the threshold, then its ids.  Returns the token (every thread).
-// PRE: the planned chunk's span is already loaded into `pre` (else loaded here).
+// mass holds the threshold, then its ids, walked by wave 0 from an LDS copy of that thread's
+// span (at most two rounds of 64 lanes).  The span's history hits are penalised in place first
+// (hv / hm: WHITV LDS slots per wave), so the per-value work is branch-free: the kept test
+// compares values (key order is value order, -0 with +0) and each vector's weights are summed
+// in float before the double total.  Returns the token (every thread).
+// PRE: the planned chunk's span is already loaded into `sp` (else loaded here).
 template <int DT, bool ALIGNED, int NT, bool PRE = false>
 __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const char* rowp, const RowSum& rs, float T,
-                                              float pres, float rep, DrawShared& sh, const Span<DT, NT>& pre) {
+                                              float pres, float rep, DrawShared& sh, Span<DT, NT>& sp, uint4* hv,
+                                              uint32_t* hm) {
   constexpr int NW = NT / WAVE;
-  constexpr int CHE = Elems<DT>::chunk, FE = CT * CV / NT * Elems<DT>::n;
-  static_assert(FE <= 64, "a thread's span fits a 64-bit mask");
+  constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk, FE = Span<DT, NT>::FE, SV = Span<DT, NT>::SV;
+  static_assert(FE <= 2 * WAVE && SV <= CV && 64 % n == 0, "a span is walked in two rounds of a wave");
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
@@ -524,29 +568,34 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
   __syncthreads();
   const int cstar = sh.chunk;
   if (cstar < 0) return V - 1;
+  if constexpr (!PRE) span_load<DT, ALIGNED, NT>(P, b, rowp, cstar, sp);
+  if (P.pbits) {
+    uint32_t bits[SV];
+#pragma unroll
+    for (int u = 0; u < SV; ++u)
+      bits[u] = (uint32_t)((u * n < 64 ? sp.blo >> (u * n) : sp.bhi >> (u * n - 64)) & ((1ull << n) - 1ull));
+    const int wid = tid / WAVE;
+    penalize_hits<DT, SV>(sp.v, bits, pres, rep, hv + wid * WHITV, hm + wid * WHITV);
+  }
   const bool use_r = sh.use_r != 0;
   const int64_t jlo = (int64_t)cstar * CHE + (int64_t)tid * FE;
-  // the span's weights stay in registers for the thread that holds the threshold
-  float w[FE];
-  uint64_t tmask = 0;  // span positions holding the cut key
+  // kept: value > vc; at the cut: value == vc (the cut key's value; -inf without a cut, where
+  // values past the row, -inf, weigh exp2(-inf) = 0 and count no tie)
+  const float vc = hist ? value_of_key<DT>(rs.vcut) : -INFINITY;
   double mt = 0.0;
-  int32_t tt = 0;
-  auto weigh = [&](int i, float x) {
-    const uint32_t k = key_of<DT>(x);
-    float wi = 0.f;
-    if (!hist || k > rs.vcut) {
-      wi = bp(x);
-    } else if (k == rs.vcut) {
-      tmask |= 1ull << i;
-      ++tt;
+  int32_t tt = 0;  // the span's values at the cut key
+#pragma unroll
+  for (int u = 0; u < SV; ++u) {
+    float su = 0.f;
+#pragma unroll
+    for (int e = 0; e < n; ++e) {
+      const float x = vec_elem<DT>(sp.v[u], e);
+      const float w = bp(x);
+      su += (!hist || x > vc) ? w : 0.f;
+      tt += (hist && x == vc) ? 1 : 0;
     }
-    w[i] = wi;
-    mt += (double)wi;
-  };
-  if constexpr (PRE)  // the planned chunk's span, loaded by the caller (cstar is that chunk)
-    span_each<DT, NT>(pre, pres, rep, weigh);
-  else
-    for_span<DT, ALIGNED, NT>(P, b, rowp, cstar, pres, rep, weigh);
+    mt += (double)su;
+  }
   int32_t tie_tot = 0;
   const int32_t tbefore = sh.tieq + block_excl_scan<NW>(tt, sh.red_i, &tie_tot);
   int32_t kept_t = 0;
@@ -571,40 +620,54 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
     const uint64_t lp = block_max_u64<NW>(w_t > 0.0 ? (uint64_t)tid + 1 : 0ull, sh.red_u);
     pt = lp ? (int)lp - 1 : -1;
   }
-  if (tid == pt) {  // the span's weights, from registers, for the wave that walks it
+  if (tid == pt) {  // the span (penalised), for the wave that walks it
 #pragma unroll
-    for (int e = 0; e < FE; ++e) sh.pw[e] = w[e];
-    sh.ptmask = tmask;
+    for (int u = 0; u < SV; ++u) sh.pv[u] = sp.v[u];
     sh.ptb = tbefore;
     sh.pick_lo = base + tlo;
   }
   __syncthreads();
   if (pt >= 0 && tid < WAVE) {
     // one id a lane in id order: kept cut-key values in rank order, the residual at the q ids,
-    // then the running sum
+    // then the running sum from the span's start
     const int lane = tid;
     const int64_t plo = (int64_t)cstar * CHE + (int64_t)pt * FE;
-    const int64_t j = plo + lane;
-    const bool live = lane < FE;
-    const uint64_t pm = sh.ptmask;
-    double Pj = live ? (double)sh.pw[lane] : 0.0;
-    if (live && ((pm >> lane) & 1ull)) {
-      const int32_t seen = __popcll(pm & ((1ull << lane) - 1ull));
-      Pj = (int64_t)sh.ptb + seen < (int64_t)rs.ktie ? P_cut : 0.0;
+    double run = sh.pick_lo;
+    int32_t seen = sh.ptb;  // cut-key values before this round
+    int64_t pick = -1, last = -1;
+#pragma unroll
+    for (int h = 0; h < (FE + WAVE - 1) / WAVE; ++h) {
+      const int i = h * WAVE + lane;
+      const bool live = i < FE;
+      float x = -INFINITY;
+      if (live) {
+        if constexpr (DT == DSV_BF16)
+          x = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(sh.pv)[i]);
+        else
+          x = reinterpret_cast<const float*>(sh.pv)[i];
+      }
+      const bool at_cut = live && hist && x == vc;
+      const uint64_t cutm = __ballot(at_cut);
+      double Pj = 0.0;
+      if (at_cut)
+        Pj = (int64_t)seen + __popcll(cutm & ((1ull << lane) - 1ull)) < (int64_t)rs.ktie ? P_cut : 0.0;
+      else if (live && (!hist || x > vc))
+        Pj = (double)bp(x);
+      seen += __popcll(cutm);
+      const int64_t j = plo + i;
+      for (uint64_t m = live ? qm : 0ull; m; m &= m - 1ull) {
+        const int l = __ffsll((long long)m) - 1;
+        if (sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
+      }
+      double wlo, whi;
+      const double tot = wave_tiles(Pj, wlo, whi);
+      const uint64_t hitj = __ballot(live && Pj > 0.0 && run + whi > thr);
+      const uint64_t pos = __ballot(live && Pj > 0.0);
+      if (pick < 0 && hitj) pick = plo + h * WAVE + (__ffsll((long long)hitj) - 1);
+      if (pos) last = plo + h * WAVE + (63 - __clzll((long long)pos));
+      run += tot;
     }
-    for (uint64_t m = live ? qm : 0ull; m; m &= m - 1ull) {
-      const int l = __ffsll((long long)m) - 1;
-      if (sh.qid[l] == j) Pj = fmax(Pj - (double)sh.qv[l], 0.0);
-    }
-    double wlo, whi;
-    wave_tiles(Pj, wlo, whi);
-    const uint64_t hitj = __ballot(live && Pj > 0.0 && sh.pick_lo + whi > thr);
-    const uint64_t pos = __ballot(live && Pj > 0.0);
-    int64_t pick = -1;
-    if (hitj)
-      pick = plo + (__ffsll((long long)hitj) - 1);
-    else if (pos)
-      pick = plo + (63 - __clzll((long long)pos));  // rounding: the last id with mass
+    if (pick < 0) pick = last;  // rounding: the last id with mass
     if (lane == 0 && pick >= 0) sh.bonus = pick;
   }
   __syncthreads();
@@ -1772,6 +1835,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   __shared__ double sd[CT / WAVE];
   __shared__ uint4 s_hv[CT / WAVE * WHITV];  // history-hit vectors of each wave
   __shared__ uint32_t s_hm[CT / WAVE * WHITV];
+  __shared__ uint32_t s_pb[CHE / 32];  // the chunk's slice of the request's history bitmap
   __shared__ int32_t s_cnt, s_nq;
   __shared__ uint32_t s_wlo;
   __shared__ float s_xtok;
@@ -1785,6 +1849,18 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   const int64_t hi = lo + CHE < V ? lo + CHE : V;
   const char* rowp = row_ptr(a, r);
   const int64_t v0 = lo / n;
+  // The request's history ids go out ahead of the chunk when the request is known without a
+  // load (dense layout) and the history is short: the chunk's slice of the history bitmap is
+  // then built while the chunk's loads are in flight.
+  constexpr int HPRE = 4;  // history ids a thread loads ahead
+  const bool hist_ahead =
+      P.softmax && P.pbits && !P.force_greedy && !a.row_offsets && a.hist_len <= HPRE * CT;
+  int32_t hid[HPRE];
+  if (hist_ahead) {
+    const int32_t* h = a.hist_ids + (int64_t)((uint32_t)r / (uint32_t)a.T) * a.hist_len;
+#pragma unroll
+    for (int k = 0; k < HPRE; ++k) hid[k] = k * CT + tid < a.hist_len ? h[k * CT + tid] : -1;
+  }
   // the chunk's loads go out first, unconditionally (addresses clamped into the row); the
   // row's request and mode are looked up under them
   uint4 v[CV];
@@ -1797,6 +1873,14 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   } else {
 #pragma unroll
     for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, false);
+  }
+  if (hist_ahead) {
+    for (int i = tid; i < CHE / 32; i += CT) s_pb[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < HPRE; ++k)
+      if (hid[k] >= lo && hid[k] < hi) atomicOr(&s_pb[(hid[k] - lo) >> 5], 1u << ((hid[k] - lo) & 31));
+    __syncthreads();
   }
   int b = 0, s = 0;
   int mode = M_GREEDY;
@@ -1845,72 +1929,28 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     // History hits (about 0.3% of the values).  Each lane copies its vectors that hold hits to
     // LDS, one lane per copied vector penalises the hit elements there, and the owners read
     // the vectors back: the registers end up penalised without a run-time register index.
-    // the n bits of vector u: word (lo + (u CT + tid) n) / 32 of the request's bitmap (lo is a
-    // multiple of 32); tokens >= vocab have no bit set, and words past the bitmap read as zeros
+    // The chunk's slice of the request's history bitmap, built from the history ids (here,
+    // unless they went out ahead of the chunk: their loads queue behind the chunk's, which the
+    // penalties wait for anyway); the workgroups of the request's first row store it for the
+    // later kernels at the end.
+    if (!hist_ahead) {
+      for (int i = tid; i < CHE / 32; i += CT) s_pb[i] = 0u;
+      __syncthreads();
+      const int32_t* h = a.hist_ids + (int64_t)b * a.hist_len;
+      for (int i = tid; i < a.hist_len; i += CT) {
+        const int64_t t = h[i];
+        if (t >= lo && t < hi) atomicOr(&s_pb[(t - lo) >> 5], 1u << ((t - lo) & 31));
+      }
+      __syncthreads();
+    }
+    // the n bits of vector u: bit (u CT + tid) n of the slice (lo is a multiple of 32)
     uint32_t bits[CV];
     {
-      const int64_t w0 = lo >> 5;
-      const auto rb = buf_rsrc(P.pbits + (int64_t)b * P.pwords + w0, (uint32_t)((P.pwords - w0) * 4));
-      const uint32_t voff = (uint32_t)((tid * n) >> 5) * 4u, sh = (uint32_t)(tid * n) & 31u;
+      const uint32_t sh = (uint32_t)(tid * n) & 31u;
 #pragma unroll
-      for (int u = 0; u < CV; ++u)
-        bits[u] = (buf_load4(rb, voff, (uint32_t)(u * CT * n / 8)) >> sh) & ((1u << n) - 1u);
+      for (int u = 0; u < CV; ++u) bits[u] = (s_pb[((u * CT + tid) * n) >> 5] >> sh) & ((1u << n) - 1u);
     }
-    int hv = 0;
-#pragma unroll
-    for (int u = 0; u < CV; ++u) hv += bits[u] != 0u;
-    // exclusive prefix and total of the hit vectors over the wave (a DPP scan)
-    const int incl = wave_incl_scan(hv);
-    const int tot = readlane<WAVE - 1>(incl);
-    uint4* wv = s_hv + wid * WHITV;
-    uint32_t* wm = s_hm + wid * WHITV;
-    // rounds of the wave's LDS slots (one unless the history is long): the round's hit vectors
-    // are copied out, one lane per vector penalises their elements, the owners read them back
-    for (int r0 = 0; r0 < tot; r0 += WHITV) {
-      int slot = incl - hv - r0;
-#pragma unroll
-      for (int u = 0; u < CV; ++u) {
-        if (bits[u]) {
-          if ((unsigned)slot < (unsigned)WHITV) {
-            wv[slot] = v[u];
-            wm[slot] = bits[u];
-          }
-          ++slot;
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int nv = tot - r0 < WHITV ? tot - r0 : WHITV;
-      for (int i = lane; i < nv; i += WAVE) {
-        uint32_t m = wm[i];
-        while (m) {
-          const int e = __ffs(m) - 1;
-          m &= m - 1u;
-          if constexpr (DT == DSV_BF16) {
-            uint16_t* el = reinterpret_cast<uint16_t*>(&wv[i]) + e;
-            *el = (uint16_t)(__float_as_uint(penalize<DT>(bf16_bits_to_f32(*el), pres, rep)) >> 16);
-          } else {
-            float* el = reinterpret_cast<float*>(&wv[i]) + e;
-            *el = penalize<DT>(*el, pres, rep);
-          }
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      slot = incl - hv - r0;
-#pragma unroll
-      for (int u = 0; u < CV; ++u) {
-        if (bits[u]) {
-          if ((unsigned)slot < (unsigned)WHITV) v[u] = wv[slot];
-          ++slot;
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    penalize_hits<DT, CV>(v, bits, pres, rep, s_hv + wid * WHITV, s_hm + wid * WHITV);
   }
 
   // the draft token's adjusted value, from the registers of the thread that holds it (read by
@@ -2181,7 +2221,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     int nb = __builtin_amdgcn_readfirstlane(s_cnt);
     if (nq > STAGE_MAX || nb > CAND_CAP) {
       // too many threads to stage, or too many admitted values: re-read the chunk
-      nb = refill_candidates<DT>(pen ? P.pbits + (int64_t)b * P.pwords : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
+      nb = refill_candidates<DT>(pen ? s_pb : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
                                  hist256, su, &s_cnt, nq > STAGE_MAX ? ((uint64_t)thr << 32) | 1ull : 0ull);
     }
     const int kk = K < nb ? K : nb;
@@ -2224,7 +2264,23 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   if (tid == 0) {
     if (tok_here) out.xtok = s_xtok;
     *st = out;
-    if (blockIdx.x == 0 && P.nuc_rows) P.nuc_rows[0] = 0;  // the merge lists full-histogram rows
+    // The row merge's per-call state, written after the last load (a store ahead of the row's
+    // parameter loads would turn those scalar loads into vector loads queued behind the
+    // chunk's): its list of full-histogram rows, and the request's merged-row count and
+    // deferred flag.  Every chunk-0 workgroup writes the same values (the merge runs after the
+    // chunk pass); a request without rows here is left to k_final.
+    if (c == 0) {
+      if (P.nuc_rows) P.nuc_rows[0] = 0;
+      if (P.req_cnt) {
+        P.req_cnt[b] = 0u;
+        P.deferred[b] = 1u;
+      }
+    }
+  }
+  if (pen && s == 0) {  // the request's history bitmap for the later kernels (its first row)
+    uint32_t* dst = P.pbits + (int64_t)b * P.pwords + (lo >> 5);
+    const int words = (int)((hi - lo + 31) >> 5);
+    for (int i = tid; i < words; i += CT) dst[i] = s_pb[i];
   }
 }
 
@@ -2267,101 +2323,6 @@ __device__ __forceinline__ void defer_nucleus(const KParams& P, int64_t r, float
     ro->rs = rs;
     ro->ok = 0;
     ro->nuc = 1;
-  }
-}
-
-// ---------------------------------------------------------------------------------------
-// k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0)
-// ---------------------------------------------------------------------------------------
-template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
-  __shared__ union {  // a row merges as a support list or as a nucleus, never both
-    MergeShared ms;
-    NucMergeShared ns;
-  } mu;
-  MergeShared& ms = mu.ms;
-  NucMergeShared& ns = mu.ns;
-  __shared__ DrawShared ds;
-  __shared__ RowPre pre;
-  __shared__ RowOut ro;
-  const dsv_verify_args& a = P.a;
-  const int64_t r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-  int b, s;
-  if (!row_request(a, r, b, s)) {
-    if (tid == 0) {
-      P.rowsum[r].mode = M_SKIP;
-      P.step_ok[r] = 0;
-    }
-    return;
-  }
-  const int mode = row_mode(a, b, 0);
-  const float T = a.temperatures[b];
-  const int cap = req_cap(a, b);
-  const bool resid = s < cap - 1;  // the row tests draft s+1, and ends the prefix when it is rejected
-  const bool tests = a.candidates != nullptr && resid;
-  // one round of reads before the merge: the chunk statistics (wave 0), the draft token, its
-  // coin and q lanes, and for dense rows the adjusted logits at the q ids (wave 1)
-  if (tid < WAVE) {
-    if (lane < P.C) pre.cs[lane] = P.cstat[r * P.C + lane];
-    if (lane == 0) {
-      pre.tok = tests ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
-      pre.u = tests ? a.uniforms[(int64_t)b * (a.T - 1) + s] : 0.f;
-      pre.uf = a.candidates ? a.uniform_final[b] : 0.f;
-      pre.top_p = a.top_ps ? a.top_ps[b] : 1.f;
-      pre.min_p = a.min_ps ? a.min_ps[b] : 0.f;
-      pre.top_k = a.top_ks[b];
-      pre.pres = P.pbits && a.presence ? a.presence[b] : 0.f;
-      pre.rep = P.pbits && a.repetition ? a.repetition[b] : 1.f;
-    }
-  } else if (tid < 2 * WAVE) {
-    fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds);
-  }
-  __syncthreads();
-  if (mode == M_HIST) {
-    if constexpr (DT == DSV_BF16)
-      merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &ro);
-    else
-      defer_nucleus<DT>(P, r, T, pre, &ro);
-  } else {
-    merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &ro);
-  }
-  __syncthreads();
-  // the bonus token this row gives when it is the request's accepted length (k_final picks it);
-  // the target-distribution entry draws none
-  const RowSum& rs = ro.rs;  // (read from LDS where used: fewer live registers)
-  int64_t bonus = 0;
-  if (!a.candidates) {
-  } else if (rs.mode == M_GREEDY) {
-    bonus = rs.argmax;
-  } else if (rs.mode == M_LIST) {
-    bonus = tid < WAVE ? list_draw(a, resid, pre.uf, ds) : 0;
-  } else if (rs.flags & FLAG_FULL_HIST) {
-    bonus = BONUS_LATER;
-  } else {
-    // the chunk and threshold; k_final scans the chunk when this row is the accepted one
-    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, pre.pres, pre.rep, resid, pre.uf, ds, true);
-    // the plan, stored by waves 1 and 2: a wave's later waits cover only its own stores, so the
-    // row's stores (wave 0, below) do not queue behind these
-    static_assert(QMAX <= WAVE && CT >= 3 * WAVE, "plan stores by waves 1 and 2");
-    DrawPlan* pl = P.plans + r;
-    const int lq = (int)threadIdx.x - WAVE;
-    if (lq >= 0 && lq < QMAX) pl->qd[lq] = ds.qd[lq];
-    if (threadIdx.x == 2 * WAVE) {
-      pl->thr = ds.thr;
-      pl->chunk_lo = ds.chunk_lo;
-      pl->chunk = ds.chunk;
-      pl->tieq = ds.tieq;
-      pl->use_r = ds.use_r;
-      pl->pad = 0;
-    }
-    bonus = BONUS_PLAN - 1 - ds.chunk;  // (the chunk, for k_final's early loads)
-  }
-  if (threadIdx.x == 0) {
-    P.rowsum[r] = rs;
-    P.step_ok[r] = ro.ok;
-    if (a.candidates) P.rbonus[r] = bonus;
-    if (ro.nuc) P.nuc_rows[1 + atomicAdd(&P.nuc_rows[0], 1)] = (int32_t)r;
   }
 }
 
@@ -2440,8 +2401,167 @@ __device__ __forceinline__ void write_outputs_at(const dsv_verify_args& a, int b
 }
 
 // ---------------------------------------------------------------------------------------
-// k_final: outputs, one workgroup per request -- the accepted length a, and the bonus token of
-// row a (drawn by the row merge, or here for rows the full histogram settled)
+// k_merge: one workgroup per row (the rank selection uses all threads, the rest wave 0).  The
+// row's decision and bonus token are stored device-coherently, then the row bumps its request's
+// counter; the workgroup that completes the count (every row of the request merged) writes the
+// request's outputs when the row merges drew its token.  Requests whose accepted row is dense
+// (the draw planned) or decided by the full histogram stay deferred: k_final resolves them.
+// ---------------------------------------------------------------------------------------
+// The request's outputs from its rows' decisions, when the row merges drew the token: the
+// accepted length a is the first row whose draft was rejected (the last row ends every prefix),
+// and row a's merge drew the bonus token (support-list and greedy rows).  A dense row at a
+// (its draw planned: a scan of one chunk) or a full-histogram row before it leaves the request
+// to k_final.
+__device__ __forceinline__ void final_rows(const KParams& P, int b, DrawShared& sh) {
+  const dsv_verify_args& a = P.a;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  const int64_t row0 = request_row0(a, b);
+  const int cap = req_cap(a, b);
+  if (tid < WAVE) {
+    int acc = cap - 1;
+    int64_t drawn = 0;
+    for (int s0 = 0; s0 < cap; s0 += WAVE) {
+      const int s = s0 + lane;
+      const int32_t ok = s < cap - 1 ? ld_dev(P.step_ok + row0 + s) : 0;
+      const int64_t rb = s < cap ? ld_dev(P.rbonus + row0 + s) : 0;
+      const uint64_t end = __ballot(s < cap && ok == 0);
+      if (end) {
+        const int l = __ffsll((long long)end) - 1;
+        acc = s0 + l;
+        drawn = readlane_at(rb, l);
+        break;
+      }
+    }
+    if (tid == 0) {
+      sh.acc = acc;
+      sh.bonus = drawn;
+    }
+  }
+  __syncthreads();
+  const int acc = sh.acc;
+  const int64_t bonus = sh.bonus;
+  if (bonus <= BONUS_PLAN) {
+    // a planned draw: k_final scans the chunk; the accepted length and the chunk go with the
+    // deferred flag (2 + a, chunk + 1 in the top byte), so that k_final loads them at once
+    const int cpl = (int)(BONUS_PLAN - 1 - bonus);
+    if (tid == 0 && acc + 2 < DEFER_ACC) P.deferred[b] = ((uint32_t)(cpl + 1) << 24) | (uint32_t)(acc + 2);
+    return;
+  }
+  if (bonus < 0) return;  // (BONUS_LATER: k_final)
+  write_outputs(a, b, acc, bonus);
+  if (tid == 0) P.deferred[b] = 0u;
+}
+
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
+  __shared__ union {  // a row merges as a support list or as a nucleus, never both
+    MergeShared ms;
+    NucMergeShared ns;
+  } mu;
+  MergeShared& ms = mu.ms;
+  NucMergeShared& ns = mu.ns;
+  __shared__ DrawShared ds;
+  __shared__ RowPre pre;
+  __shared__ RowOut ro;
+  __shared__ uint32_t s_last;
+  const dsv_verify_args& a = P.a;
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+  int b, s;
+  if (!row_request(a, r, b, s)) {
+    if (tid == 0) {
+      P.rowsum[r].mode = M_SKIP;
+      P.step_ok[r] = 0;
+    }
+    return;
+  }
+  const int mode = row_mode(a, b, 0);
+  const float T = a.temperatures[b];
+  const int cap = req_cap(a, b);
+  const bool resid = s < cap - 1;  // the row tests draft s+1, and ends the prefix when it is rejected
+  const bool tests = a.candidates != nullptr && resid;
+  // one round of reads before the merge: the chunk statistics (wave 0), the draft token, its
+  // coin and q lanes, and for dense rows the adjusted logits at the q ids (wave 1)
+  if (tid < WAVE) {
+    if (lane < P.C) pre.cs[lane] = P.cstat[r * P.C + lane];
+    if (lane == 0) {
+      pre.tok = tests ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
+      pre.u = tests ? a.uniforms[(int64_t)b * (a.T - 1) + s] : 0.f;
+      pre.uf = a.candidates ? a.uniform_final[b] : 0.f;
+      pre.top_p = a.top_ps ? a.top_ps[b] : 1.f;
+      pre.min_p = a.min_ps ? a.min_ps[b] : 0.f;
+      pre.top_k = a.top_ks[b];
+      pre.pres = P.pbits && a.presence ? a.presence[b] : 0.f;
+      pre.rep = P.pbits && a.repetition ? a.repetition[b] : 1.f;
+    }
+  } else if (tid < 2 * WAVE) {
+    fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds);
+  }
+  __syncthreads();
+  if (mode == M_HIST) {
+    if constexpr (DT == DSV_BF16)
+      merge_nucleus<DT>(P, r, b, s, T, ns, ds, pre, &ro);
+    else
+      defer_nucleus<DT>(P, r, T, pre, &ro);
+  } else {
+    merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &ro);
+  }
+  __syncthreads();
+  // The bonus token this row gives when it is the request's accepted length: none for a row
+  // whose draft was accepted before the last row (the accepted length lies beyond it), nor for
+  // the target-distribution entry.
+  const RowSum& rs = ro.rs;  // (read from LDS where used: fewer live registers)
+  int64_t bonus = 0;
+  if (!a.candidates || (resid && ro.ok)) {
+  } else if (rs.mode == M_GREEDY) {
+    bonus = rs.argmax;
+  } else if (rs.mode == M_LIST) {
+    bonus = tid < WAVE ? list_draw(a, resid, pre.uf, ds) : 0;
+  } else if (rs.flags & FLAG_FULL_HIST) {
+    bonus = BONUS_LATER;
+  } else {
+    // dense rows: the chunk and threshold; k_final scans the chunk when this row is the accepted
+    // one.  The plan, stored by waves 1 and 2: a wave's later waits cover only its own stores,
+    // so the row's stores (wave 0, below) do not queue behind these.
+    dense_plan<DT, ALIGNED, CT>(P, b, row_ptr(a, r), rs, T, pre.pres, pre.rep, resid, pre.uf, ds, true);
+    static_assert(QMAX <= WAVE && CT >= 3 * WAVE, "plan stores by waves 1 and 2");
+    DrawPlan* pl = P.plans + r;
+    const int lq = (int)threadIdx.x - WAVE;
+    if (lq >= 0 && lq < QMAX) pl->qd[lq] = ds.qd[lq];
+    if (threadIdx.x == 2 * WAVE) {
+      pl->thr = ds.thr;
+      pl->chunk_lo = ds.chunk_lo;
+      pl->chunk = ds.chunk;
+      pl->tieq = ds.tieq;
+      pl->use_r = ds.use_r;
+      pl->pad = 0;
+    }
+    bonus = BONUS_PLAN - 1 - ds.chunk;  // (the chunk, for k_final's early loads)
+  }
+  if (tid == 0) {
+    P.rowsum[r] = rs;
+    st_dev(P.step_ok + r, ro.ok);
+    if (a.candidates) st_dev(P.rbonus + r, bonus);
+    if (ro.nuc) {
+      const int32_t at = atomicAdd(&P.nuc_rows[0], 1);
+      if (at < a.rows) P.nuc_rows[1 + at] = (int32_t)r;
+    }
+  }
+  if (!a.candidates) return;  // (the target-distribution entry writes no outputs)
+  // the row's decision and token have reached the coherence point before the row is counted;
+  // the workgroup that completes the request's count writes the request's outputs
+  if (tid == 0) {
+    publish_wait();
+    s_last = atomicAdd(P.req_cnt + b, 1u) == (uint32_t)(cap - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_last) final_rows(P, b, ds);
+}
+
+// ---------------------------------------------------------------------------------------
+// k_final: outputs, one workgroup per request the row merge left (only_deferred; else every
+// request) -- the accepted length a, and the bonus token of row a (drawn by the row merge, or
+// here for rows the full histogram settled)
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(FCT) void k_final(KParams P) {
@@ -2450,8 +2570,18 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   extern __shared__ __align__(16) unsigned char dyn[];  // (final_nuc: the full-histogram LDS)
   __shared__ DrawShared sh;
   __shared__ RowOut fro;  // a full-histogram row resolved here
+  __shared__ uint4 s_hv[FCT / WAVE * WHITV];  // history-hit slots of the draw
+  __shared__ uint32_t s_hm[FCT / WAVE * WHITV];
   const dsv_verify_args& a = P.a;
   const int b = blockIdx.x;
+  const uint32_t dfl = P.only_deferred ? P.deferred[b] : 1u;
+  if (dfl == 0u) {
+    // the row merge wrote the request's outputs -- if the request has rows (its deferred flag
+    // is set by the chunk pass of its own rows; one without is decided here)
+    int b0 = -1, s0 = -1;
+    const int64_t r0 = request_row0(a, b);
+    if (r0 >= 0 && r0 < a.rows && row_request(a, r0, b0, s0) && b0 == b && s0 == 0) return;
+  }
   const int tid = threadIdx.x, lane = tid & (WAVE - 1);
   const int64_t V = a.vocab;
   int64_t row0 = request_row0(a, b);
@@ -2495,9 +2625,16 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     }
     __syncthreads();
   };
-  scan(0);
-  int acc = sh.acc;
-  int64_t bonus = sh.bonus;
+  int acc;
+  int64_t bonus;
+  if (dfl >= 2u) {  // the row merge's scan: a planned draw at a known accepted length
+    acc = (int)(dfl & (DEFER_ACC - 1)) - 2;
+    bonus = BONUS_PLAN - 1 - ((int64_t)(dfl >> 24) - 1);
+  } else {
+    scan(0);
+    acc = sh.acc;
+    bonus = sh.bonus;
+  }
   bool own = false;  // the accepted row's RowSum is fro.rs (resolved here)
   if (P.final_nuc) {
     // A row whose cut the merge's windows did not settle carries a placeholder decision (0):
@@ -2555,7 +2692,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
       if (lane == 0) sh.qmask = qm;
     }
     const RowSum rs = P.rowsum[rstar];
-    bonus = dense_pick<DT, ALIGNED, FCT, true>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh, sp);
+    bonus = dense_pick<DT, ALIGNED, FCT, true>(P, b, row_ptr(a, rstar), rs, T, pres, rep, sh, sp, s_hv, s_hm);
   } else if (bonus == BONUS_LATER) {
     const int64_t rstar = row0 + acc;
     const RowSum rs = own ? fro.rs : P.rowsum[rstar];
@@ -2583,8 +2720,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
     __syncthreads();
     dense_plan<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, resid, uf, sh);
     Span<DT, FCT> unused;
-    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh, unused);
-    (void)CHE;
+    bonus = dense_pick<DT, ALIGNED, FCT>(P, b, rowp, rs, T, pres, rep, sh, unused, s_hv, s_hm);
   }
   write_outputs_at(a, b, acc, bonus, og, FCT - WAVE, plen);
 }
@@ -2794,7 +2930,7 @@ using namespace dsv;
 static int64_t align_up(int64_t x, int64_t al) { return (x + al - 1) / al * al; }
 
 struct WsLayout {
-  int64_t rowsum, lists, cstat, cand, hpart, nhist, nuc, rbonus, rties, plans, step_ok, pbits, total;
+  int64_t rowsum, lists, cstat, cand, hpart, nhist, nuc, rbonus, rties, plans, step_ok, req_cnt, deferred, pbits, total;
 };
 static void launch_chunk(const KParams& P, int dtype, unsigned grid, hipStream_t stream) {
   if (dtype == DSV_BF16) {
@@ -2834,6 +2970,8 @@ static WsLayout ws_layout(int64_t rows, int32_t bs, int64_t vocab, int dtype, in
   take(w.rties, rows * NCHK * 4);
   take(w.plans, rows * (int64_t)sizeof(DrawPlan));
   take(w.step_ok, rows * 4);
+  take(w.req_cnt, (int64_t)bs * 4);
+  take(w.deferred, (int64_t)bs * 4);
   take(w.pbits, history ? (int64_t)bs * pen_words(vocab) * 4 : 0);
   w.total = o;
   return w;
@@ -2907,6 +3045,8 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   P.rbonus = reinterpret_cast<int64_t*>(ws + w.rbonus);
   P.rties = reinterpret_cast<int32_t*>(ws + w.rties);
   P.plans = reinterpret_cast<DrawPlan*>(ws + w.plans);
+  P.req_cnt = reinterpret_cast<uint32_t*>(ws + w.req_cnt);
+  P.deferred = reinterpret_cast<uint32_t*>(ws + w.deferred);
   P.step_ok = reinterpret_cast<int32_t*>(ws + w.step_ok);
   P.pbits = history ? reinterpret_cast<uint32_t*>(ws + w.pbits) : nullptr;
   P.pwords = pen_words(a.vocab);
@@ -2921,11 +3061,6 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
 // The row stage: history bitmaps, the chunk pass, the row merge, and the full-histogram rows.
 static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipStream_t stream) {
   const dsv_verify_args& a = P.a;
-  if (P.pbits) {
-    const unsigned spans = (unsigned)((P.pwords + PREP_WORDS - 1) / PREP_WORDS);
-    hipLaunchKernelGGL(k_prep, dim3(spans, (unsigned)a.bs), dim3(BCT), 0, stream, P);
-    DSV_CHECK_LAUNCH("k_prep");
-  }
   if (profile && g_prof_start && g_prof_stop && hipEventRecord(g_prof_start, stream) != hipSuccess)
     DSV_FAIL(DSV_ERR_LAUNCH, "dsv_verify: cannot record the profiling start event");
   launch_chunk(P, a.logits_dtype, (unsigned)(a.rows * P.C), stream);
@@ -2986,11 +3121,18 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   // with k_final in the launch, each request's workgroup resolves its own full-histogram rows
   // (usually none: the merge's windows settle the cut) and no k_nuc launch is needed
   P.final_nuc = (stages & 4) && hist_possible ? 1 : 0;
+  // The row merge writes the outputs of the requests whose accepted row drew its token there
+  // (greedy and support-list rows).  k_final takes the rest: requests whose accepted row is a
+  // dense row (unfiltered or nucleus: only when a top-k above the support list, or no filter,
+  // can occur), and requests whose ragged row offsets leave rows outside the logits.
+  const bool all_greedy = a.any_greedy && a.max_top_k <= 1;
+  const bool dense_possible = !all_greedy && (!a.filter || a.max_top_k > DSV_LIST_K);
+  P.only_deferred = (stages & 1) ? 1 : 0;
   if (stages & 1) {
     const int rc2 = launch_rows(P, hist_possible, true, stream);
     if (rc2 != DSV_OK) return rc2;
   }
-  if (stages & 4) {
+  if ((stages & 4) && (!(stages & 1) || dense_possible || a.row_offsets)) {
     const size_t lds = !P.final_nuc ? 0 : a.logits_dtype == DSV_BF16 ? (size_t)HIST_WORDS * 4 : sizeof(F32NucLds);
     auto go = [&](const void* fn, auto kernel) {
       if (lds) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
