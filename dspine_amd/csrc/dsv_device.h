@@ -265,6 +265,24 @@ __device__ __forceinline__ uint32_t wave_first_key(uint32_t lo, uint32_t hi, F&&
   return lo;
 }
 
+// wave_first_key with a guess of the answer: one round over the 64 keys from guess - 32, which
+// settles it when the boundary lies among them (the usual case for a guess from the closed form
+// of the predicate); otherwise the search goes on over the side of that round that holds it.
+template <class F>
+__device__ __forceinline__ uint32_t wave_first_key_near(uint32_t lo, uint32_t hi, uint32_t guess, F&& pred) {
+  if (lo >= hi) return lo;
+  const uint32_t lane = threadIdx.x & (WAVE - 1);
+  uint32_t g0 = guess > lo + WAVE / 2 ? guess - WAVE / 2 : lo;
+  if (g0 >= hi) g0 = hi - 1;
+  const uint32_t k = g0 + lane;
+  const bool valid = k < hi;
+  const uint64_t yes = __ballot(valid && pred(k));
+  if (yes & 1ull) return wave_first_key(lo, g0, pred);  // key g0 holds: the boundary is at or below it
+  if (yes) return g0 + (uint32_t)(__ffsll((long long)yes) - 1);
+  const uint32_t past = g0 + (uint32_t)(64 - __clzll((long long)__ballot(valid)));  // past the last key tried
+  return past >= hi ? hi : wave_first_key(past, hi, pred);
+}
+
 // Element e (a run-time index) of a vector, and its replacement: branch-free, through the two
 // 64-bit halves of the vector.
 template <int DT>

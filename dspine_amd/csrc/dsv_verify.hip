@@ -955,10 +955,14 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   if (tid < WAVE) {
     const double eps = (Z * (double)invZ - (double)top_p - 1e-6) / (double)a.vocab;
     uint32_t kb = 0x80u;  // the lowest finite key: no floor
-    if (eps > 0.0 && kmax >= 0x80u)  // smallest key with p >= eps (p is non-decreasing in the key)
-      kb = wave_first_key(0x80u, kmax, [&](uint32_t k) {
+    if (eps > 0.0 && kmax >= 0x80u) {  // smallest key with p >= eps (p is non-decreasing in the key)
+      // the closed form's key, x = T (m_f + ln(eps Z)), as the search's guess
+      const float lnp = (__builtin_amdgcn_logf((float)eps) - __builtin_amdgcn_logf(invZ)) * 0.693147180559945309f;
+      const uint32_t guess = key_of<DT>(T * (m_f + lnp));
+      kb = wave_first_key_near(0x80u, kmax, guess, [&](uint32_t k) {
         return (double)prob_of(value_of_key<DT>(k), T, m_f, invZ) >= eps;
       });
+    }
     if (lane == 0) {
       sh.kb_row = kb;
       sh.xtok = (tok >= 0 && tok < a.vocab) ? cs[tok / Elems<DT>::chunk].xtok : -INFINITY;
@@ -995,8 +999,20 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   const uint32_t kscan = sh.kb_row > kcov ? sh.kb_row : kcov;
   const int W = (int)(kmax - kscan) + 1;  // <= HWIN: the max's own chunk window ends at kmax
   const bool keep_hc = W <= HC_KEYS && C <= 8;  // the per-chunk counts serve the bonus masses too
+  // With the window in the per-chunk tables, the counts' unused tail holds each key's exp terms,
+  // computed once: e^(x/T - m_f) (p = that * invZ, as prob_of) and 2^(x c2 - M c2) (the bonus
+  // draw's P = that * scale, as BonusP) -- the same floats as the direct formulas.
+  float* const ptab = reinterpret_cast<float*>(sh.h + HC_KEYS);
+  float* const etab = reinterpret_cast<float*>(sh.h + 2 * HC_KEYS);
+  static_assert(3 * HC_KEYS <= HWIN, "exp tables in the counts' tail");
+  const float c2b = log2e_over(T), mc2b = value_of_key<DT>(kmax) * c2b;
   for (int q = tid; q < W; q += CT) {
     const uint32_t k = kmax - (uint32_t)q;
+    if (keep_hc) {
+      const float x = value_of_key<DT>(k);
+      ptab[q] = expf(x / T - m_f);
+      etab[q] = __builtin_amdgcn_exp2f(fmaf(x, c2b, -mc2b));
+    }
     uint32_t cnt = 0;
     for (int c0 = 0; c0 < C; c0 += 8) {  // eight chunks' words loaded together (in-bounds addresses)
       uint32_t word[8], o[8];
@@ -1028,7 +1044,8 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   for (int q = wid * SL + lane; q < q_end; q += WAVE) {
     const uint32_t cnt = sh.h[q];
     if (!cnt) continue;
-    mt += (double)cnt * (double)prob_of(value_of_key<DT>(kmax - (uint32_t)q), T, m_f, invZ);
+    const float p = keep_hc ? ptab[q] * invZ : prob_of(value_of_key<DT>(kmax - (uint32_t)q), T, m_f, invZ);
+    mt += (double)cnt * (double)p;
     cw += cnt;
   }
   mt = wave_sum(mt);
@@ -1060,7 +1077,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       const uint32_t cnt = q < q_end ? sh.h[q] : 0u;
       if (__ballot(cnt != 0u) == 0ull) continue;
       const uint32_t k = kmax - (uint32_t)q;
-      const float p = cnt ? prob_of(value_of_key<DT>(k), T, m_f, invZ) : 0.f;
+      const float p = !cnt ? 0.f : keep_hc ? ptab[q] * invZ : prob_of(value_of_key<DT>(k), T, m_f, invZ);
       double lo_m, hi_m;
       const double it_m = wave_tiles((double)cnt * (double)p, lo_m, hi_m);
       int64_t c_excl = wave_incl_scan((int64_t)cnt);
@@ -1178,7 +1195,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
       for (int q = lane; q < W; q += WAVE) {
         const uint32_t k = kmax - (uint32_t)q;
         const uint32_t cnt = sh.hc[c * HC_KEYS + q];
-        if (k > rs.vcut && cnt) mc += (double)cnt * (double)bp(value_of_key<DT>(k));
+        if (k > rs.vcut && cnt) mc += (double)cnt * (double)(etab[q] * bp.scale);
         if (k == rs.vcut) tc = (int32_t)cnt;
       }
       mc = wave_sum(mc);
@@ -1926,9 +1943,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
   }
 
   if (pen) {
-    // History hits (about 0.3% of the values).  Each lane copies its vectors that hold hits to
-    // LDS, one lane per copied vector penalises the hit elements there, and the owners read
-    // the vectors back: the registers end up penalised without a run-time register index.
+    // History hits (about 0.3% of the values), penalised in place by penalize_hits.
     // The chunk's slice of the request's history bitmap, built from the history ids (here,
     // unless they went out ahead of the chunk: their loads queue behind the chunk's, which the
     // penalties wait for anyway); the workgroups of the request's first row store it for the
@@ -2060,7 +2075,9 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
           const float floor_e = 2.f * (1.f - top_p) / (float)V * (float)(out.s * (double)C);
           if (floor_e > 0.f && kmax > 0x80u) {
             const float c2 = log2e_over(T);
-            kb = wave_first_key(0x80u, kmax, [&](uint32_t k) {
+            // the closed form's key, x = m + log2(floor) / c2, as the search's guess
+            const uint32_t guess = key_of<DT>(out.m + __builtin_amdgcn_logf(floor_e) / c2);
+            kb = wave_first_key_near(0x80u, kmax, guess, [&](uint32_t k) {
               return __builtin_amdgcn_exp2f((value_of_key<DT>(k) - out.m) * c2) >= floor_e;
             });
           }
