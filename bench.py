@@ -44,15 +44,16 @@ ROTATE_BYTES = 661 << 20  # logits copies read in turn: more than twice the 256 
 def verify_bytes(bs, T, V, K, hist_len, esize, rows=None):
     """(whole step, chunk pass) algorithmic HBM bytes of a fused verify step.  The step: one
     read of every verified logit row plus the small per-request inputs and outputs.  The chunk
-    pass k_chunk: the logits and each request's history bitmap (V/8 bytes, read once per
-    request; its rows find it in L2) -- its per-chunk statistics, candidates and value counts
-    are workspace it writes for the merge (counted in the traffic figure, not here)."""
+    pass k_chunk: the logits and each request's history ids (read once per request; the
+    request's other chunks find them in L2) -- its per-chunk statistics, candidates, value
+    counts and the requests' history bitmaps are workspace it writes for the later kernels
+    (counted in the traffic figure, not here)."""
     rows = bs * T if rows is None else rows
     logits = rows * V * esize
     small_in = (bs * hist_len * 4 + bs * (T - 1) * K * (8 + 4) + bs * T * 8 + bs * (T - 1) * 4 + bs * 4
                 + bs * 4 * 4 + bs * 4 + bs * T * 4)
     outputs = bs * (4 + 4 + 8 + 4) + bs * T * 8 + bs * T * 4
-    chunk_pass = logits + (bs * ((V + 31) // 32) * 4 if hist_len else 0)
+    chunk_pass = logits + bs * hist_len * 4
     return logits + small_in + outputs, chunk_pass
 
 
