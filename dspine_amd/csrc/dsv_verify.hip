@@ -690,6 +690,7 @@ struct RowOut {
 struct MergeShared {
   uint64_t buf[NCHK * DSV_LIST_K];
   uint64_t top[DSV_LIST_K];
+  uint64_t cmin[NCHK];  // each chunk's smallest candidate
   int32_t off[NCHK + 1];
 };
 
@@ -711,6 +712,7 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
       }
       ms.off[C] = o;
     }
+    if (tid < C) ms.cmin[tid] = ~0ull;
     // every chunk's candidate slots, loaded together (in-bounds addresses, unused slots dropped)
     const int kc = P.kcand, nslot = C * kc;
     const uint64_t* src = P.cand + r * (int64_t)nslot;
@@ -728,17 +730,43 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
         const int idx = base + u * CT + tid;
         if (idx < nslot) {
           const int c = idx / kc, i = idx - c * kc;
-          if (i < ms.off[c + 1] - ms.off[c]) ms.buf[ms.off[c] + i] = v[u];
+          if (i < ms.off[c + 1] - ms.off[c]) {
+            ms.buf[ms.off[c] + i] = v[u];
+            atomicMin(&ms.cmin[c], (unsigned long long)v[u]);
+          }
         }
       }
     }
     __syncthreads();
     const int n_all = ms.off[C];
-    // rank of each candidate among the row's candidates (values are distinct)
-    for (int i = tid; i < n_all; i += CT) {
+    // A chunk whose list holds K candidates holds its K largest values, so the row's K largest
+    // are at or above that list's smallest: the largest such minimum bounds them from below.
+    // The candidates at or above it are compacted to the front of the buffer (values are
+    // distinct) and ranked among themselves.
+    uint64_t lb = 0ull;
+    for (int c = 0; c < C; ++c)
+      if (ms.off[c + 1] - ms.off[c] >= K && ms.cmin[c] > lb) lb = ms.cmin[c];
+    constexpr int PER = NCHK * DSV_LIST_K / CT;
+    uint64_t keep_v[PER];
+    int nk = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = u * CT + tid;
+      keep_v[u] = i < n_all ? ms.buf[i] : 0ull;
+      nk += (i < n_all && keep_v[u] >= lb) ? 1 : 0;
+    }
+    int n_keep = 0;
+    int at = block_excl_scan<CT / WAVE>(nk, ds.red_i, &n_keep);  // (its barriers follow every read)
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = u * CT + tid;
+      if (i < n_all && keep_v[u] >= lb) ms.buf[at++] = keep_v[u];
+    }
+    __syncthreads();
+    for (int i = tid; i < n_keep; i += CT) {
       const uint64_t v = ms.buf[i];
       int rank = 0;
-      for (int j = 0; j < n_all; ++j) rank += ms.buf[j] > v;
+      for (int j = 0; j < n_keep; ++j) rank += ms.buf[j] > v;
       if (rank < K) ms.top[rank] = v;
     }
     __syncthreads();
