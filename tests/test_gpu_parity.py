@@ -244,6 +244,27 @@ def test_verify_small_mixed(device, seed, dtype, penalties):
     assert len(near) <= 1
 
 
+@pytest.mark.parametrize("mix", ["greedy", "lists", "unfiltered", "nucleus", "lists_and_greedy"])
+def test_verify_launch_sets(device, mix):
+    """Batches of one kind of request, which launch different kernel sets: greedy-only and
+    support-list-only batches finish every request in the row merge (no k_final launch);
+    unfiltered and nucleus batches leave their dense accepted rows to k_final."""
+    batch = _small_batch(40 + len(mix), dtype=torch.bfloat16, penalties=True)
+    bs = batch["candidates"].shape[0]
+    half = bs // 2
+    temps, ks, ps = {
+        "greedy": ([0.0] * bs, [0] * bs, [1.0] * bs),
+        "lists": ([0.8] * bs, [20] * bs, [0.9] * bs),
+        "unfiltered": ([0.8] * bs, [0] * bs, [1.0] * bs),
+        "nucleus": ([0.8] * bs, [0] * bs, [0.9] * bs),
+        "lists_and_greedy": ([0.0] * half + [1.0] * (bs - half), [0] * half + [5] * (bs - half), [1.0] * bs),
+    }[mix]
+    batch["info"] = W.sampling_info(temps, ks, ps)
+    gpu = run_gpu_verify(batch, device)
+    ref = run_oracle(batch, list(range(bs)))
+    assert len(compare_outputs(gpu, ref, range(bs), f"launch set {mix}")) <= 1
+
+
 @pytest.mark.parametrize("seed", [5, 6])
 def test_verify_page_table_edges(device, seed):
     """KV slots where the committed positions run past the page table's columns (-1 there, as
