@@ -58,7 +58,7 @@ constexpr int NUC_SLICE = 65528;     // values per 16-bit histogram pass (no cou
 constexpr int HWIN = 4096;           // keys of a chunk's value-count window (nucleus rows)
 constexpr uint32_t WIN_EMPTY = 0x10000u;
 constexpr uint32_t KX_UNKNOWN = 0xFFFFFFFFu;  // ChunkStat::kx when the chunk did not track it
-constexpr int STAGE_MAX = 96;        // list rows: threads whose vectors fit the LDS stage
+constexpr int STAGE_VECS = 256;      // list rows: vectors (those reaching the admission bound) the LDS stage holds
 constexpr int WHITV = 64;            // LDS slots of a wave for vectors holding history hits
 constexpr int NCHK = 32;             // most chunks a row may have (per-row chunk arrays)
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels

@@ -1867,19 +1867,19 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
 // k_chunk: one pass over a 20480-value (bf16) / 10240-value (fp32) chunk held in registers
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT) void k_chunk(KParams P) {
+__global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_chunk(KParams P) {
   constexpr int n = Elems<DT>::n;
   constexpr int CHE = Elems<DT>::chunk;
-  __shared__ uint64_t cbuf[CAND_CAP];
-  __shared__ uint32_t hist256[256];
-  // nucleus rows: 32-bit value counts of the window; list rows: staged vectors
+  // nucleus rows: 32-bit value counts of the window; list rows: staged vectors, their ids, the
+  // candidates and the radix counts (below); first the penalty step's slots (below)
   __shared__ uint4 big[HWIN / 4];
-  static_assert(STAGE_MAX * CV <= HWIN / 4, "list stage exceeds the window buffer");
-  __shared__ int16_t s_qtid[STAGE_MAX];
   __shared__ uint64_t su[CT / WAVE];
   __shared__ double sd[CT / WAVE];
-  __shared__ uint4 s_hv[CT / WAVE * WHITV];  // history-hit vectors of each wave
-  __shared__ uint32_t s_hm[CT / WAVE * WHITV];
+  // history-hit vectors and masks of each wave: the penalty step is done, in every wave,
+  // before the barriers of the chunk's max, which precede every other use of big
+  uint4* const s_hv = big;
+  uint32_t* const s_hm = reinterpret_cast<uint32_t*>(big + CT / WAVE * WHITV);
+  static_assert(CT / WAVE * WHITV * 5 / 4 <= HWIN / 4, "penalty slots exceed the window buffer");
   __shared__ uint32_t s_pb[CHE / 32];  // the chunk's slice of the request's history bitmap
   __shared__ int32_t s_cnt, s_nq;
   __shared__ uint32_t s_wlo;
@@ -2204,40 +2204,95 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     uint32_t thr = 0xFFFFFFFFu;
 #pragma unroll
     for (int i = 0; i < CT / WAVE; ++i) thr = (uint32_t)su[i] < thr ? (uint32_t)su[i] : thr;
-    // only the threads whose max reaches the bound hold admitted values: they stage their
-    // vectors in LDS and the whole workgroup scans them
-    uint4* stage = reinterpret_cast<uint4*>(big);
+    // A positive bound (the usual case): a value reaches it iff its bits, as a signed integer
+    // of the value's width, reach the bound's value bits (negative values are negative
+    // integers); its key is then bits | the sign bit.
+    constexpr uint32_t SIGNB = DT == DSV_BF16 ? 0x8000u : 0x80000000u;
+    const bool pos_thr = thr > SIGNB;
+    const int t0 = (int)(thr - SIGNB);
+    auto sbits = [&](const uint4& w, int e) -> int {
+      if constexpr (DT == DSV_BF16)
+        return (int)(int16_t)bf16_bits(w, e);
+      else
+        return (int)(e == 0 ? w.x : e == 1 ? w.y : e == 2 ? w.z : w.w);
+    };
+    // the list pass's LDS, in big (the penalty slots there are done with)
+    uint4* const stage = big;  // the vectors holding a value at or above the bound
+    int16_t* const s_qid = reinterpret_cast<int16_t*>(big + STAGE_VECS);  // tid | vector << 8
+    uint32_t* const hist256 = reinterpret_cast<uint32_t*>(big + STAGE_VECS + STAGE_VECS / 8);
+    uint64_t* const cbuf = reinterpret_cast<uint64_t*>(big + STAGE_VECS + STAGE_VECS / 8 + 64);
+    static_assert(STAGE_VECS + STAGE_VECS / 8 + 64 + CAND_CAP / 2 <= HWIN / 4, "list pass exceeds the window buffer");
+    static_assert(CT <= 256 && CV <= 127, "stage ids are 16-bit");
+    // only the threads whose max reaches the bound hold admitted values: they stage those of
+    // their vectors that reach it (usually one) and the whole workgroup scans them
+    uint32_t qm = 0u;  // the thread's vectors holding a value at or above the bound
     if (kt >= thr) {
-      const int slot = atomicAdd(&s_nq, 1);
-      if (slot < STAGE_MAX) {
-        s_qtid[slot] = (int16_t)tid;
 #pragma unroll
-        for (int u = 0; u < CV; ++u) stage[slot * CV + u] = v[u];
+      for (int u = 0; u < CV; ++u) {
+        bool hit = false;
+        if (pos_thr && DT == DSV_BF16) {
+          typedef short s16x2 __attribute__((ext_vector_type(2)));
+          const s16x2 a = __builtin_elementwise_max(__builtin_bit_cast(s16x2, v[u].x), __builtin_bit_cast(s16x2, v[u].y));
+          const s16x2 c2 = __builtin_elementwise_max(__builtin_bit_cast(s16x2, v[u].z), __builtin_bit_cast(s16x2, v[u].w));
+          const s16x2 d = __builtin_elementwise_max(a, c2);
+          hit = ((int)d.x > (int)d.y ? (int)d.x : (int)d.y) >= t0;
+        } else if (pos_thr) {
+          hit = max(max((int)v[u].x, (int)v[u].y), max((int)v[u].z, (int)v[u].w)) >= t0;
+        } else if constexpr (DT == DSV_F32) {
+          // float bits as signed integers with the negative values' magnitude bits flipped
+          // order as their keys do (key = image ^ 2^31), -0 one below +0; a zero bound (the key
+          // of +-0) is lowered by one to take -0 in
+          const int tb = (int)(thr ^ 0x80000000u);
+          const int tl = tb == 0 ? -1 : tb;
+          const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+          int s4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s4[e] = (int)(w4[e] ^ ((uint32_t)((int)w4[e] >> 31) >> 1));
+          const int mx = max(max(s4[0], s4[1]), max(s4[2], s4[3]));
+          hit = mx >= tl;
+        } else {
+#pragma unroll
+          for (int e = 0; e < n; ++e) hit |= key_of<DT>(vec_elem<DT>(v[u], e)) >= thr;
+        }
+        qm |= (uint32_t)hit << u;
+      }
+    }
+    {
+      const int nv = __popc(qm);
+      const int incl = wave_incl_scan(nv);
+      const int tot = readlane<WAVE - 1>(incl);
+      int base = 0;
+      if (lane == 0 && tot) base = atomicAdd(&s_nq, tot);
+      int at = readlane<0>(base) + incl - nv;
+#pragma unroll
+      for (int u = 0; u < CV; ++u) {
+        if ((qm >> u) & 1u) {
+          if (at < STAGE_VECS) {
+            stage[at] = v[u];
+            s_qid[at] = (int16_t)(tid | (u << 8));
+          }
+          ++at;
+        }
       }
     }
     __syncthreads();
     const int nq = s_nq;
-    const bool pos_thr = DT == DSV_BF16 && thr > 0x8000u;  // (the usual case)
-    const int t0 = (int)thr - 0x8000;
-    if (nq <= STAGE_MAX) {
-      for (int vb = 0; vb < nq * CV; vb += CT) {
+    if (nq <= STAGE_VECS) {
+      for (int vb = 0; vb < nq; vb += CT) {
         const int vi = vb + tid;
         uint4 w = make_uint4(0u, 0u, 0u, 0u);
         int64_t j0 = hi;
-        if (vi < nq * CV) {
-          const int slot = vi / CV, u = vi - slot * CV;
+        if (vi < nq) {
+          const int q = s_qid[vi];
           w = stage[vi];
-          j0 = (v0 + (int64_t)u * CT + s_qtid[slot]) * n;
+          j0 = (v0 + (int64_t)(q >> 8) * CT + (q & 255)) * n;
         }
         uint32_t am = 0u;  // the vector's admitted elements
         if (pos_thr) {
-          // a positive bf16 threshold: a value reaches it iff its bits, as a signed 16-bit
-          // integer, reach thr - 0x8000 (negative values are negative integers); its key is
-          // then bits | 0x8000
 #pragma unroll
-          for (int e = 0; e < n; ++e) am |= (uint32_t)((int)(int16_t)bf16_bits(w, e) >= t0) << e;
+          for (int e = 0; e < n; ++e) am |= (uint32_t)(sbits(w, e) >= t0) << e;
           const int64_t nval = hi - j0;  // elements of the vector inside the row
-          am &= nval >= n ? 0xFFu : (nval <= 0 ? 0u : (1u << (uint32_t)nval) - 1u);
+          am &= nval >= n ? (1u << n) - 1u : (nval <= 0 ? 0u : (1u << (uint32_t)nval) - 1u);
         } else {
 #pragma unroll
           for (int e = 0; e < n; ++e)
@@ -2254,7 +2309,7 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
 #pragma unroll
           for (int e = 0; e < n; ++e) {
             if ((am >> e) & 1u) {
-              const uint32_t key = pos_thr ? (bf16_bits(w, e) | 0x8000u) : key_of<DT>(vec_elem<DT>(w, e));
+              const uint32_t key = pos_thr ? ((uint32_t)sbits(w, e) & (SIGNB | (SIGNB - 1u))) | SIGNB : key_of<DT>(vec_elem<DT>(w, e));
               if (at < CAND_CAP) cbuf[at] = pack(key, j0 + e);
               ++at;
             }
@@ -2264,10 +2319,10 @@ __global__ __launch_bounds__(CT) void k_chunk(KParams P) {
     }
     __syncthreads();
     int nb = __builtin_amdgcn_readfirstlane(s_cnt);
-    if (nq > STAGE_MAX || nb > CAND_CAP) {
-      // too many threads to stage, or too many admitted values: re-read the chunk
+    if (nq > STAGE_VECS || nb > CAND_CAP) {
+      // too many vectors to stage, or too many admitted values: re-read the chunk
       nb = refill_candidates<DT>(pen ? s_pb : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
-                                 hist256, su, &s_cnt, nq > STAGE_MAX ? ((uint64_t)thr << 32) | 1ull : 0ull);
+                                 hist256, su, &s_cnt, nq > STAGE_VECS ? ((uint64_t)thr << 32) | 1ull : 0ull);
     }
     const int kk = K < nb ? K : nb;
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;

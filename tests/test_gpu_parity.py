@@ -128,11 +128,15 @@ def test_topk_serving_rows(device, dtype, k):
 @pytest.mark.parametrize("k", [1, 20, 64, 256])
 def test_topk_degenerate_rows(device, k):
     V = 70001
-    rows = torch.zeros(4, V)
+    rows = torch.zeros(6, V)
     rows[1] = torch.arange(V).float()          # ascending: every block raises the threshold
     rows[2] = -torch.arange(V).float()         # descending
     rows[3, :] = -torch.inf
     rows[3, 5::1000] = 1.0                     # only 71 finite values
+    rows[4, 1::2] = -0.0                       # +0 / -0 alternating, a zero bound that takes -0 in
+    rows[4, ::3] = -1.0
+    g = torch.Generator().manual_seed(7)
+    rows[5] = -torch.rand(V, generator=g) * 4.0 - 0.5  # every value negative: a negative bound
     for dtype in (torch.float32, torch.bfloat16):
         _topk_check(rows.to(dtype), k, device)
 
