@@ -1216,22 +1216,34 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
   // kcov, or below every counted value), so the window counts hold them all.
   const BonusP bp = bonus_p<DT>(rs, T);
   if (keep_hc && fc != ~0ull) {
-    // the cut is in the merged window: every key above it, and the cut key, are in the LDS counts
-    for (int c = wid; c < C; c += NW) {
-      double mc = 0.0;
-      int32_t tc = 0;
-      for (int q = lane; q < W; q += WAVE) {
-        const uint32_t k = kmax - (uint32_t)q;
-        const uint32_t cnt = sh.hc[c * HC_KEYS + q];
-        if (k > rs.vcut && cnt) mc += (double)cnt * (double)(etab[q] * bp.scale);
-        if (k == rs.vcut) tc = (int32_t)cnt;
+    // the cut is in the merged window: every key above it, and the cut key, are in the LDS
+    // counts.  Wave w takes chunks w and w + NW (C <= 8) in one pass over the keys.
+    static_assert(2 * NW >= 8, "two chunks a wave cover the per-chunk tables");
+    const int c2w[2] = {wid, wid + NW};
+    double mc[2] = {0.0, 0.0};
+    int32_t tc[2] = {0, 0};
+    for (int q = lane; q < W; q += WAVE) {
+      const uint32_t k = kmax - (uint32_t)q;
+      const float e = etab[q] * bp.scale;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t cnt = c2w[h] < C ? sh.hc[c2w[h] * HC_KEYS + q] : 0u;
+        if (k > rs.vcut && cnt) mc[h] += (double)cnt * (double)e;
+        if (k == rs.vcut) tc[h] = (int32_t)cnt;
       }
-      mc = wave_sum(mc);
-      tc = wave_sum(tc);
-      if (lane == 0) {
-        ds.cm[c] = mc;
-        ds.ct[c] = tc;
-        if (!a.candidates) P.rties[r * NCHK + c] = tc;  // (for k_dense_p; the step keeps them in LDS)
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mc[h] = wave_sum(mc[h]);
+      tc[h] = wave_sum(tc[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c2w[h];
+      if (lane == 0 && c < C) {
+        ds.cm[c] = mc[h];
+        ds.ct[c] = tc[h];
+        if (!a.candidates) P.rties[r * NCHK + c] = tc[h];  // (for k_dense_p; the step keeps them in LDS)
       }
     }
   } else {
@@ -1989,9 +2001,12 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
     // the n bits of vector u: bit (u CT + tid) n of the slice (lo is a multiple of 32)
     uint32_t bits[CV];
     {
+      // vector u's word is u CT n / 32 words past vector 0's (CT n a multiple of 32)
+      static_assert((CT * n) % 32 == 0, "vector rows of the bitmap slice are whole words");
       const uint32_t sh = (uint32_t)(tid * n) & 31u;
+      const uint32_t* pbt = s_pb + ((tid * n) >> 5);
 #pragma unroll
-      for (int u = 0; u < CV; ++u) bits[u] = (s_pb[((u * CT + tid) * n) >> 5] >> sh) & ((1u << n) - 1u);
+      for (int u = 0; u < CV; ++u) bits[u] = (pbt[u * (CT * n / 32)] >> sh) & ((1u << n) - 1u);
     }
     penalize_hits<DT, CV>(v, bits, pres, rep, s_hv + wid * WHITV, s_hm + wid * WHITV);
   }
