@@ -219,10 +219,19 @@ __device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, 
                                              bool want_x, DrawShared& sh) {
   const dsv_verify_args& a = P.a;
   const int lane = threadIdx.x & (WAVE - 1);
-  const int64_t qi = ((int64_t)b * (a.T - 1) + step) * a.K;
   const bool on = live && lane < a.K;
-  const int64_t qid = on ? load_index(a.q_ids, a.q_ids_i64, qi + lane) : -1;
-  const float qr = on ? a.q_values[qi + lane] : 0.f;
+  // loaded whether or not the row tests a draft (its step and lane clamped into the request's
+  // q rows), so that the loads do not wait for the request's verify length
+  int64_t qid_l = -1;
+  float qr_l = 0.f;
+  if (a.candidates && a.q_ids && a.q_values && a.T >= 2 && a.K >= 1) {
+    const int st = step < a.T - 1 ? step : a.T - 2;
+    const int64_t qs = ((int64_t)b * (a.T - 1) + st) * a.K + (lane < a.K ? lane : 0);
+    qid_l = load_index(a.q_ids, a.q_ids_i64, qs);
+    qr_l = a.q_values[qs];
+  }
+  const int64_t qid = on ? qid_l : -1;
+  const float qr = on ? qr_l : 0.f;
   sh.qid[lane] = qid;
   sh.qraw[lane] = qr;
   sh.qv[lane] = clamp01(qr);
@@ -2600,8 +2609,16 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   if (tid < WAVE) {
     if (lane < P.C) pre.cs[lane] = P.cstat[r * P.C + lane];
     if (lane == 0) {
-      pre.tok = tests ? a.candidates[(int64_t)b * a.T + s + 1] : -1;
-      pre.u = tests ? a.uniforms[(int64_t)b * (a.T - 1) + s] : 0.f;
+      // the draft token and its coin, loaded before the verify length settles whether the row
+      // tests one (positions clamped into the request's rows)
+      int64_t tk = -1;
+      float u = 0.f;
+      if (a.candidates && a.T >= 2) {
+        tk = a.candidates[(int64_t)b * a.T + (s + 1 < a.T ? s + 1 : a.T - 1)];
+        u = a.uniforms[(int64_t)b * (a.T - 1) + (s < a.T - 1 ? s : a.T - 2)];
+      }
+      pre.tok = tests ? tk : -1;
+      pre.u = tests ? u : 0.f;
       pre.uf = a.candidates ? a.uniform_final[b] : 0.f;
       pre.top_p = a.top_ps ? a.top_ps[b] : 1.f;
       pre.min_p = a.min_ps ? a.min_ps[b] : 0.f;
