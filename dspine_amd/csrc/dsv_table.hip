@@ -6,9 +6,11 @@
 //   ref    = x[n] + scale[n] * (msg @ w_last^T)                    [H]
 //   T[n, j, c] = (ref / sqrt(mean(ref^2) + eps) * norm_w) . head[n, c]
 // in float32 on the matrix cores (v_mfma_f32_16x16x4f32), three launches:
-//   k_rs_message  sender rows x R: the gathered, scaled codebook rows times [pg; pv]^T, with the
-//                 gate, the value and their product in the epilogue -> msg [n*K, R]
-//   k_rs_table    (row, 16 senders, H slice): msg times w_last^T in 16 x 16 output blocks that are
+//   k_rs_message  sender rows x R: the gathered, scaled codebook rows times [pg; pv]^T (the pg / pv
+//                 rows staged in LDS tiles shared by a workgroup's waves), with the gate, the value
+//                 and their product in the epilogue -> msg [n*K, R]
+//   k_rs_table    (row, 16 senders, H slice): msg times w_last^T (w_last staged in LDS tiles of 16
+//                 rows shared by a workgroup's four units) in 16 x 16 output blocks that are
 //                 already the B operand of the second product against the 16 candidates' head
 //                 rows, so ref never leaves registers; partial sums of ref^2 and of the dot products
 //   k_rs_finish   the slices combined, divided by sqrt(mean + eps)
@@ -83,10 +85,18 @@ __device__ __forceinline__ int64_t state_row(const RsArgs& A, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------------------
-// k_rs_message: 64 sender rows x 64 R columns a workgroup (wave w: sender rows 16w..16w+15)
+// k_rs_message: 64 sender rows x 64 R columns a workgroup (wave w: sender rows 16w..16w+15).
+// The B operands (pg and pv rows r0..r0+63) go through LDS in tiles of 64 k, shared by the four
+// waves, the next tile's loads in flight in registers while the current one is used.
 // ---------------------------------------------------------------------------------------
+constexpr int RS_MK = 64;            // k of a staged tile (four 16-wide k steps)
+constexpr int RS_MROW = RS_MK + 4;   // LDS row stride (floats): a lane group's 16 rows of one
+                                     // k step fall in distinct bank groups
+constexpr int RS_MCH = 2 * 64 * RS_MK / 4 / 256;  // 16-byte chunks of a tile pair a thread copies
+
 __global__ __launch_bounds__(256) void k_rs_message(RsArgs A) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, li = lane & 15;
+  __shared__ __align__(16) float bt[2 * 64 * RS_MROW];  // pg tile, then pv tile
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int64_t Ns = (int64_t)A.n * A.K;
   const int64_t i = (int64_t)blockIdx.x * 64 + w * 16 + li;  // the A-operand row of this lane
   const bool live = i < Ns;
@@ -96,15 +106,38 @@ __global__ __launch_bounds__(256) void k_rs_message(RsArgs A) {
   f4 accg[4], accv[4];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) accg[cb] = accv[cb] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < A.C; k0 += 16) {
-    f4 a = bf4(erow + k0 + 4 * g);
-    a *= A.sqrt_c;
-    if (!live) a = f4{0.f, 0.f, 0.f, 0.f};
+  // tile copy: chunk q = c * 256 + tid -> matrix q / 1024, row (q % 1024) / 16, k chunk q % 16
+  f4 pre[RS_MCH];
+  auto fetch = [&](int k0) {
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int64_t r = r0 + 16 * cb + li;
-      accg[cb] = mfma4(a, ld4(A.pg + r * A.C + k0 + 4 * g), accg[cb]);
-      accv[cb] = mfma4(a, ld4(A.pv + r * A.C + k0 + 4 * g), accv[cb]);
+    for (int c = 0; c < RS_MCH; ++c) {
+      const int q = c * 256 + tid, mat = q >> 10, row = (q >> 4) & 63, kc = q & 15;
+      const float* src = mat ? A.pv : A.pg;
+      if (k0 + 4 * kc < A.C) pre[c] = ld4(src + (int64_t)(r0 + row) * A.C + k0 + 4 * kc);
+    }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < A.C; k0 += RS_MK) {
+    __syncthreads();  // (the previous tile's readers are done)
+#pragma unroll
+    for (int c = 0; c < RS_MCH; ++c) {
+      const int q = c * 256 + tid, mat = q >> 10, row = (q >> 4) & 63, kc = q & 15;
+      if (k0 + 4 * kc < A.C) *reinterpret_cast<f4*>(bt + (mat * 64 + row) * RS_MROW + 4 * kc) = pre[c];
+    }
+    __syncthreads();
+    if (k0 + RS_MK < A.C) fetch(k0 + RS_MK);  // in flight under this tile's products
+    const int ns = (A.C - k0) / 16 < RS_MK / 16 ? (A.C - k0) / 16 : RS_MK / 16;
+#pragma unroll 1
+    for (int st = 0; st < ns; ++st) {  // (ns < 4: a partial last tile when C is not a multiple of RS_MK)
+      f4 a = bf4(erow + k0 + 16 * st + 4 * g);
+      a *= A.sqrt_c;
+      if (!live) a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const float* bp = bt + (16 * cb + li) * RS_MROW + 16 * st + 4 * g;
+        accg[cb] = mfma4(a, *reinterpret_cast<const f4*>(bp), accg[cb]);
+        accv[cb] = mfma4(a, *reinterpret_cast<const f4*>(bp + 64 * RS_MROW), accv[cb]);
+      }
     }
   }
   if (A.res_emb) {  // the terminal residual: value += res_emb[sender] @ res_proj^T
@@ -129,26 +162,33 @@ __global__ __launch_bounds__(256) void k_rs_message(RsArgs A) {
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       const int r = r0 + 16 * cb + li;
-      const float pre = (bf(qrow[r]) + accg[cb][v]) + A.gb[r];
-      const float gate = 1.f / (1.f + expf(-pre));
+      const float pre_ = (bf(qrow[r]) + accg[cb][v]) + A.gb[r];
+      const float gate = 1.f / (1.f + expf(-pre_));
       A.msg[io * A.R + r] = gate * accv[cb][v];
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// k_rs_table: one (row, 16-sender block) a wave, 4 a workgroup, one H slice a grid column
+// k_rs_table: one (row, 16-sender block) a wave, 4 a workgroup, one H slice a grid column.  The
+// workgroup stages each 16-row tile of w_last (16 h x R) in LDS once for its four waves, the
+// next tile's loads in flight in registers while the current tile feeds the matrix cores.
 // ---------------------------------------------------------------------------------------
+constexpr int RS_TROW = RS_RMAX + 4;  // LDS row stride of a w_last tile (floats): 16 rows' 16-byte
+                                      // A fragments of one k step fall in distinct bank groups
+constexpr int RS_TCH = 16 * RS_RMAX / 4 / 256;  // 16-byte chunks of a full tile a thread copies
+
 template <int KB>
 __global__ __launch_bounds__(256) void k_rs_table(RsArgs A) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, li = lane & 15;
+  __shared__ __align__(16) float tile[16 * RS_TROW];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int unit = blockIdx.x * 4 + w;
-  if (unit >= A.units) return;  // (whole waves; the kernel has no barriers)
+  const bool ulive = unit < A.units;  // (a wave past the last unit still copies tiles)
   const int slice = blockIdx.y;
-  const int64_t n = unit / KB;
-  const int jb = unit - (int)n * KB;
+  const int64_t n = ulive ? unit / KB : 0;
+  const int jb = ulive ? unit - (int)n * KB : 0;
   const int j = jb * 16 + li;  // the sender lane of this lane's B-operand column
-  const bool jlive = j < A.K;
+  const bool jlive = ulive && j < A.K;
   const int64_t mrow = state_row(A, n);
   const float scale = A.rms[mrow];
   const uint16_t* xrow = A.raw + mrow * A.raw_stride;
@@ -166,7 +206,7 @@ __global__ __launch_bounds__(256) void k_rs_table(RsArgs A) {
 #pragma unroll
   for (int cb = 0; cb < KB; ++cb) {
     const int c = cb * 16 + li;
-    clive[cb] = c < A.K;
+    clive[cb] = ulive && c < A.K;
     const int64_t cc = clive[cb] ? c : 0;
     hrow[cb] = A.head_is_cand ? A.head + (n * A.K + cc) * A.H : A.head + A.cand[n * A.K + cc] * A.H;
   }
@@ -175,13 +215,39 @@ __global__ __launch_bounds__(256) void k_rs_table(RsArgs A) {
   for (int cb = 0; cb < KB; ++cb) dot[cb] = f4{0.f, 0.f, 0.f, 0.f};
   float ss = 0.f;
   const int h_lo = slice * A.hs, h_hi = h_lo + A.hs;
+  // tile copy: chunk q = i * 256 + tid of the tile's 16 x R/4 chunks -> row q / (R/4), column
+  // chunk q % (R/4); chunks past 4R (R < RS_RMAX) are not copied (goff -1)
+  const int rq = A.R / 4, nq = 16 * rq;
+  int goff[RS_TCH], loff[RS_TCH];  // this thread's chunks: offsets in w_last rows h0.. and in the tile
+#pragma unroll
+  for (int i = 0; i < RS_TCH; ++i) {
+    const int q = i * 256 + tid;
+    const int row = q / rq, col = q - row * rq;
+    goff[i] = q < nq ? row * A.R + 4 * col : -1;
+    loff[i] = row * RS_TROW + 4 * col;
+  }
+  f4 pre[RS_TCH];
+  auto fetch = [&](int h0) {
+    const float* base = A.w_last + (int64_t)h0 * A.R;
+#pragma unroll
+    for (int i = 0; i < RS_TCH; ++i)
+      if (goff[i] >= 0) pre[i] = ld4(base + goff[i]);
+  };
+  fetch(h_lo);
   for (int h0 = h_lo; h0 < h_hi; h0 += 16) {
-    // ref^T block [16 h x 16 senders]: A = w_last rows h0 + li, B = msg^T
+    __syncthreads();  // (the previous tile's readers are done)
+#pragma unroll
+    for (int i = 0; i < RS_TCH; ++i)
+      if (goff[i] >= 0) *reinterpret_cast<f4*>(tile + loff[i]) = pre[i];
+    __syncthreads();
+    if (h0 + 16 < h_hi) fetch(h0 + 16);  // in flight under this tile's products
+    if (!ulive) continue;
+    // ref^T block [16 h x 16 senders]: A = w_last rows h0 + li (from the tile), B = msg^T
     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-    const float* wrow = A.w_last + (int64_t)(h0 + li) * A.R + 4 * g;
+    const float* arow = tile + li * RS_TROW + 4 * g;
 #pragma unroll
     for (int t = 0; t < RS_RMAX / 16; ++t)
-      if (16 * t < A.R) acc = mfma4(ld4(wrow + 16 * t), mb[t], acc);
+      if (16 * t < A.R) acc = mfma4(*reinterpret_cast<const f4*>(arow + 16 * t), mb[t], acc);
     // lane: h = h0 + 4g + v, sender j; ref, its square, and ref * norm_w as the B operand
     const f4 xv = bf4(xrow + h0 + 4 * g);
     const f4 nw = ld4(A.norm_w + h0 + 4 * g);
@@ -199,6 +265,7 @@ __global__ __launch_bounds__(256) void k_rs_table(RsArgs A) {
       dot[cb] = mfma4(a, bv, dot[cb]);
     }
   }
+  if (!ulive) return;
   // the slice's partial sums: ss over the lane group's h (lanes li, li+16, li+32, li+48 share j),
   // dot[cb][v] = sum_h head[c = cb*16 + 4g + v][h] * ref[j][h] * norm_w[h]
   ss += __shfl_xor(ss, 16);
