@@ -34,6 +34,11 @@ __device__ __forceinline__ int64_t request_of_row(const int64_t* row_to_request,
   return row_to_request ? row_to_request[r] : r / rows_per_request;
 }
 
+__device__ __forceinline__ float adjust_one(float x, float s, int32_t op) {
+  return op == DSV_ADJ_ADD ? x + s : (x < 0.f ? x * s : x / s);
+}
+
+// One element a thread a step (any alignment).
 template <typename E>
 __global__ __launch_bounds__(ADJ_THREADS) void k_adjust(E* logits, int64_t vocab, int64_t row_stride,
                                                        const int64_t* row_to_request, int32_t rows_per_request,
@@ -42,15 +47,48 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust(E* logits, int64_t vocab
   const int64_t req = request_of_row(row_to_request, rows_per_request, r);
   E* row = logits + r * row_stride;
   const float* v = values + req * values_stride;
-  for (int64_t j = (int64_t)blockIdx.x * ADJ_THREADS + threadIdx.x; j < vocab; j += (int64_t)gridDim.x * ADJ_THREADS) {
-    const float x = elem_load<E>(row + j);
-    const float s = v[j];
-    float y;
-    if (op == DSV_ADJ_ADD)
-      y = x + s;
-    else
-      y = x < 0.f ? x * s : x / s;
-    elem_store(row + j, y);
+  for (int64_t j = (int64_t)blockIdx.x * ADJ_THREADS + threadIdx.x; j < vocab; j += (int64_t)gridDim.x * ADJ_THREADS)
+    elem_store(row + j, adjust_one(elem_load<E>(row + j), v[j], op));
+}
+
+// Eight consecutive elements a thread a step, 16-byte loads and stores (rows and value rows
+// 16-byte aligned); the row's last vocab % 8 elements one at a time.
+constexpr int ADJ_VEC = 8;
+template <typename E>
+__global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t vocab, int64_t row_stride,
+                                                           const int64_t* row_to_request, int32_t rows_per_request,
+                                                           int32_t op, const float* values, int64_t values_stride) {
+  const int64_t r = blockIdx.y;
+  const int64_t req = request_of_row(row_to_request, rows_per_request, r);
+  E* row = logits + r * row_stride;
+  const float* v = values + req * values_stride;
+  const int64_t step = (int64_t)gridDim.x * ADJ_THREADS * ADJ_VEC;
+  for (int64_t j = ((int64_t)blockIdx.x * ADJ_THREADS + threadIdx.x) * ADJ_VEC; j < vocab; j += step) {
+    if (j + ADJ_VEC <= vocab) {
+      const float4 s0 = *reinterpret_cast<const float4*>(v + j), s1 = *reinterpret_cast<const float4*>(v + j + 4);
+      const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      if constexpr (sizeof(E) == 2) {
+        uint4 w = *reinterpret_cast<const uint4*>(row + j);
+        uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float lo = adjust_one(bf16_bits_to_f32(wp[k] & 0xFFFFu), s[2 * k], op);
+          const float hi = adjust_one(bf16_bits_to_f32(wp[k] >> 16), s[2 * k + 1], op);
+          wp[k] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+        }
+        *reinterpret_cast<uint4*>(row + j) = w;
+      } else {
+        float4 x0 = *reinterpret_cast<const float4*>(row + j), x1 = *reinterpret_cast<const float4*>(row + j + 4);
+        x0 = make_float4(adjust_one(x0.x, s[0], op), adjust_one(x0.y, s[1], op), adjust_one(x0.z, s[2], op),
+                         adjust_one(x0.w, s[3], op));
+        x1 = make_float4(adjust_one(x1.x, s[4], op), adjust_one(x1.y, s[5], op), adjust_one(x1.z, s[6], op),
+                         adjust_one(x1.w, s[7], op));
+        *reinterpret_cast<float4*>(row + j) = x0;
+        *reinterpret_cast<float4*>(row + j + 4) = x1;
+      }
+    } else {
+      for (int64_t k = j; k < vocab; ++k) elem_store(row + k, adjust_one(elem_load<E>(row + k), v[k], op));
+    }
   }
 }
 
@@ -123,6 +161,7 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
                                                           int32_t capacity, int32_t* ids, float* values,
                                                           int32_t* lengths, int32_t* overflow) {
   constexpr int NW = CMP_THREADS / WAVE;
+  constexpr int64_t TILE = (int64_t)CMP_THREADS * CMP_E;
   __shared__ int32_t red[NW];
   __shared__ int32_t s_bad;
   const int64_t r = blockIdx.x;
@@ -130,14 +169,30 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
   const float* row = p + r * row_stride;
   int32_t* oid = ids + r * capacity;
   float* oval = values + r * capacity;
+  const bool vec = (uintptr_t)row % 16 == 0;  // (CMP_E = 8 ids a thread: two 16-byte loads)
   if (tid == 0) s_bad = 0;
+  // a tile's eight values of this thread; the next tile's loads are in flight while a tile is
+  // counted and written
+  auto fetch = [&](int64_t t0, float (&x)[CMP_E]) {
+    const int64_t j0 = t0 + (int64_t)tid * CMP_E;
+    if (vec && j0 + CMP_E <= vocab) {
+      const float4 a = *reinterpret_cast<const float4*>(row + j0), b = *reinterpret_cast<const float4*>(row + j0 + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < CMP_E; ++e) x[e] = j0 + e < vocab ? row[j0 + e] : 0.f;
+    }
+  };
   int64_t total = 0;  // kept ids before the current tile
   bool bad = false;
-  for (int64_t t0 = 0; t0 < vocab; t0 += (int64_t)CMP_THREADS * CMP_E) {
-    const int64_t j0 = t0 + (int64_t)tid * CMP_E;
+  float xn[CMP_E];
+  fetch(0, xn);
+  for (int64_t t0 = 0; t0 < vocab; t0 += TILE) {
     float x[CMP_E];
 #pragma unroll
-    for (int e = 0; e < CMP_E; ++e) x[e] = j0 + e < vocab ? row[j0 + e] : 0.f;
+    for (int e = 0; e < CMP_E; ++e) x[e] = xn[e];
+    if (t0 + TILE < vocab) fetch(t0 + TILE, xn);
+    const int64_t j0 = t0 + (int64_t)tid * CMP_E;
     int32_t cnt = 0;
 #pragma unroll
     for (int e = 0; e < CMP_E; ++e) {
@@ -156,6 +211,9 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
         ++at;
       }
     total += tot;
+    // more than capacity kept ids: the row overflows whatever the rest holds, and the first
+    // capacity ids are written (total is the same in every thread)
+    if (total > capacity) break;
   }
   if (bad) s_bad = 1;
   __syncthreads();
@@ -638,13 +696,28 @@ extern "C" int dsv_adjust_logits(void* logits, int32_t logits_dtype, int64_t row
              (long long)rows, (long long)requests, rows_per_request);
   if (rows == 0) return DSV_OK;
   if (rows > 65535) DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_adjust_logits: at most 65535 rows per call");
-  const dim3 grid = row_grid(rows, vocab);
-  if (logits_dtype == DSV_BF16)
-    hipLaunchKernelGGL(k_adjust<uint16_t>, grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits, vocab, row_stride,
-                       row_to_request, rows_per_request, op, values, values_stride);
-  else
-    hipLaunchKernelGGL(k_adjust<float>, grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab, row_stride,
-                       row_to_request, rows_per_request, op, values, values_stride);
+  const int64_t esize = logits_dtype == DSV_BF16 ? 2 : 4;
+  const bool vec = (uintptr_t)logits % 16 == 0 && (row_stride * esize) % 16 == 0 && (uintptr_t)values % 16 == 0 &&
+                   values_stride % 4 == 0;
+  if (vec) {
+    int64_t bx = (vocab + ADJ_THREADS * ADJ_VEC - 1) / (ADJ_THREADS * ADJ_VEC);
+    if (bx > 64) bx = 64;
+    const dim3 grid((unsigned)bx, (unsigned)rows);
+    if (logits_dtype == DSV_BF16)
+      hipLaunchKernelGGL(k_adjust_vec<uint16_t>, grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits, vocab,
+                         row_stride, row_to_request, rows_per_request, op, values, values_stride);
+    else
+      hipLaunchKernelGGL(k_adjust_vec<float>, grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab, row_stride,
+                         row_to_request, rows_per_request, op, values, values_stride);
+  } else {
+    const dim3 grid = row_grid(rows, vocab);
+    if (logits_dtype == DSV_BF16)
+      hipLaunchKernelGGL(k_adjust<uint16_t>, grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits, vocab,
+                         row_stride, row_to_request, rows_per_request, op, values, values_stride);
+    else
+      hipLaunchKernelGGL(k_adjust<float>, grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab, row_stride,
+                         row_to_request, rows_per_request, op, values, values_stride);
+  }
   DSV_CHECK_LAUNCH("dsv_adjust_logits");
   return DSV_OK;
 }

@@ -2858,11 +2858,13 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
 }
 
 // ---------------------------------------------------------------------------------------
-// k_dense_p: the target distribution written out densely (runtime/worker.py:440-508), one
-// workgroup per (row, chunk), each thread a span of consecutive ids.
+// The target distribution of one (row, chunk) written out densely with each thread a span of
+// consecutive ids (runtime/worker.py:440-508): the ordered path of k_dense_p -- rows whose cut
+// keeps only some of the values at the cut key (their rank in id order decides), and outputs
+// that are not 16-byte aligned.
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
+__device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int64_t out_stride) {
   constexpr int CHE = Elems<DT>::chunk, FE = CV * Elems<DT>::n;
   constexpr int NW = CT / WAVE;
   __shared__ int32_t red_i[NW];
@@ -2969,6 +2971,153 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
     seen += hist && k == rs.vcut;
     if (vec_ok) put(i, v); else put1(i, v);
   });
+}
+
+
+// ---------------------------------------------------------------------------------------
+// k_dense_p: the target distribution written out densely (runtime/worker.py:440-508), one
+// workgroup per (row, chunk).  The chunk's values are laid out as the chunk pass loads them
+// (thread t, vector u: ids (u CT + t) n .. + n), so that a wave's loads and 16-byte stores are
+// contiguous; support-list rows write zeros with the list's values at their ids (an LDS bitmap
+// of the chunk's list ids), greedy rows the one-hot row.  Rows whose cut keeps only some of the
+// values at the cut key, and unaligned outputs, take the ordered path above.
+// ---------------------------------------------------------------------------------------
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
+  constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
+  constexpr int NW = CT / WAVE;
+  __shared__ ListEntry lst[DSV_LIST_K];
+  __shared__ uint32_t s_bm[CHE / 32];  // list rows: the chunk's list ids; softmax rows: history bits
+  __shared__ uint4 s_hv[NW * WHITV];    // history-hit vectors of each wave
+  __shared__ uint32_t s_hm[NW * WHITV];
+  const dsv_verify_args& a = P.a;
+  const int C = P.C;
+  const int64_t r = blockIdx.x / C;
+  const int c = (int)(blockIdx.x - r * C);
+  const int tid = threadIdx.x, wid = tid / WAVE;
+  const int64_t V = a.vocab;
+  float* orow = out + r * out_stride;
+  int b = 0, s = 0;
+  const bool live_row = row_request(a, r, b, s);
+  const RowSum rs = P.rowsum[r];
+  const int mode = live_row ? rs.mode : M_SKIP;
+  const bool hist = mode == M_HIST;
+  const bool vec_ok = (out_stride % 4 == 0) && ((uintptr_t)out % 16 == 0);
+  if (!vec_ok || (hist && rs.ktie > 0 && rs.ktie != INT_MAX)) {
+    dense_p_spans<DT, ALIGNED>(P, out, out_stride);
+    return;
+  }
+  const int64_t lo = (int64_t)c * CHE, hi = lo + CHE < V ? lo + CHE : V;
+  const int64_t v0 = lo / n;
+  // vector u's n values at ids j0 = (v0 + u CT + tid) n: 16-byte stores, element stores at the
+  // row's end
+  auto store_vec = [&](int64_t j0, const float (&x)[n]) {
+    if (j0 + n <= hi) {
+#pragma unroll
+      for (int q = 0; q < n / 4; ++q)
+        *reinterpret_cast<float4*>(orow + j0 + 4 * q) = make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < n; ++e)
+        if (j0 + e < hi) orow[j0 + e] = x[e];
+    }
+  };
+  if (mode != M_UNF && !hist) {  // skipped, greedy and support-list rows
+    const int nl = mode == M_LIST ? rs.nlist : 0;
+    if (mode == M_LIST) {
+      for (int i = tid; i < CHE / 32; i += CT) s_bm[i] = 0u;
+      for (int i = tid; i < nl; i += CT) lst[i] = P.lists[r * DSV_LIST_K + i];
+      __syncthreads();
+      for (int i = tid; i < nl; i += CT) {
+        const int64_t id = lst[i].id;
+        if (id >= lo && id < hi) atomicOr(&s_bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
+      if (j0 >= hi) continue;
+      float x[n];
+#pragma unroll
+      for (int e = 0; e < n; ++e) x[e] = mode == M_GREEDY && j0 + e == (int64_t)rs.argmax ? 1.f : 0.f;
+      if (mode == M_LIST) {
+        const uint32_t bits = (s_bm[(j0 - lo) >> 5] >> ((j0 - lo) & 31)) & ((1u << n) - 1u);
+        if (bits) {
+#pragma unroll
+          for (int e = 0; e < n; ++e) {
+            if (!((bits >> e) & 1u)) continue;
+            const int64_t j = j0 + e;
+            for (int q = 0; q < nl; ++q)
+              if ((int64_t)lst[q].id == j) {
+                x[e] = lst[q].P;
+                if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
+                  float xv = load_elem<DT>(row_ptr(a, r), j);
+                  if (P.pbits && pen_test(P, b, j))
+                    xv = penalize<DT>(xv, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
+                  x[e] = prob_of(xv, a.temperatures[b], rs.m_f, rs.invZ);
+                }
+              }
+          }
+        }
+      }
+      store_vec(j0, x);
+    }
+    return;
+  }
+  // softmax rows: the chunk in registers, as the chunk pass loads it
+  const bool pen = P.pbits != nullptr;
+  const float pres = pen && a.presence ? a.presence[b] : 0.f;
+  const float rep = pen && a.repetition ? a.repetition[b] : 1.f;
+  const float T = a.temperatures[b];
+  const char* rowp = row_ptr(a, r);
+  uint4 v[CV];
+  const int64_t nfull = hi / n;
+  if constexpr (ALIGNED) {
+    const auto rsr = buf_rsrc(rowp + lo * (16 / n), (uint32_t)((hi - lo) * (16 / n)));
+#pragma unroll
+    for (int u = 0; u < CV; ++u) v[u] = buf_load16(rsr, (uint32_t)tid * 16u, (uint32_t)(u * CT * 16));
+    if (hi - lo < CHE) {  // the row's last chunk: the partial last vector element by element
+      const int64_t rel = nfull - v0;
+#pragma unroll
+      for (int u = 0; u < CV; ++u)
+        if (hi % n && u == rel / CT && tid == rel % CT) v[u] = load_vec<DT>(rowp, nfull, hi, false);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < CV; ++u) v[u] = load_vec<DT>(rowp, v0 + (int64_t)u * CT + tid, hi, false);
+  }
+  if (pen) {
+    for (int i = tid; i < CHE / 32; i += CT) {
+      const int64_t w = (lo >> 5) + i;
+      s_bm[i] = w < P.pwords ? pen_word(P, b, w) : 0u;
+    }
+    __syncthreads();
+    static_assert((CT * n) % 32 == 0, "vector rows of the bitmap slice are whole words");
+    uint32_t bits[CV];
+    const uint32_t sh = (uint32_t)(tid * n) & 31u;
+    const uint32_t* pbt = s_bm + ((tid * n) >> 5);
+#pragma unroll
+    for (int u = 0; u < CV; ++u) bits[u] = (pbt[u * (CT * n / 32)] >> sh) & ((1u << n) - 1u);
+    penalize_hits<DT, CV>(v, bits, pres, rep, s_hv + wid * WHITV, s_hm + wid * WHITV);
+  }
+  // kept: every value of an unfiltered row; a nucleus row's values above the cut key, and the
+  // ones at it when the cut keeps all of them (ktie == INT_MAX) or none (0)
+  const bool all_ties = rs.ktie == INT_MAX;
+#pragma unroll
+  for (int u = 0; u < CV; ++u) {
+    const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
+    if (j0 >= hi) continue;
+    float x[n];
+#pragma unroll
+    for (int e = 0; e < n; ++e) {
+      const float xe = vec_elem<DT>(v[u], e);
+      const uint32_t k = key_of<DT>(xe);
+      const bool kept = !hist || k > rs.vcut || (k == rs.vcut && all_ties);
+      x[e] = kept ? (P.raw_p ? prob_of(xe, T, rs.m_f, rs.invZ) : (float)dense_P(rs, T, xe)) : 0.f;
+    }
+    store_vec(j0, x);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
