@@ -247,6 +247,7 @@ struct ChainShared {
   double red_d[CH_NW];
   int32_t red_i[CH_NW];
   double tile_mass[CH_TILES_MAX];
+  double tile_wave[CH_TILES_MAX * CH_NW];  // each wave's part of a tile's mass
   int64_t qid[QMAX];
   float qc[QMAX];       // clamped q of the lane
   int32_t qlast[QMAX];  // last lane with its id
@@ -307,7 +308,30 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
   int cap = a.verify_lens ? a.verify_lens[b] : T;
   cap = cap < 1 ? 1 : (cap > T ? T : cap);
   // ---- accept loop (wave 0) ----
-  if (tid < WAVE) {
+  if (tid < WAVE && !a.p_ids && cap <= WAVE) {  // (a lane past the last step always fails)
+    // dense P: every draft step's test at once, one lane a step (its token, P and q at the
+    // token, its coin); the accepted length is the run of passing steps from the first
+    const int step = lane + 1;
+    bool ok = false;
+    if (step < cap) {
+      const int64_t row = chain_row(a, b, step - 1);
+      const int64_t tok = a.candidates[(int64_t)b * T + step];
+      const bool tok_ok = tok >= 0 && tok < V;
+      const float p = tok_ok ? chain_dense_p(a, row, tok) : 0.f;
+      float q = 0.f;
+      if (a.dense_q) {
+        if (tok_ok) q = a.dense_q[((int64_t)b * (T - 1) + step - 1) * a.q_stride + tok];
+      } else {
+        const int64_t qi = ((int64_t)b * (T - 1) + step - 1) * a.K;
+        for (int l = 0; l < a.K; ++l)  // the lanes holding the token, in lane order
+          if (load_index(a.q_ids, a.q_ids_i64, qi + l) == tok) q += a.q_values[qi + l];
+      }
+      const float coin = a.uniforms[(int64_t)b * (T - 1) + step - 1];
+      ok = q > 0.f && q <= 1.f && coin * q < p;
+    }
+    const uint64_t fail = ~__ballot(ok);
+    if (tid == 0) sh.acc = __ffsll((long long)fail) - 1;  // (lanes past the last step fail)
+  } else if (tid < WAVE) {
     int acc = 0;
     for (int step = 1; step < cap; ++step) {
       const int64_t row = chain_row(a, b, step - 1);
@@ -420,29 +444,61 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
     __syncthreads();
     bool pure = all;
     double mass = 0.0;
+    const int wid = tid / WAVE;
+    // P's eight values of this thread in tile t (16-byte loads when the rows are aligned)
+    const bool vec = a.p_stride % 4 == 0 && (uintptr_t)a.dense_p % 16 == 0;
+    auto fetch = [&](int t, float (&x)[CH_E]) {
+      const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
+      const float* pr = a.dense_p + row * a.p_stride;
+      if (vec && j0 + CH_E <= V) {
+        const float4 u0 = *reinterpret_cast<const float4*>(pr + j0), u1 = *reinterpret_cast<const float4*>(pr + j0 + 4);
+        x[0] = u0.x; x[1] = u0.y; x[2] = u0.z; x[3] = u0.w; x[4] = u1.x; x[5] = u1.y; x[6] = u1.z; x[7] = u1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < CH_E; ++e) x[e] = j0 + e < V ? pr[j0 + e] : 0.f;
+      }
+    };
     for (int pass = 0; pass < 2; ++pass) {
+      // Each wave's part of every tile's mass, the next tile's loads in flight; then one
+      // barrier and the tiles summed over the waves in wave order (the block sum's order).
+      const bool plain = !pure && !a.dense_q;  // sparse q: P here, the q ids' reductions after
+      float xn[CH_E];
+      if (plain) fetch(0, xn);
       for (int t = 0; t < ntiles; ++t) {
         const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
         double w = 0.0;
-        if (pure || a.dense_q) {
+        if (plain) {
+          float x[CH_E];
+#pragma unroll
+          for (int e = 0; e < CH_E; ++e) x[e] = xn[e];
+          if (t + 1 < ntiles) fetch(t + 1, xn);
+          const float den = a.denominator ? a.denominator[row] : 1.f;
 #pragma unroll
           for (int e = 0; e < CH_E; ++e)
-            if (j0 + e < V) w += chain_weight(a, row, b, acc, j0 + e, pure, sh);
+            if (j0 + e < V) w += (double)(a.denominator ? x[e] / den : x[e]);
         } else {
 #pragma unroll
           for (int e = 0; e < CH_E; ++e)
-            if (j0 + e < V) w += (double)chain_dense_p(a, row, j0 + e);
+            if (j0 + e < V) w += chain_weight(a, row, b, acc, j0 + e, pure, sh);
         }
-        w = block_sum<CH_NW>(w, sh.red_d);
-        if (!pure && !a.dense_q)  // sparse q: the tile's reductions at its q ids
+        w = wave_sum(w);
+        if (lane == 0) sh.tile_wave[t * CH_NW + wid] = w;
+      }
+      __syncthreads();
+      for (int t = tid; t < ntiles; t += CH_THREADS) {
+        double w = 0.0;
+        for (int i = 0; i < CH_NW; ++i) w += sh.tile_wave[t * CH_NW + i];
+        if (plain)  // sparse q: the tile's reductions at its q ids
           for (int l = 0; l < a.K; ++l)
             if (sh.qlast[l] && sh.qid[l] / CH_TILE == t) w -= sh.qd[l];
-        if (tid == 0) sh.tile_mass[t] = w;
-        mass += w;
+        sh.tile_mass[t] = w;
       }
-      if (pure || mass > 0.0) break;
-      pure = true;  // the residual has no mass: draw from P
+      __syncthreads();
       mass = 0.0;
+      for (int t = 0; t < ntiles; ++t) mass += sh.tile_mass[t];
+      if (pure || mass > 0.0) break;
+      __syncthreads();  // (the second pass rewrites the tiles' parts)
+      pure = true;  // the residual has no mass: draw from P
     }
     __syncthreads();
     const double thr = (double)uf * mass;
