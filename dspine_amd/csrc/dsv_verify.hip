@@ -2990,11 +2990,13 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
   __shared__ uint32_t s_bm[CHE / 32];  // list rows: the chunk's list ids; softmax rows: history bits
   __shared__ uint4 s_hv[NW * WHITV];    // history-hit vectors of each wave
   __shared__ uint32_t s_hm[NW * WHITV];
+  __shared__ int32_t s_wt[CV * NW];     // partial ties: each wave's cut-key values of vector u
+  __shared__ int32_t s_before;          // partial ties: the cut-key values of the earlier chunks
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
   const int c = (int)(blockIdx.x - r * C);
-  const int tid = threadIdx.x, wid = tid / WAVE;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   const int64_t V = a.vocab;
   float* orow = out + r * out_stride;
   int b = 0, s = 0;
@@ -3003,7 +3005,9 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
   const int mode = live_row ? rs.mode : M_SKIP;
   const bool hist = mode == M_HIST;
   const bool vec_ok = (out_stride % 4 == 0) && ((uintptr_t)out % 16 == 0);
-  if (!vec_ok || (hist && rs.ktie > 0 && rs.ktie != INT_MAX)) {
+  // a cut that keeps only the first ktie values of the cut key in id order (partial ties)
+  const bool part_ties = hist && rs.ktie > 0 && rs.ktie != INT_MAX;
+  if (!vec_ok || (part_ties && (rs.flags & FLAG_FULL_HIST))) {
     dense_p_spans<DT, ALIGNED>(P, out, out_stride);
     return;
   }
@@ -3101,19 +3105,60 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
     for (int u = 0; u < CV; ++u) bits[u] = (pbt[u * (CT * n / 32)] >> sh) & ((1u << n) - 1u);
     penalize_hits<DT, CV>(v, bits, pres, rep, s_hv + wid * WHITV, s_hm + wid * WHITV);
   }
+  // Partial ties: a cut-key value's rank in id order is the earlier chunks' count (the row
+  // merge's per-chunk counts), the values of the vectors before its vector (vector index order
+  // u CT + t is id order: a prefix over vectors u-major, from one wave scan a vector and the
+  // waves' totals), then the ones before it in its vector.
+  int32_t rank0[CV];
+#pragma unroll
+  for (int u = 0; u < CV; ++u) rank0[u] = 0;
+  if (part_ties) {
+    int32_t incl[CV];
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
+      int32_t cnt = 0;  // (ids past the row, zeros of the buffer loads, do not count)
+#pragma unroll
+      for (int e = 0; e < n; ++e) cnt += j0 + e < hi && key_of<DT>(vec_elem<DT>(v[u], e)) == rs.vcut ? 1 : 0;
+      incl[u] = wave_incl_scan(cnt);
+      rank0[u] = incl[u] - cnt;
+      if (lane == WAVE - 1) s_wt[u * NW + wid] = incl[u];
+    }
+    if (tid == 0) {
+      int32_t before = 0;
+      for (int c2 = 0; c2 < c; ++c2) before += P.rties[r * NCHK + c2];
+      s_before = before;
+    }
+    __syncthreads();
+    int32_t run = s_before;
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      int32_t below = 0, tot = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int32_t t = s_wt[u * NW + w];
+        below += w < wid ? t : 0;
+        tot += t;
+      }
+      rank0[u] += run + below;
+      run += tot;
+    }
+  }
   // kept: every value of an unfiltered row; a nucleus row's values above the cut key, and the
-  // ones at it when the cut keeps all of them (ktie == INT_MAX) or none (0)
-  const bool all_ties = rs.ktie == INT_MAX;
+  // ones at it while their rank is below ktie (all of them at INT_MAX, none at 0)
 #pragma unroll
   for (int u = 0; u < CV; ++u) {
     const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
     if (j0 >= hi) continue;
     float x[n];
+    int32_t seen = 0;
 #pragma unroll
     for (int e = 0; e < n; ++e) {
       const float xe = vec_elem<DT>(v[u], e);
       const uint32_t k = key_of<DT>(xe);
-      const bool kept = !hist || k > rs.vcut || (k == rs.vcut && all_ties);
+      const bool tie = hist && k == rs.vcut;
+      const bool kept = !hist || k > rs.vcut || (tie && (int64_t)rank0[u] + seen < (int64_t)rs.ktie);
+      seen += tie ? 1 : 0;
       x[e] = kept ? (P.raw_p ? prob_of(xe, T, rs.m_f, rs.invZ) : (float)dense_P(rs, T, xe)) : 0.f;
     }
     store_vec(j0, x);
