@@ -227,9 +227,9 @@ def setup_verify(config, args, torch, dev):
                     workspace=ws)
 
     total, chunk = verify_bytes(bs, T, V, K, H, esize, rows=rows)
-    C = math.ceil(V / (20480 if esize == 2 else 10240))
+    C = math.ceil(V / (20480 if esize == 2 else 12288))
     facts = dict(name=name, batch=batch, rows=rows, total=total, chunk=chunk, dtype="bf16" if esize == 2 else "f32",
-                 kernel=f"k_chunk (chunk pass: {rows} rows x {C} chunks of {20480 if esize == 2 else 10240} "
+                 kernel=f"k_chunk (chunk pass: {rows} rows x {C} chunks of {20480 if esize == 2 else 12288} "
                         f"{'bf16' if esize == 2 else 'fp32'})",
                  config={"workload": workload, "requests": bs, "rows_per_request": T, "rows": rows, "vocab": V,
                          "q_width": K, "history": H, "logits_dtype": "bf16" if esize == 2 else "fp32",

@@ -49,7 +49,7 @@ static_assert(sizeof(ChunkStat) == 40, "ChunkStat layout");
 
 
 constexpr int CT = 256;              // threads of a chunk workgroup
-constexpr int CV = 10;               // 16-byte vectors per thread per chunk
+constexpr int CV_MAX = 12;           // most 16-byte vectors a thread holds of a chunk (float32 rows)
 constexpr int CAND_CAP = 512;        // LDS candidate buffer of a chunk (> largest k)
 constexpr int TOPK_MAX = 256;        // largest k of the top-k entry point
 constexpr int NUC_THREADS = 512;     // full-histogram nucleus workgroup
@@ -66,10 +66,12 @@ constexpr int QMAX = 64;             // largest supported sparse-q width K
 constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram
 
 template <int DT>
-struct Elems {  // elements per 16-byte vector
-  static constexpr int n = DT == DSV_BF16 ? 8 : 4;
-  static constexpr int chunk = CT * CV * n;
+struct Elems {
+  static constexpr int n = DT == DSV_BF16 ? 8 : 4;    // elements per 16-byte vector
+  static constexpr int cv = DT == DSV_BF16 ? 10 : 12;  // 16-byte vectors per thread per chunk
+  static constexpr int chunk = CT * cv * n;
 };
+static_assert(Elems<DSV_F32>::cv <= CV_MAX && Elems<DSV_BF16>::cv <= CV_MAX, "CV_MAX bounds both");
 
 __device__ __forceinline__ int64_t load_index(const void* p, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t) reinterpret_cast<const int32_t*>(p)[i];

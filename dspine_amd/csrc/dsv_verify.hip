@@ -2,7 +2,7 @@
 // residual resample, accepted-prefix compaction and KV-slot gather.
 //
 // Launches of one verify step (no host synchronisation):
-//   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 10240 fp32 values held in
+//   k_chunk  (rows x C)         every row, in chunks of 20480 bf16 / 12288 fp32 values held in
 //                               registers: penalties (the chunk's slice of the request's history
 //                               bitmap built in LDS), max/argmax, softmax partial sums, exact
 //                               top-k candidates, nucleus value counts -- one read of the logits
@@ -161,7 +161,7 @@ struct DrawShared {
   int32_t acc, chunk, tieq, use_r, pick_thread, ptb;
   uint64_t rmask;    // q lanes that need their rank at a split cut key
   uint64_t qmask;    // residual q lanes whose id lies in the planned chunk
-  uint4 pv[CV];       // the picked thread's span (penalised)
+  uint4 pv[CV_MAX];   // the picked thread's span (penalised)
 };
 
 // The draw's P at value x: exp2(x c2 - M c2) * scale, scale = 1/Z (over the kept mass S for a
@@ -211,12 +211,19 @@ __device__ __forceinline__ bool q_last_lane(int64_t qid, int K, int64_t V) {
   return last;
 }
 
+// The logit and history word at a q lane's id, loaded by fetch_q_wave and left in flight until
+// qx_finish penalises them into sh.qx (the row merge runs in between).
+struct QxLoad {
+  uint32_t xb;  // the logit's bits at the id (bf16: the 16 bits; -inf without an id)
+  uint32_t hw;  // the history word holding the id's bit (0 without a history)
+};
+
 // The q lanes of draft step+1 for one wave (lanes are the q lanes): ids, given and clamped
-// values, whether the lane is the last with its id, and -- want_x -- the adjusted logit at each
-// such id.  Leaves them in sh; the workgroup sees them after a barrier.
+// values, whether the lane is the last with its id -- left in sh, which the workgroup sees after
+// a barrier -- and, want_x, the loads of the logit at each such id (ql, for qx_finish).
 template <int DT>
 __device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, bool live, const char* rowp,
-                                             bool want_x, DrawShared& sh) {
+                                             bool want_x, DrawShared& sh, QxLoad& ql) {
   const dsv_verify_args& a = P.a;
   const int lane = threadIdx.x & (WAVE - 1);
   const bool on = live && lane < a.K;
@@ -239,12 +246,25 @@ __device__ __forceinline__ void fetch_q_wave(const KParams& P, int b, int step, 
   sh.qrank[lane] = -1;
   const bool last = q_last_lane(qid, a.K, a.vocab);
   sh.qlast[lane] = last;
-  float xq = -INFINITY;
+  // raw bits: a conversion here would wait for the load
+  ql.xb = DT == DSV_BF16 ? 0xff80u : 0xff800000u;
+  ql.hw = 0u;
   if (want_x && last) {
-    xq = load_elem<DT>(rowp, qid);
-    if (P.pbits && pen_test(P, b, qid))
-      xq = penalize<DT>(xq, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
+    if constexpr (DT == DSV_BF16)
+      ql.xb = reinterpret_cast<const uint16_t*>(rowp)[qid];
+    else
+      ql.xb = reinterpret_cast<const uint32_t*>(rowp)[qid];
+    if (P.pbits) ql.hw = pen_word(P, b, qid >> 5);
   }
+}
+
+// The adjusted logit at each q lane's id into sh.qx (the wave that called fetch_q_wave; pres /
+// rep: the request's penalties).
+template <int DT>
+__device__ __forceinline__ void qx_finish(const QxLoad& ql, float pres, float rep, DrawShared& sh) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  float xq = DT == DSV_BF16 ? bf16_bits_to_f32((uint16_t)ql.xb) : __uint_as_float(ql.xb);
+  if ((ql.hw >> (sh.qid[lane] & 31)) & 1u) xq = penalize<DT>(xq, pres, rep);
   sh.qx[lane] = xq;
 }
 
@@ -341,7 +361,7 @@ __device__ __forceinline__ void penalize_hits(uint4 (&v)[NV], const uint32_t (&b
 // order, by span_each as f(i, x); -inf past the row.
 template <int DT, int NT>
 struct Span {
-  static constexpr int SV = CT * CV / NT, FE = SV * Elems<DT>::n;  // vectors and ids a thread
+  static constexpr int SV = CT * Elems<DT>::cv / NT, FE = SV * Elems<DT>::n;  // vectors and ids a thread
   uint4 v[SV];
   uint64_t blo, bhi;  // the span's history bits (tokens >= vocab have none)
 };
@@ -349,7 +369,7 @@ template <int DT, bool ALIGNED, int NT>
 __device__ __forceinline__ void span_load(const KParams& P, int b, const char* rowp, int c, Span<DT, NT>& sp) {
   constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
   constexpr int SV = Span<DT, NT>::SV;
-  static_assert(SV * NT == CT * CV && Span<DT, NT>::FE <= 96, "spans tile a chunk");
+  static_assert(SV * NT == CT * Elems<DT>::cv && Span<DT, NT>::FE <= 96, "spans tile a chunk");
   const int64_t V = P.a.vocab;
   const int64_t clo = (int64_t)c * CHE, chi = clo + CHE < V ? clo + CHE : V;
   const int64_t jlo = clo + (int64_t)threadIdx.x * Span<DT, NT>::FE;
@@ -563,7 +583,7 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
                                               uint32_t* hm) {
   constexpr int NW = NT / WAVE;
   constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk, FE = Span<DT, NT>::FE, SV = Span<DT, NT>::SV;
-  static_assert(FE <= 2 * WAVE && SV <= CV && 64 % n == 0, "a span is walked in two rounds of a wave");
+  static_assert(FE <= 2 * WAVE && SV <= CV_MAX && 64 % n == 0, "a span is walked in two rounds of a wave");
   const dsv_verify_args& a = P.a;
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
@@ -1885,11 +1905,11 @@ __global__ __launch_bounds__(NUC_THREADS) void k_nuc(KParams P) {
 }
 
 // ---------------------------------------------------------------------------------------
-// k_chunk: one pass over a 20480-value (bf16) / 10240-value (fp32) chunk held in registers
+// k_chunk: one pass over a 20480-value (bf16) / 12288-value (fp32) chunk held in registers
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_chunk(KParams P) {
-  constexpr int n = Elems<DT>::n;
+  constexpr int n = Elems<DT>::n, CV = Elems<DT>::cv;
   constexpr int CHE = Elems<DT>::chunk;
   // nucleus rows: 32-bit value counts of the window; list rows: staged vectors, their ids, the
   // candidates and the radix counts (below); first the penalty step's slots (below)
@@ -2604,8 +2624,8 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   const int cap = req_cap(a, b);
   const bool resid = s < cap - 1;  // the row tests draft s+1, and ends the prefix when it is rejected
   const bool tests = a.candidates != nullptr && resid;
-  // one round of reads before the merge: the chunk statistics (wave 0), the draft token, its
-  // coin and q lanes, and for dense rows the adjusted logits at the q ids (wave 1)
+  // one round of reads before the merge: the chunk statistics, the draft token and its coin
+  // (wave 0), the q lanes (wave 1)
   if (tid < WAVE) {
     if (lane < P.C) pre.cs[lane] = P.cstat[r * P.C + lane];
     if (lane == 0) {
@@ -2626,9 +2646,12 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
       pre.pres = P.pbits && a.presence ? a.presence[b] : 0.f;
       pre.rep = P.pbits && a.repetition ? a.repetition[b] : 1.f;
     }
-  } else if (tid < 2 * WAVE) {
-    fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds);
   }
+  // wave 1: the q lanes, and for dense rows the loads of the logits at their ids, which stay in
+  // flight through the merge (the bonus plan is their first use)
+  QxLoad ql;
+  if (tid >= WAVE && tid < 2 * WAVE)
+    fetch_q_wave<DT>(P, b, s, tests, row_ptr(a, r), mode == M_UNF || mode == M_HIST, ds, ql);
   __syncthreads();
   if (mode == M_HIST) {
     if constexpr (DT == DSV_BF16)
@@ -2638,6 +2661,7 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
   } else {
     merge_row<DT>(P, r, b, s, mode, T, ms, ds, pre, &ro);
   }
+  if (tid >= WAVE && tid < 2 * WAVE) qx_finish<DT>(ql, pre.pres, pre.rep, ds);
   __syncthreads();
   // The bonus token this row gives when it is the request's accepted length: none for a row
   // whose draft was accepted before the last row (the accepted length lies beyond it), nor for
@@ -2865,7 +2889,7 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
 __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int64_t out_stride) {
-  constexpr int CHE = Elems<DT>::chunk, FE = CV * Elems<DT>::n;
+  constexpr int CV = Elems<DT>::cv, CHE = Elems<DT>::chunk, FE = CV * Elems<DT>::n;
   constexpr int NW = CT / WAVE;
   __shared__ int32_t red_i[NW];
   __shared__ ListEntry lst[DSV_LIST_K];
@@ -2984,7 +3008,7 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
 __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
-  constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
+  constexpr int n = Elems<DT>::n, CV = Elems<DT>::cv, CHE = Elems<DT>::chunk;
   constexpr int NW = CT / WAVE;
   __shared__ ListEntry lst[DSV_LIST_K];
   __shared__ uint32_t s_bm[CHE / 32];  // list rows: the chunk's list ids; softmax rows: history bits

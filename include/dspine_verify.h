@@ -148,7 +148,7 @@ int64_t dsv_greedy_workspace_bytes(int64_t rows, int64_t vocab);
 /* in the reference: it is for callers that cannot allocate device memory (code under HIP      */
 /* graph capture, serving loops or harnesses that forbid hipMalloc).  The per-chunk statistics */
 /* live in a static device array of the library (2.5 MiB a device, held until the process     */
-/* ends): rows * ceil(vocab / 20480) (bf16) or rows * ceil(vocab / 10240) (float32) must not   */
+/* ends): rows * ceil(vocab / 20480) (bf16) or rows * ceil(vocab / 12288) (float32) must not   */
 /* exceed 65536 (DSV_ERR_INVALID otherwise; e.g. 8192 bf16 rows of 151936).  Calls that        */
 /* overlap on one device share that array and race; the stream must belong to the current     */
 /* device.  Same arguments and outputs as dsv_greedy_verify otherwise.                         */
