@@ -1925,6 +1925,7 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
   __shared__ int32_t s_cnt, s_nq;
   __shared__ uint32_t s_wlo;
   __shared__ float s_xtok;
+  __shared__ int32_t s_arg;  // the chunk's first argmax id, from the thread that holds it
   const dsv_verify_args& a = P.a;
   const int C = P.C;
   const int64_t r = blockIdx.x / C;
@@ -2091,8 +2092,12 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
       }
     }
   }
-  uint64_t mine = 0ull;
-  if (bu >= 0) {
+  // the chunk's max and the first vector holding it (the thread's first such vector, then the
+  // lowest vector index over the workgroup: vectors are id-ordered); the element within it is
+  // found by that vector's owner alone, which stores it with the statistics at the end
+  const uint64_t cbest =
+      block_max_u64<CT / WAVE>(bu >= 0 ? pack(key_of<DT>(m_t), v0 + (int64_t)bu * CT + tid) : 0ull, su);
+  if (cbest && (uint32_t)(unpack_id(cbest) - v0) % CT == (uint32_t)tid) {
     uint4 w = v[0];
 #pragma unroll
     for (int u = 1; u < CV; ++u)
@@ -2101,13 +2106,12 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
 #pragma unroll
     for (int e = n - 1; e >= 0; --e)
       if (vec_elem<DT>(w, e) == m_t) e0 = e;
-    mine = pack(key_of<DT>(m_t), (v0 + (int64_t)bu * CT + tid) * n + e0);
+    s_arg = unpack_id(cbest) * n + e0;
   }
   reg_fence(v);
-  const uint64_t cbest = block_max_u64<CT / WAVE>(mine, su);
   ChunkStat out;
   out.m = cbest ? value_of_key<DT>(unpack_key(cbest)) : -INFINITY;
-  out.arg = cbest ? unpack_id(cbest) : INT_MAX;
+  out.arg = INT_MAX;  // (stored from s_arg by its owner, at the end)
   out.s = 0.0;
   out.ncand = 0;
   out.tieq = 0;
@@ -2404,10 +2408,20 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
     }
     out.ncand = kk;
   }
-  if (tok_here) __syncthreads();  // (orders the owner's s_xtok before thread 0 in every mode)
+  // The statistics: thread 0 writes all but the argmax id and the draft token's value, which
+  // their owners store from their own LDS writes (no barrier: the fields are disjoint).
+  if (cbest && (uint32_t)(unpack_id(cbest) - v0) % CT == (uint32_t)tid) st->arg = s_arg;
+  if (tok_here && tid == (int)((tok - lo) / n) % CT) st->xtok = s_xtok;
   if (tid == 0) {
-    if (tok_here) out.xtok = s_xtok;
-    *st = out;
+    st->m = out.m;
+    st->s = out.s;
+    st->ncand = out.ncand;
+    st->tieq = out.tieq;
+    st->wlo = out.wlo;
+    st->kx = out.kx;
+    st->pad = 0;
+    if (!cbest) st->arg = INT_MAX;
+    if (!tok_here) st->xtok = 0.f;
     // The row merge's per-call state, written after the last load (a store ahead of the row's
     // parameter loads would turn those scalar loads into vector loads queued behind the
     // chunk's): its list of full-histogram rows, and the request's merged-row count and
