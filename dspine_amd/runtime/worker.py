@@ -60,24 +60,38 @@ def filter_target_probs(probs, sampling_info, t, bs, sampling_backend, normalize
     (``normalize``) renormalised; without a filter flag the input is returned as a view.
 
     The HIP row kernels take logits: log(p) at temperature 1 has softmax p / sum(p), which
-    selects the same support as p (the filter's cumulative masses see p / sum(p), equal to p
-    for a softmax row) and renormalises to the same distribution.  With ``normalize`` False the
-    kept entries are the input values themselves."""
-    need = any(bool(getattr(sampling_info, n, False))
-               for n in ("need_top_k_sampling", "need_top_p_sampling", "need_min_p_sampling"))
-    if not need:
+    renormalises to the same distribution; top-k and min-p (a ratio to the row's top p) select
+    the same ids.  The reference's top-p test compares the raw mass ranked ahead of an id with
+    top_p (:52-67; flashinfer's joint branch likewise, its min-p branch renormalises over the
+    top-k first), so each row runs as a request of its own with top_p divided by the row's
+    mass.  With ``normalize`` False the kept entries are the input values themselves."""
+    need_k = bool(getattr(sampling_info, "need_top_k_sampling", False))
+    need_p = bool(getattr(sampling_info, "need_top_p_sampling", False))
+    need_min_p = bool(getattr(sampling_info, "need_min_p_sampling", False))
+    if not (need_k or need_p or need_min_p):
         return probs.view(bs, t, -1)
     if sampling_backend not in ("pytorch", "flashinfer"):
         raise ValueError(f"DSPINE sampled verify: unsupported sampling backend {sampling_backend!r}")
     flat = probs.reshape(bs * t, -1)
     if flat.dtype != torch.float32:
         raise ValueError("filter_target_probs expects float32 probabilities")
-    info = SimpleNamespace(**{k: getattr(sampling_info, k) for k in (
-        "top_ks", "top_ps", "min_ps", "need_top_k_sampling", "need_top_p_sampling",
-        "need_min_p_sampling", "max_top_k") if hasattr(sampling_info, k)})
-    info.temperatures = torch.ones(bs, device=flat.device)
-    info.is_any_greedy = False
-    out = target_probs(torch.log(flat), info, bs=bs, T=t, sampling_backend=sampling_backend)
+    rows, dev = bs * t, flat.device
+
+    def per_row(x, dtype):  # a request's value for each of its t rows
+        return torch.repeat_interleave(torch.as_tensor(x, device=dev).reshape(-1).to(dtype), t)
+
+    top_ps = per_row(sampling_info.top_ps, torch.float32)
+    if need_p and not (sampling_backend == "flashinfer" and need_min_p):
+        mass = flat.sum(-1, dtype=torch.float64)
+        top_ps = torch.where(mass > 0, top_ps.double() / mass, top_ps.double()).float()
+    info = SimpleNamespace(
+        top_ks=per_row(sampling_info.top_ks, torch.int32), top_ps=top_ps,
+        min_ps=per_row(sampling_info.min_ps, torch.float32) if getattr(sampling_info, "min_ps", None) is not None
+        else None,
+        need_top_k_sampling=need_k, need_top_p_sampling=need_p, need_min_p_sampling=need_min_p,
+        max_top_k=getattr(sampling_info, "max_top_k", None),
+        temperatures=torch.ones(rows, device=dev), is_any_greedy=False)
+    out = target_probs(torch.log(flat), info, bs=rows, T=1, sampling_backend=sampling_backend)
     if not normalize:
         out = torch.where(out > 0, flat, torch.zeros((), device=flat.device))
     return out.view(bs, t, -1)

@@ -332,6 +332,34 @@ def test_filter_target_probs(device, normalize):
         assert torch.equal(got.cpu()[kept], probs.view(bs, T, V)[kept])
 
 
+@pytest.mark.parametrize("backend,min_p", [("pytorch", False), ("pytorch", True), ("flashinfer", False),
+                                           ("flashinfer", True)])
+def test_filter_target_probs_unnormalised_rows(device, backend, min_p):
+    """Rows whose mass is not 1 (runtime/worker.py:52-67, 473-508): the top-p test compares the
+    raw mass ranked ahead of an id with top_p -- a row of mass 0.7 under top-p 0.6 keeps ids
+    until 0.6 of raw mass (0.857 of its own) lies ahead; flashinfer's min-p branch renormalises
+    over the top-k first, so there only the renormalised row matters."""
+    from dspine_amd.runtime.worker import filter_target_probs
+
+    O = _O()
+    bs, T, V = 4, 2, 3001
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(bs * T, V, generator=g) * 2.0
+    mass = torch.tensor([0.7, 1.6, 0.35, 1.0, 0.9, 1.25, 0.5, 2.0])
+    probs = torch.softmax(logits.double(), -1).float() * mass.view(-1, 1)
+    # list rows (k 50), nucleus rows (no top-k; k 2000 with a cut) and the top-p values
+    info = W.sampling_info([1.0] * bs, [0, 50, 0, 2000], [0.6, 0.8, 0.9, 0.95],
+                           [0.0, 0.02, 0.0, 0.01] if min_p else None)
+    got = filter_target_probs(probs.to(device), W.info_to(info, device), T, bs, backend)
+    torch.cuda.synchronize()
+    ref = O.filter_target_probs(probs.clone(), info, T, bs, backend)
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
+    assert torch.equal(got.cpu() > 0, ref > 0)
+    if not (backend == "flashinfer" and min_p):  # the raw masses decide a different support here
+        unit = O.filter_target_probs((probs / probs.sum(-1, keepdim=True)).clone(), info, T, bs, backend)
+        assert not torch.equal(unit > 0, ref > 0)
+
+
 def test_softmax_temp(device):
     from dspine_amd.runtime.worker import SoftmaxTemp
 
