@@ -1964,9 +1964,13 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
   if (hist_ahead) {
     for (int i = tid; i < CHE / 32; i += CT) s_pb[i] = 0u;
     __syncthreads();
+    // (offsets into the chunk in 32-bit arithmetic: ids below lo wrap past the chunk's extent)
+    const uint32_t ext = (uint32_t)(hi - lo);
 #pragma unroll
-    for (int k = 0; k < HPRE; ++k)
-      if (hid[k] >= lo && hid[k] < hi) atomicOr(&s_pb[(hid[k] - lo) >> 5], 1u << ((hid[k] - lo) & 31));
+    for (int k = 0; k < HPRE; ++k) {
+      const uint32_t o = (uint32_t)hid[k] - (uint32_t)lo;
+      if (o < ext) atomicOr(&s_pb[o >> 5], 1u << (o & 31));
+    }
     __syncthreads();
   }
   int b = 0, s = 0;
@@ -2022,9 +2026,10 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
       for (int i = tid; i < CHE / 32; i += CT) s_pb[i] = 0u;
       __syncthreads();
       const int32_t* h = a.hist_ids + (int64_t)b * a.hist_len;
+      const uint32_t ext = (uint32_t)(hi - lo);
       for (int i = tid; i < a.hist_len; i += CT) {
-        const int64_t t = h[i];
-        if (t >= lo && t < hi) atomicOr(&s_pb[(t - lo) >> 5], 1u << ((t - lo) & 31));
+        const uint32_t o = (uint32_t)h[i] - (uint32_t)lo;
+        if (o < ext) atomicOr(&s_pb[o >> 5], 1u << (o & 31));
       }
       __syncthreads();
     }
@@ -3071,20 +3076,31 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
       for (int i = tid; i < nl; i += CT) lst[i] = P.lists[r * DSV_LIST_K + i];
       __syncthreads();
       for (int i = tid; i < nl; i += CT) {
-        const int64_t id = lst[i].id;
-        if (id >= lo && id < hi) atomicOr(&s_bm[(id - lo) >> 5], 1u << ((id - lo) & 31));
+        const uint32_t o = (uint32_t)lst[i].id - (uint32_t)lo;
+        if (o < (uint32_t)(hi - lo)) atomicOr(&s_bm[o >> 5], 1u << (o & 31));
       }
       __syncthreads();
     }
+    // chunk offsets in 32 bits; a vector's nonzero elements from one subtraction (greedy: the
+    // one-hot's offset, -1 for none) or one bitmap word (support lists), the values only then
+    const uint32_t ext = (uint32_t)(hi - lo);
+    const uint32_t oh = mode == M_GREEDY ? (uint32_t)rs.argmax - (uint32_t)lo : 0xFFFFFFFFu;
 #pragma unroll
     for (int u = 0; u < CV; ++u) {
-      const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
-      if (j0 >= hi) continue;
+      const uint32_t o0 = (uint32_t)((u * CT + tid) * n);
+      if (o0 >= ext) continue;
+      const int64_t j0 = lo + o0;
       float x[n];
 #pragma unroll
-      for (int e = 0; e < n; ++e) x[e] = mode == M_GREEDY && j0 + e == (int64_t)rs.argmax ? 1.f : 0.f;
-      if (mode == M_LIST) {
-        const uint32_t bits = (s_bm[(j0 - lo) >> 5] >> ((j0 - lo) & 31)) & ((1u << n) - 1u);
+      for (int e = 0; e < n; ++e) x[e] = 0.f;
+      if (mode == M_GREEDY) {
+        const uint32_t e1 = oh - o0;
+        if (e1 < (uint32_t)n) {
+#pragma unroll
+          for (int e = 0; e < n; ++e) x[e] = (uint32_t)e == e1 ? 1.f : 0.f;
+        }
+      } else if (mode == M_LIST) {
+        const uint32_t bits = (s_bm[o0 >> 5] >> (o0 & 31)) & ((1u << n) - 1u);
         if (bits) {
 #pragma unroll
           for (int e = 0; e < n; ++e) {
