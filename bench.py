@@ -98,25 +98,24 @@ def time_eager(step, steps, warmup, torch):
 
 
 def time_graph(step, steps, warmup, nbuf, torch):
-    """One graph holds one step on each logits copy; it is replayed until `steps` steps ran."""
+    """One graph holds all `steps` steps (the logits copies in turn), replayed once untimed and
+    once timed: the GPU idles ~9 us between two replays of a graph, which a graph of a few steps
+    would charge to every few steps."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(nbuf):
-            step(i)
-    for _ in range(2):
-        g.replay()
+        for i in range(steps):
+            step(i % nbuf)
+    g.replay()
     torch.cuda.synchronize()
-    replays = max(1, math.ceil(steps / nbuf))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(replays):
-        g.replay()
+    g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (replays * nbuf), g
+    return start.elapsed_time(end) / steps, g
 
 
 def copies(t, torch):
