@@ -54,40 +54,115 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust(E* logits, int64_t vocab
 // Eight consecutive elements a thread a step, 16-byte loads and stores (rows and value rows
 // 16-byte aligned); the row's last vocab % 8 elements one at a time.
 constexpr int ADJ_VEC = 8;
+// Eight bf16 values (one 16-byte vector) adjusted with their eight operands.
+template <typename E>
+__device__ __forceinline__ void adjust_vec8(uint4& w, const float (&s)[8], int32_t op) {
+  if constexpr (sizeof(E) == 2) {
+    uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lo = adjust_one(bf16_bits_to_f32(wp[k] & 0xFFFFu), s[2 * k], op);
+      const float hi = adjust_one(bf16_bits_to_f32(wp[k] >> 16), s[2 * k + 1], op);
+      wp[k] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+  }
+}
+// Up to ADJ_ROWS consecutive rows a workgroup: their logits vectors go out together, and a
+// request's eight operands are read again only when the next row belongs to another request
+// (compact rows of one request are consecutive).
+constexpr int ADJ_ROWS = 4;
 template <typename E>
 __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t vocab, int64_t row_stride,
-                                                           const int64_t* row_to_request, int32_t rows_per_request,
-                                                           int32_t op, const float* values, int64_t values_stride) {
-  const int64_t r = blockIdx.y;
-  const int64_t req = request_of_row(row_to_request, rows_per_request, r);
-  E* row = logits + r * row_stride;
+                                                           int64_t rows, const int64_t* row_to_request,
+                                                           int32_t rows_per_request, int32_t op, const float* values,
+                                                           int64_t values_stride) {
+  constexpr int NV = sizeof(E) == 2 ? 1 : 2;  // 16-byte vectors a row holds of eight values
+  const int64_t ra = (int64_t)blockIdx.y * ADJ_ROWS;
+  int64_t req[ADJ_ROWS];
+#pragma unroll
+  for (int t = 0; t < ADJ_ROWS; ++t) req[t] = ra + t < rows ? request_of_row(row_to_request, rows_per_request, ra + t) : -1;
+  const int64_t step = (int64_t)gridDim.x * ADJ_THREADS * ADJ_VEC;
+  for (int64_t j = ((int64_t)blockIdx.x * ADJ_THREADS + threadIdx.x) * ADJ_VEC; j < vocab; j += step) {
+    if (j + ADJ_VEC <= vocab) {
+      uint4 w[ADJ_ROWS][NV];
+#pragma unroll
+      for (int t = 0; t < ADJ_ROWS; ++t)
+        if (req[t] >= 0)
+#pragma unroll
+          for (int h = 0; h < NV; ++h)
+            w[t][h] = *reinterpret_cast<const uint4*>(logits + (ra + t) * row_stride + j + h * (16 / sizeof(E)));
+      float s[8];
+      int64_t cur = -1;
+#pragma unroll
+      for (int t = 0; t < ADJ_ROWS; ++t) {
+        if (req[t] < 0) continue;
+        if (req[t] != cur) {
+          const float* v = values + req[t] * values_stride + j;
+          const float4 s0 = *reinterpret_cast<const float4*>(v), s1 = *reinterpret_cast<const float4*>(v + 4);
+          s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w;
+          s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+          cur = req[t];
+        }
+        if constexpr (sizeof(E) == 2) {
+          adjust_vec8<E>(w[t][0], s, op);
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float* x = reinterpret_cast<float*>(&w[t][h]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = adjust_one(x[e], s[4 * h + e], op);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < NV; ++h)
+          *reinterpret_cast<uint4*>(logits + (ra + t) * row_stride + j + h * (16 / sizeof(E))) = w[t][h];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < ADJ_ROWS; ++t) {
+        if (req[t] < 0) continue;
+        E* row = logits + (ra + t) * row_stride;
+        const float* v = values + req[t] * values_stride;
+        for (int64_t k = j; k < vocab; ++k) elem_store(row + k, adjust_one(elem_load<E>(row + k), v[k], op));
+      }
+    }
+  }
+}
+
+// The contiguous layout (rows_per_request rows a request, no row map): a thread's eight values
+// are read once and applied to each of the request's rows, ADJ_ROWS rows' loads in flight at a
+// time -- a request's value row crosses HBM once instead of once per row.
+template <typename E>
+__global__ __launch_bounds__(ADJ_THREADS) void k_adjust_req(E* logits, int64_t vocab, int64_t row_stride,
+                                                           int64_t rows, int32_t rows_per_request, int32_t op,
+                                                           const float* values, int64_t values_stride) {
+  static_assert(sizeof(E) == 2, "bf16 rows");
+  const int64_t req = blockIdx.y;
+  const int64_t r0 = req * rows_per_request;
+  const int64_t r1 = r0 + rows_per_request < rows ? r0 + rows_per_request : rows;
   const float* v = values + req * values_stride;
   const int64_t step = (int64_t)gridDim.x * ADJ_THREADS * ADJ_VEC;
   for (int64_t j = ((int64_t)blockIdx.x * ADJ_THREADS + threadIdx.x) * ADJ_VEC; j < vocab; j += step) {
     if (j + ADJ_VEC <= vocab) {
       const float4 s0 = *reinterpret_cast<const float4*>(v + j), s1 = *reinterpret_cast<const float4*>(v + j + 4);
       const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-      if constexpr (sizeof(E) == 2) {
-        uint4 w = *reinterpret_cast<const uint4*>(row + j);
-        uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
+      for (int64_t rb = r0; rb < r1; rb += ADJ_ROWS) {
+        uint4 w[ADJ_ROWS];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float lo = adjust_one(bf16_bits_to_f32(wp[k] & 0xFFFFu), s[2 * k], op);
-          const float hi = adjust_one(bf16_bits_to_f32(wp[k] >> 16), s[2 * k + 1], op);
-          wp[k] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+        for (int t = 0; t < ADJ_ROWS; ++t)
+          if (rb + t < r1) w[t] = *reinterpret_cast<const uint4*>(logits + (rb + t) * row_stride + j);
+#pragma unroll
+        for (int t = 0; t < ADJ_ROWS; ++t) {
+          if (rb + t < r1) {
+            adjust_vec8<E>(w[t], s, op);
+            *reinterpret_cast<uint4*>(logits + (rb + t) * row_stride + j) = w[t];
+          }
         }
-        *reinterpret_cast<uint4*>(row + j) = w;
-      } else {
-        float4 x0 = *reinterpret_cast<const float4*>(row + j), x1 = *reinterpret_cast<const float4*>(row + j + 4);
-        x0 = make_float4(adjust_one(x0.x, s[0], op), adjust_one(x0.y, s[1], op), adjust_one(x0.z, s[2], op),
-                         adjust_one(x0.w, s[3], op));
-        x1 = make_float4(adjust_one(x1.x, s[4], op), adjust_one(x1.y, s[5], op), adjust_one(x1.z, s[6], op),
-                         adjust_one(x1.w, s[7], op));
-        *reinterpret_cast<float4*>(row + j) = x0;
-        *reinterpret_cast<float4*>(row + j + 4) = x1;
       }
     } else {
-      for (int64_t k = j; k < vocab; ++k) elem_store(row + k, adjust_one(elem_load<E>(row + k), v[k], op));
+      for (int64_t r = r0; r < r1; ++r)
+        for (int64_t k = j; k < vocab; ++k)
+          elem_store(logits + r * row_stride + k, adjust_one(elem_load<E>(logits + r * row_stride + k), v[k], op));
     }
   }
 }
@@ -755,16 +830,21 @@ extern "C" int dsv_adjust_logits(void* logits, int32_t logits_dtype, int64_t row
   const int64_t esize = logits_dtype == DSV_BF16 ? 2 : 4;
   const bool vec = (uintptr_t)logits % 16 == 0 && (row_stride * esize) % 16 == 0 && (uintptr_t)values % 16 == 0 &&
                    values_stride % 4 == 0;
-  if (vec) {
+  if (vec && logits_dtype == DSV_BF16 && !row_to_request && rows_per_request > 1) {
+    const int64_t bx = (vocab + ADJ_THREADS * ADJ_VEC - 1) / (ADJ_THREADS * ADJ_VEC);
+    const int64_t nreq = (rows + rows_per_request - 1) / rows_per_request;
+    hipLaunchKernelGGL(k_adjust_req<uint16_t>, dim3((unsigned)bx, (unsigned)nreq), dim3(ADJ_THREADS), 0, stream,
+                       (uint16_t*)logits, vocab, row_stride, rows, rows_per_request, op, values, values_stride);
+  } else if (vec) {
     int64_t bx = (vocab + ADJ_THREADS * ADJ_VEC - 1) / (ADJ_THREADS * ADJ_VEC);
     if (bx > 64) bx = 64;
-    const dim3 grid((unsigned)bx, (unsigned)rows);
+    const dim3 grid((unsigned)bx, (unsigned)((rows + ADJ_ROWS - 1) / ADJ_ROWS));
     if (logits_dtype == DSV_BF16)
       hipLaunchKernelGGL(k_adjust_vec<uint16_t>, grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits, vocab,
-                         row_stride, row_to_request, rows_per_request, op, values, values_stride);
+                         row_stride, rows, row_to_request, rows_per_request, op, values, values_stride);
     else
       hipLaunchKernelGGL(k_adjust_vec<float>, grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab, row_stride,
-                         row_to_request, rows_per_request, op, values, values_stride);
+                         rows, row_to_request, rows_per_request, op, values, values_stride);
   } else {
     const dim3 grid = row_grid(rows, vocab);
     if (logits_dtype == DSV_BF16)

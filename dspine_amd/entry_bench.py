@@ -110,13 +110,16 @@ def main():
     us = timed(chain, args.calls)
     line("chain_on_probs", us, bs * V * 4, requests=bs, mean_accept=round(float(outs[0].float().mean()), 2))
 
-    # a14: an additive penalty row per request applied to the logits in place (on a copy)
+    # a14: an additive penalty row per request applied to the logits in place (on a copy): the
+    # full block as [bs, T, V] (sampling/compact.py:116) and compact rows with a row map (:99)
     work = logits.clone()
     pen = torch.randn((bs, V), device=dev) * 0.1
     info_pen = SimpleNamespace(acc_additive_penalties=pen)
+    us = timed(lambda: adjust_logits(work.view(bs, T, V), info_pen, None), args.calls)
+    line("adjust_logits", us, n_logits * 4 + bs * V * 4, shape=[bs, T, V], op="additive")
     rtr = torch.arange(rows, device=dev) // T
     us = timed(lambda: adjust_logits(work, info_pen, rtr), args.calls)
-    line("adjust_logits", us, n_logits * 4 + bs * V * 4, shape=[rows, V], op="additive")
+    line("adjust_logits_row_map", us, n_logits * 4 + bs * V * 4, shape=[rows, V], op="additive")
 
     us = timed(lambda: adjust_history(work, d["hist_ids"], d["presence"], d["repetition"], rtr), args.calls)
     line("adjust_history", us, None, history=int(d["hist_ids"].shape[1]))

@@ -470,6 +470,31 @@ def test_adjust_logits_bitexact(device, dtype, mapped):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_adjust_logits_request_rows_padded(device, dtype):
+    """The [bs, T, V] layout with 7 rows a request (a partial group of the per-request pass's
+    four rows), a vocab that is a multiple of 4 but not of 8 (the rows' four-value tails; the
+    value rows stay 16-byte aligned) and 16-byte aligned logits rows on a padded stride:
+    bit-exact against the oracle, padding untouched."""
+    from types import SimpleNamespace
+
+    from dspine_amd.sampling.compact import adjust_logits
+
+    O = _O()
+    g = torch.Generator().manual_seed(23)
+    bs, T, V, Vp = 3, 7, 50020, 50024
+    full = (torch.randn(bs * T, Vp, generator=g) * 3).to(dtype)
+    add = torch.randn(bs, V, generator=g) * 0.2
+    scl = 1 + torch.rand(bs, V, generator=g)
+    for info in (SimpleNamespace(acc_additive_penalties=add), SimpleNamespace(acc_scaling_penalties=scl)):
+        ref = full.clone()
+        O.adjust_logits(ref[:, :V].view(bs, T, V), info, None)
+        got = full.to(device)
+        adjust_logits(got[:, :V].view(bs, T, V), info, None)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_logits_padding(device, dtype):
     """tests/test_release.py:45-67: rows [0, -inf, ...]."""
     from dspine_amd.sampling.padding import logits_padding
