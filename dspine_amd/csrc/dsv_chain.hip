@@ -311,9 +311,9 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
 // scanned, then the thread holding it.  Dense P subtracts the clamped q of the last lane with
 // an id; packed P the clamped q summed over the lanes with its id (accept.py:163-166,186-193).
 // ---------------------------------------------------------------------------------------
-constexpr int CH_THREADS = 512;
+constexpr int CH_THREADS = 1024;                 // (sixteen waves: the loads in flight of one CU)
 constexpr int CH_NW = CH_THREADS / WAVE;
-constexpr int CH_E = 8;                          // consecutive ids a thread per tile
+constexpr int CH_E = 4;                          // consecutive ids a thread per tile
 constexpr int CH_TILE = CH_THREADS * CH_E;       // 4096
 constexpr int CH_TILES_MAX = 128;                // vocab <= 524288
 constexpr int CH_PACK_MAX = 64;                  // packed capacity handled by one wave
@@ -397,9 +397,22 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
       if (a.dense_q) {
         if (tok_ok) q = a.dense_q[((int64_t)b * (T - 1) + step - 1) * a.q_stride + tok];
       } else {
+        // the lanes holding the token, in lane order; sixteen lanes' ids and values loaded
+        // together (one memory round trip per sixteen lanes, not per lane)
         const int64_t qi = ((int64_t)b * (T - 1) + step - 1) * a.K;
-        for (int l = 0; l < a.K; ++l)  // the lanes holding the token, in lane order
-          if (load_index(a.q_ids, a.q_ids_i64, qi + l) == tok) q += a.q_values[qi + l];
+        for (int l0 = 0; l0 < a.K; l0 += 16) {
+          int64_t id[16];
+          float qv[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            const bool in = l0 + u < a.K;
+            id[u] = in ? load_index(a.q_ids, a.q_ids_i64, qi + l0 + u) : -1;
+            qv[u] = in ? a.q_values[qi + l0 + u] : 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (id[u] == tok) q += qv[u];
+        }
       }
       const float coin = a.uniforms[(int64_t)b * (T - 1) + step - 1];
       ok = q > 0.f && q <= 1.f && coin * q < p;
@@ -520,49 +533,76 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
     bool pure = all;
     double mass = 0.0;
     const int wid = tid / WAVE;
-    // P's eight values of this thread in tile t (16-byte loads when the rows are aligned)
+    // P's CH_E values of this thread in tile t (16-byte loads when the rows are aligned)
     const bool vec = a.p_stride % 4 == 0 && (uintptr_t)a.dense_p % 16 == 0;
     auto fetch = [&](int t, float (&x)[CH_E]) {
       const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
       const float* pr = a.dense_p + row * a.p_stride;
       if (vec && j0 + CH_E <= V) {
-        const float4 u0 = *reinterpret_cast<const float4*>(pr + j0), u1 = *reinterpret_cast<const float4*>(pr + j0 + 4);
-        x[0] = u0.x; x[1] = u0.y; x[2] = u0.z; x[3] = u0.w; x[4] = u1.x; x[5] = u1.y; x[6] = u1.z; x[7] = u1.w;
+#pragma unroll
+        for (int h = 0; h < CH_E / 4; ++h) {
+          const float4 u = *reinterpret_cast<const float4*>(pr + j0 + 4 * h);
+          x[4 * h] = u.x; x[4 * h + 1] = u.y; x[4 * h + 2] = u.z; x[4 * h + 3] = u.w;
+        }
       } else {
 #pragma unroll
         for (int e = 0; e < CH_E; ++e) x[e] = j0 + e < V ? pr[j0 + e] : 0.f;
       }
     };
     for (int pass = 0; pass < 2; ++pass) {
-      // Each wave's part of every tile's mass, the next tile's loads in flight; then one
-      // barrier and the tiles summed over the waves in wave order (the block sum's order).
-      const bool plain = !pure && !a.dense_q;  // sparse q: P here, the q ids' reductions after
-      float xn[CH_E];
-      if (plain) fetch(0, xn);
-      for (int t = 0; t < ntiles; ++t) {
-        const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
-        double w = 0.0;
-        if (plain) {
-          float x[CH_E];
+      // Tile masses.  Without a dense q the weights are P itself (the residual's reductions at
+      // the sparse q ids are taken after, per tile) and each wave sums whole tiles; with a dense
+      // q every wave takes its part of every tile, summed over the waves in wave order after
+      // one barrier.
+      const bool direct = !a.dense_q;
+      const bool plain = direct && !pure;  // sparse q: P here, the q ids' reductions after
+      if (direct) {
+        // wave w sums whole tiles (w, w + CH_NW, ...), lane l the tile's float4s l, l + 64, ...
+        // (coalesced, sixteen loads in flight); four partial sums a lane (independent chains of
+        // float64 additions), then one wave reduction a tile
+        constexpr int NQ = CH_TILE / 4 / WAVE;  // float4s a lane per tile
+        const float den = a.denominator ? a.denominator[row] : 1.f;
+        const float* pr = a.dense_p + row * a.p_stride;
+        for (int t = wid; t < ntiles; t += CH_NW) {
+          const int64_t tlo = (int64_t)t * CH_TILE;
+          double w = 0.0;
+          if (vec && tlo + CH_TILE <= V) {
+            float4 xb[NQ];
 #pragma unroll
-          for (int e = 0; e < CH_E; ++e) x[e] = xn[e];
-          if (t + 1 < ntiles) fetch(t + 1, xn);
-          const float den = a.denominator ? a.denominator[row] : 1.f;
+            for (int i = 0; i < NQ; ++i) xb[i] = *reinterpret_cast<const float4*>(pr + tlo + (int64_t)(i * WAVE + lane) * 4);
+            double w4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-          for (int e = 0; e < CH_E; ++e)
-            if (j0 + e < V) w += (double)(a.denominator ? x[e] / den : x[e]);
-        } else {
+            for (int i = 0; i < NQ; ++i) {
+              const float* x = reinterpret_cast<const float*>(&xb[i]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w4[e] += (double)(a.denominator ? x[e] / den : x[e]);
+            }
+            w = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+          } else {
+            for (int64_t j = tlo + lane; j < tlo + CH_TILE && j < V; j += WAVE)
+              w += (double)(a.denominator ? pr[j] / den : pr[j]);
+          }
+          w = wave_sum(w);
+          if (lane == 0) sh.tile_wave[t * CH_NW] = w;
+        }
+      } else {
+        for (int t = 0; t < ntiles; ++t) {
+          const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
+          double w = 0.0;
 #pragma unroll
           for (int e = 0; e < CH_E; ++e)
             if (j0 + e < V) w += chain_weight(a, row, b, acc, j0 + e, pure, sh);
+          w = wave_sum(w);
+          if (lane == 0) sh.tile_wave[t * CH_NW + wid] = w;
         }
-        w = wave_sum(w);
-        if (lane == 0) sh.tile_wave[t * CH_NW + wid] = w;
       }
       __syncthreads();
       for (int t = tid; t < ntiles; t += CH_THREADS) {
         double w = 0.0;
-        for (int i = 0; i < CH_NW; ++i) w += sh.tile_wave[t * CH_NW + i];
+        if (direct)
+          w = sh.tile_wave[t * CH_NW];
+        else
+          for (int i = 0; i < CH_NW; ++i) w += sh.tile_wave[t * CH_NW + i];
         if (plain)  // sparse q: the tile's reductions at its q ids
           for (int l = 0; l < a.K; ++l)
             if (sh.qlast[l] && sh.qid[l] / CH_TILE == t) w -= sh.qd[l];
@@ -605,10 +645,31 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
       const int64_t j0 = (int64_t)tile * CH_TILE + (int64_t)tid * CH_E;
       double w[CH_E];
       double wt = 0.0;
+      if (!a.dense_q) {
+        // P from one vector load, then the residual at the sparse q ids inside this thread's
+        // eight (the last lane with an id carries its q)
+        float x[CH_E];
+        fetch(tile, x);
+        const float den = a.denominator ? a.denominator[row] : 1.f;
 #pragma unroll
-      for (int e = 0; e < CH_E; ++e) {
-        w[e] = j0 + e < V ? chain_weight(a, row, b, acc, j0 + e, pu, sh) : 0.0;
-        wt += w[e];
+        for (int e = 0; e < CH_E; ++e) w[e] = j0 + e < V ? (double)(a.denominator ? x[e] / den : x[e]) : 0.0;
+        if (!pu)
+          for (int l = 0; l < a.K; ++l) {
+            const uint64_t o = (uint64_t)(sh.qid[l] - j0);
+            if (sh.qlast[l] && o < (uint64_t)CH_E) {
+#pragma unroll
+              for (int e = 0; e < CH_E; ++e)
+                if ((uint64_t)e == o) w[e] = fmax(w[e] - (double)sh.qc[l], 0.0);
+            }
+          }
+#pragma unroll
+        for (int e = 0; e < CH_E; ++e) wt += w[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < CH_E; ++e) {
+          w[e] = j0 + e < V ? chain_weight(a, row, b, acc, j0 + e, pu, sh) : 0.0;
+          wt += w[e];
+        }
       }
       double tlo, thi;
       block_tiles<CH_NW>(wt, sh.red_d, tlo, thi);
