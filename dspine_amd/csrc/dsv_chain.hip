@@ -7,6 +7,8 @@
 // and kernels/dspine.py:616-772.
 #include <string.h>
 
+#include <type_traits>
+
 #include "dsv_device.h"
 
 namespace dsv {
@@ -559,32 +561,42 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
       if (direct) {
         // wave w sums whole tiles (w, w + CH_NW, ...), lane l the tile's float4s l, l + 64, ...
         // (coalesced, sixteen loads in flight); four partial sums a lane (independent chains of
-        // float64 additions), then one wave reduction a tile
+        // float64 additions), then one wave reduction a tile.  RAW rows (a denominator) and the
+        // others are separate instantiations: a select in the loop would compute the IEEE
+        // division for every value.
         constexpr int NQ = CH_TILE / 4 / WAVE;  // float4s a lane per tile
-        const float den = a.denominator ? a.denominator[row] : 1.f;
         const float* pr = a.dense_p + row * a.p_stride;
-        for (int t = wid; t < ntiles; t += CH_NW) {
-          const int64_t tlo = (int64_t)t * CH_TILE;
-          double w = 0.0;
-          if (vec && tlo + CH_TILE <= V) {
-            float4 xb[NQ];
+        auto sum_tiles = [&](auto raw_tag) {
+          constexpr bool RAW = decltype(raw_tag)::value;
+          const float den = RAW ? a.denominator[row] : 1.f;
+          for (int t = wid; t < ntiles; t += CH_NW) {
+            const int64_t tlo = (int64_t)t * CH_TILE;
+            double w = 0.0;
+            if (vec && tlo + CH_TILE <= V) {
+              float4 xb[NQ];
 #pragma unroll
-            for (int i = 0; i < NQ; ++i) xb[i] = *reinterpret_cast<const float4*>(pr + tlo + (int64_t)(i * WAVE + lane) * 4);
-            double w4[4] = {0.0, 0.0, 0.0, 0.0};
+              for (int i = 0; i < NQ; ++i)
+                xb[i] = *reinterpret_cast<const float4*>(pr + tlo + (int64_t)(i * WAVE + lane) * 4);
+              double w4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-            for (int i = 0; i < NQ; ++i) {
-              const float* x = reinterpret_cast<const float*>(&xb[i]);
+              for (int i = 0; i < NQ; ++i) {
+                const float* x = reinterpret_cast<const float*>(&xb[i]);
 #pragma unroll
-              for (int e = 0; e < 4; ++e) w4[e] += (double)(a.denominator ? x[e] / den : x[e]);
+                for (int e = 0; e < 4; ++e) w4[e] += (double)(RAW ? x[e] / den : x[e]);
+              }
+              w = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+            } else {
+              for (int64_t j = tlo + lane; j < tlo + CH_TILE && j < V; j += WAVE)
+                w += (double)(RAW ? pr[j] / den : pr[j]);
             }
-            w = (w4[0] + w4[1]) + (w4[2] + w4[3]);
-          } else {
-            for (int64_t j = tlo + lane; j < tlo + CH_TILE && j < V; j += WAVE)
-              w += (double)(a.denominator ? pr[j] / den : pr[j]);
+            w = wave_sum(w);
+            if (lane == 0) sh.tile_wave[t * CH_NW] = w;
           }
-          w = wave_sum(w);
-          if (lane == 0) sh.tile_wave[t * CH_NW] = w;
-        }
+        };
+        if (a.denominator)
+          sum_tiles(std::true_type{});
+        else
+          sum_tiles(std::false_type{});
       } else {
         for (int t = 0; t < ntiles; ++t) {
           const int64_t j0 = (int64_t)t * CH_TILE + (int64_t)tid * CH_E;
@@ -650,9 +662,13 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
         // eight (the last lane with an id carries its q)
         float x[CH_E];
         fetch(tile, x);
-        const float den = a.denominator ? a.denominator[row] : 1.f;
+        if (a.denominator) {  // (a branch: a select would divide every value)
+          const float den = a.denominator[row];
 #pragma unroll
-        for (int e = 0; e < CH_E; ++e) w[e] = j0 + e < V ? (double)(a.denominator ? x[e] / den : x[e]) : 0.0;
+          for (int e = 0; e < CH_E; ++e) x[e] = x[e] / den;
+        }
+#pragma unroll
+        for (int e = 0; e < CH_E; ++e) w[e] = j0 + e < V ? (double)x[e] : 0.0;
         if (!pu)
           for (int l = 0; l < a.K; ++l) {
             const uint64_t o = (uint64_t)(sh.qid[l] - j0);
