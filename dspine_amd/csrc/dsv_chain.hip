@@ -57,14 +57,14 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust(E* logits, int64_t vocab
 // 16-byte aligned); the row's last vocab % 8 elements one at a time.
 constexpr int ADJ_VEC = 8;
 // Eight bf16 values (one 16-byte vector) adjusted with their eight operands.
-template <typename E>
-__device__ __forceinline__ void adjust_vec8(uint4& w, const float (&s)[8], int32_t op) {
+template <typename E, int OP>
+__device__ __forceinline__ void adjust_vec8(uint4& w, const float (&s)[8]) {
   if constexpr (sizeof(E) == 2) {
     uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float lo = adjust_one(bf16_bits_to_f32(wp[k] & 0xFFFFu), s[2 * k], op);
-      const float hi = adjust_one(bf16_bits_to_f32(wp[k] >> 16), s[2 * k + 1], op);
+      const float lo = adjust_one(bf16_bits_to_f32(wp[k] & 0xFFFFu), s[2 * k], OP);
+      const float hi = adjust_one(bf16_bits_to_f32(wp[k] >> 16), s[2 * k + 1], OP);
       wp[k] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
     }
   }
@@ -73,10 +73,10 @@ __device__ __forceinline__ void adjust_vec8(uint4& w, const float (&s)[8], int32
 // request's eight operands are read again only when the next row belongs to another request
 // (compact rows of one request are consecutive).
 constexpr int ADJ_ROWS = 4;
-template <typename E>
+template <typename E, int OP>
 __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t vocab, int64_t row_stride,
                                                            int64_t rows, const int64_t* row_to_request,
-                                                           int32_t rows_per_request, int32_t op, const float* values,
+                                                           int32_t rows_per_request, const float* values,
                                                            int64_t values_stride) {
   constexpr int NV = sizeof(E) == 2 ? 1 : 2;  // 16-byte vectors a row holds of eight values
   const int64_t ra = (int64_t)blockIdx.y * ADJ_ROWS;
@@ -106,13 +106,13 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t v
           cur = req[t];
         }
         if constexpr (sizeof(E) == 2) {
-          adjust_vec8<E>(w[t][0], s, op);
+          adjust_vec8<E, OP>(w[t][0], s);
         } else {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             float* x = reinterpret_cast<float*>(&w[t][h]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = adjust_one(x[e], s[4 * h + e], op);
+            for (int e = 0; e < 4; ++e) x[e] = adjust_one(x[e], s[4 * h + e], OP);
           }
         }
 #pragma unroll
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t v
         if (req[t] < 0) continue;
         E* row = logits + (ra + t) * row_stride;
         const float* v = values + req[t] * values_stride;
-        for (int64_t k = j; k < vocab; ++k) elem_store(row + k, adjust_one(elem_load<E>(row + k), v[k], op));
+        for (int64_t k = j; k < vocab; ++k) elem_store(row + k, adjust_one(elem_load<E>(row + k), v[k], OP));
       }
     }
   }
@@ -134,9 +134,9 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_vec(E* logits, int64_t v
 // The contiguous layout (rows_per_request rows a request, no row map): a thread's eight values
 // are read once and applied to each of the request's rows, ADJ_ROWS rows' loads in flight at a
 // time -- a request's value row crosses HBM once instead of once per row.
-template <typename E>
+template <typename E, int OP>
 __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_req(E* logits, int64_t vocab, int64_t row_stride,
-                                                           int64_t rows, int32_t rows_per_request, int32_t op,
+                                                           int64_t rows, int32_t rows_per_request,
                                                            const float* values, int64_t values_stride) {
   static_assert(sizeof(E) == 2, "bf16 rows");
   const int64_t req = blockIdx.y;
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_req(E* logits, int64_t v
 #pragma unroll
         for (int t = 0; t < ADJ_ROWS; ++t) {
           if (rb + t < r1) {
-            adjust_vec8<E>(w[t], s, op);
+            adjust_vec8<E, OP>(w[t], s);
             *reinterpret_cast<uint4*>(logits + (rb + t) * row_stride + j) = w[t];
           }
         }
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(ADJ_THREADS) void k_adjust_req(E* logits, int64_t v
     } else {
       for (int64_t r = r0; r < r1; ++r)
         for (int64_t k = j; k < vocab; ++k)
-          elem_store(logits + r * row_stride + k, adjust_one(elem_load<E>(logits + r * row_stride + k), v[k], op));
+          elem_store(logits + r * row_stride + k, adjust_one(elem_load<E>(logits + r * row_stride + k), v[k], OP));
     }
   }
 }
@@ -910,18 +910,31 @@ extern "C" int dsv_adjust_logits(void* logits, int32_t logits_dtype, int64_t row
   if (vec && logits_dtype == DSV_BF16 && !row_to_request && rows_per_request > 1) {
     const int64_t bx = (vocab + ADJ_THREADS * ADJ_VEC - 1) / (ADJ_THREADS * ADJ_VEC);
     const int64_t nreq = (rows + rows_per_request - 1) / rows_per_request;
-    hipLaunchKernelGGL(k_adjust_req<uint16_t>, dim3((unsigned)bx, (unsigned)nreq), dim3(ADJ_THREADS), 0, stream,
-                       (uint16_t*)logits, vocab, row_stride, rows, rows_per_request, op, values, values_stride);
+    // (the op as a template argument: a run-time select would compute the division of every value)
+    const dim3 grid((unsigned)bx, (unsigned)nreq);
+    if (op == DSV_ADJ_ADD)
+      hipLaunchKernelGGL((k_adjust_req<uint16_t, DSV_ADJ_ADD>), grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits,
+                         vocab, row_stride, rows, rows_per_request, values, values_stride);
+    else
+      hipLaunchKernelGGL((k_adjust_req<uint16_t, DSV_ADJ_SCALE>), grid, dim3(ADJ_THREADS), 0, stream,
+                         (uint16_t*)logits, vocab, row_stride, rows, rows_per_request, values, values_stride);
   } else if (vec) {
     int64_t bx = (vocab + ADJ_THREADS * ADJ_VEC - 1) / (ADJ_THREADS * ADJ_VEC);
     if (bx > 64) bx = 64;
     const dim3 grid((unsigned)bx, (unsigned)((rows + ADJ_ROWS - 1) / ADJ_ROWS));
-    if (logits_dtype == DSV_BF16)
-      hipLaunchKernelGGL(k_adjust_vec<uint16_t>, grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits, vocab,
-                         row_stride, rows, row_to_request, rows_per_request, op, values, values_stride);
+    if (logits_dtype == DSV_BF16 && op == DSV_ADJ_ADD)
+      hipLaunchKernelGGL((k_adjust_vec<uint16_t, DSV_ADJ_ADD>), grid, dim3(ADJ_THREADS), 0, stream, (uint16_t*)logits,
+                         vocab, row_stride, rows, row_to_request, rows_per_request, values, values_stride);
+    else if (logits_dtype == DSV_BF16)
+      hipLaunchKernelGGL((k_adjust_vec<uint16_t, DSV_ADJ_SCALE>), grid, dim3(ADJ_THREADS), 0, stream,
+                         (uint16_t*)logits, vocab, row_stride, rows, row_to_request, rows_per_request, values,
+                         values_stride);
+    else if (op == DSV_ADJ_ADD)
+      hipLaunchKernelGGL((k_adjust_vec<float, DSV_ADJ_ADD>), grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab,
+                         row_stride, rows, row_to_request, rows_per_request, values, values_stride);
     else
-      hipLaunchKernelGGL(k_adjust_vec<float>, grid, dim3(ADJ_THREADS), 0, stream, (float*)logits, vocab, row_stride,
-                         rows, row_to_request, rows_per_request, op, values, values_stride);
+      hipLaunchKernelGGL((k_adjust_vec<float, DSV_ADJ_SCALE>), grid, dim3(ADJ_THREADS), 0, stream, (float*)logits,
+                         vocab, row_stride, rows, row_to_request, rows_per_request, values, values_stride);
   } else {
     const dim3 grid = row_grid(rows, vocab);
     if (logits_dtype == DSV_BF16)
