@@ -233,6 +233,7 @@ __global__ void k_window_index(const void* qo, int32_t qo_i64, int32_t T, int64_
 // ---------------------------------------------------------------------------------------
 constexpr int CMP_THREADS = 512;
 constexpr int CMP_E = 8;  // consecutive ids a thread per tile
+constexpr int CMP_AHEAD = 4;  // tiles whose loads are in flight
 
 __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_t vocab, int64_t row_stride,
                                                           int32_t capacity, int32_t* ids, float* values,
@@ -246,15 +247,17 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
   const float* row = p + r * row_stride;
   int32_t* oid = ids + r * capacity;
   float* oval = values + r * capacity;
-  const bool vec = (uintptr_t)row % 16 == 0;  // (CMP_E = 8 ids a thread: two 16-byte loads)
+  const bool vec = (uintptr_t)row % 16 == 0;  // (CMP_E ids a thread: 16-byte loads)
   if (tid == 0) s_bad = 0;
-  // a tile's eight values of this thread; the next tile's loads are in flight while a tile is
-  // counted and written
+  // a tile's CMP_E values of this thread
   auto fetch = [&](int64_t t0, float (&x)[CMP_E]) {
     const int64_t j0 = t0 + (int64_t)tid * CMP_E;
     if (vec && j0 + CMP_E <= vocab) {
-      const float4 a = *reinterpret_cast<const float4*>(row + j0), b = *reinterpret_cast<const float4*>(row + j0 + 4);
-      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+      for (int h = 0; h < CMP_E / 4; ++h) {
+        const float4 u = *reinterpret_cast<const float4*>(row + j0 + 4 * h);
+        x[4 * h] = u.x; x[4 * h + 1] = u.y; x[4 * h + 2] = u.z; x[4 * h + 3] = u.w;
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < CMP_E; ++e) x[e] = j0 + e < vocab ? row[j0 + e] : 0.f;
@@ -262,35 +265,46 @@ __global__ __launch_bounds__(CMP_THREADS) void k_compress(const float* p, int64_
   };
   int64_t total = 0;  // kept ids before the current tile
   bool bad = false;
-  float xn[CMP_E];
-  fetch(0, xn);
-  for (int64_t t0 = 0; t0 < vocab; t0 += TILE) {
-    float x[CMP_E];
+  // CMP_AHEAD tiles' loads in flight: a ring of registers, the tile loop unrolled by its size so
+  // that every slot index is static; a slot is refilled with the tile CMP_AHEAD further on as
+  // soon as its values are taken
+  float xr[CMP_AHEAD][CMP_E];
 #pragma unroll
-    for (int e = 0; e < CMP_E; ++e) x[e] = xn[e];
-    if (t0 + TILE < vocab) fetch(t0 + TILE, xn);
-    const int64_t j0 = t0 + (int64_t)tid * CMP_E;
-    int32_t cnt = 0;
+  for (int d = 0; d < CMP_AHEAD; ++d)
+    if ((int64_t)d * TILE < vocab) fetch((int64_t)d * TILE, xr[d]);
+  bool done = false;
+  for (int64_t tg = 0; tg < vocab && !done; tg += CMP_AHEAD * TILE) {
 #pragma unroll
-    for (int e = 0; e < CMP_E; ++e) {
-      cnt += x[e] > 0.f;
-      bad |= x[e] < 0.f || x[e] != x[e] || fabsf(x[e]) == INFINITY;
-    }
-    int32_t tot = 0;
-    int64_t at = total + block_excl_scan<NW>(cnt, red, &tot);
+    for (int d = 0; d < CMP_AHEAD; ++d) {
+      const int64_t t0 = tg + (int64_t)d * TILE;
+      if (done || t0 >= vocab) break;
+      float x[CMP_E];
 #pragma unroll
-    for (int e = 0; e < CMP_E; ++e)
-      if (x[e] > 0.f) {
-        if (at < capacity) {
-          oid[at] = (int32_t)(j0 + e);
-          oval[at] = x[e];
-        }
-        ++at;
+      for (int e = 0; e < CMP_E; ++e) x[e] = xr[d][e];
+      if (t0 + CMP_AHEAD * TILE < vocab) fetch(t0 + CMP_AHEAD * TILE, xr[d]);
+      const int64_t j0 = t0 + (int64_t)tid * CMP_E;
+      int32_t cnt = 0;
+#pragma unroll
+      for (int e = 0; e < CMP_E; ++e) {
+        cnt += x[e] > 0.f;
+        bad |= x[e] < 0.f || x[e] != x[e] || fabsf(x[e]) == INFINITY;
       }
-    total += tot;
-    // more than capacity kept ids: the row overflows whatever the rest holds, and the first
-    // capacity ids are written (total is the same in every thread)
-    if (total > capacity) break;
+      int32_t tot = 0;
+      int64_t at = total + block_excl_scan<NW>(cnt, red, &tot);
+#pragma unroll
+      for (int e = 0; e < CMP_E; ++e)
+        if (x[e] > 0.f) {
+          if (at < capacity) {
+            oid[at] = (int32_t)(j0 + e);
+            oval[at] = x[e];
+          }
+          ++at;
+        }
+      total += tot;
+      // more than capacity kept ids: the row overflows whatever the rest holds, and the first
+      // capacity ids are written (total is the same in every thread)
+      if (total > capacity) done = true;
+    }
   }
   if (bad) s_bad = 1;
   __syncthreads();
