@@ -32,6 +32,8 @@
 
 #include <mutex>
 
+#include <type_traits>
+
 #include "dsv_device.h"
 
 namespace dsv {
@@ -3199,24 +3201,34 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
     }
   }
   // kept: every value of an unfiltered row; a nucleus row's values above the cut key, and the
-  // ones at it while their rank is below ktie (all of them at INT_MAX, none at 0)
+  // ones at it while their rank is below ktie (all of them at INT_MAX, none at 0).  The value
+  // is dense_P's (p, over the kept mass for nucleus and renormalised rows) or, raw_p, p itself:
+  // the row's choice is a branch around the loop (a select in it would divide every value).
+  auto write_rows = [&](auto div_tag) {
+    constexpr bool DIV = decltype(div_tag)::value;
 #pragma unroll
-  for (int u = 0; u < CV; ++u) {
-    const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
-    if (j0 >= hi) continue;
-    float x[n];
-    int32_t seen = 0;
+    for (int u = 0; u < CV; ++u) {
+      const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
+      if (j0 >= hi) continue;
+      float x[n];
+      int32_t seen = 0;
 #pragma unroll
-    for (int e = 0; e < n; ++e) {
-      const float xe = vec_elem<DT>(v[u], e);
-      const uint32_t k = key_of<DT>(xe);
-      const bool tie = hist && k == rs.vcut;
-      const bool kept = !hist || k > rs.vcut || (tie && (int64_t)rank0[u] + seen < (int64_t)rs.ktie);
-      seen += tie ? 1 : 0;
-      x[e] = kept ? (P.raw_p ? prob_of(xe, T, rs.m_f, rs.invZ) : (float)dense_P(rs, T, xe)) : 0.f;
+      for (int e = 0; e < n; ++e) {
+        const float xe = vec_elem<DT>(v[u], e);
+        const uint32_t k = key_of<DT>(xe);
+        const bool tie = hist && k == rs.vcut;
+        const bool kept = !hist || k > rs.vcut || (tie && (int64_t)rank0[u] + seen < (int64_t)rs.ktie);
+        seen += tie ? 1 : 0;
+        const float pe = prob_of(xe, T, rs.m_f, rs.invZ);
+        x[e] = kept ? (DIV ? pe / rs.S_f : pe) : 0.f;
+      }
+      store_vec(j0, x);
     }
-    store_vec(j0, x);
-  }
+  };
+  if (!P.raw_p && (rs.mode == M_HIST || rs.norm))
+    write_rows(std::true_type{});
+  else
+    write_rows(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------------------
