@@ -347,6 +347,7 @@ struct ChainShared {
   int32_t pure;
   int32_t tile, pick_thread;
   double thr, tile_lo, pick_lo;
+  double mass;  // the tiles' total (wave scan)
   int64_t bonus;
 };
 
@@ -635,15 +636,45 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
         sh.tile_mass[t] = w;
       }
       __syncthreads();
-      mass = 0.0;
-      for (int t = 0; t < ntiles; ++t) mass += sh.tile_mass[t];
+      if (ntiles <= WAVE) {  // the total by a wave scan over the tiles (lanes hold tiles)
+        if (tid < WAVE) {
+          double lo, hi;
+          const double tot = wave_tiles(lane < ntiles ? sh.tile_mass[lane] : 0.0, lo, hi);
+          if (lane == 0) sh.mass = tot;
+        }
+        __syncthreads();
+        mass = sh.mass;
+      } else {
+        mass = 0.0;
+        for (int t = 0; t < ntiles; ++t) mass += sh.tile_mass[t];
+      }
       if (pure || mass > 0.0) break;
       __syncthreads();  // (the second pass rewrites the tiles' parts)
       pure = true;  // the residual has no mass: draw from P
     }
     __syncthreads();
     const double thr = (double)uf * mass;
-    if (tid == 0) {
+    if (ntiles <= WAVE && tid < WAVE) {
+      // the first tile with mass whose interval (the same scan as the total) ends past thr
+      const double m = lane < ntiles ? sh.tile_mass[lane] : 0.0;
+      double lo, hi;
+      wave_tiles(m, lo, hi);
+      uint64_t hit = __ballot(lane < ntiles && m > 0.0 && thr < hi);
+      if (!hit) {  // rounding: the last tile with mass
+        const uint64_t pos = __ballot(lane < ntiles && m > 0.0);
+        hit = pos ? 1ull << (63 - __clzll((long long)pos)) : 0ull;
+      }
+      const int tile = hit ? __ffsll((long long)hit) - 1 : -1;
+      const double before = readlane_at(lo, tile >= 0 ? tile : 0);
+      if (lane == 0) {
+        sh.tile = tile;
+        sh.tile_lo = tile >= 0 ? before : 0.0;
+        sh.thr = thr;
+        sh.pure = pure ? 1 : 0;
+        sh.pick_thread = -1;
+        sh.bonus = V - 1;
+      }
+    } else if (ntiles > WAVE && tid == 0) {
       double before = 0.0;
       int tile = -1, last = -1;
       for (int t = 0; t < ntiles; ++t) {
