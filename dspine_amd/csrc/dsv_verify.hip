@@ -3083,29 +3083,33 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
       }
       __syncthreads();
     }
-    // chunk offsets in 32 bits; a vector's nonzero elements from one subtraction (greedy: the
-    // one-hot's offset, -1 for none) or one bitmap word (support lists), the values only then
+    // No logits are read here, so the values go out as 4-float groups with a wave's lanes on
+    // consecutive groups (16-byte stores a wave covers 1 KB with, where the 8-value vectors of
+    // the softmax rows take two half-filled stores).  Chunk offsets in 32 bits; a group's
+    // nonzero elements from one subtraction (greedy: the one-hot's offset, -1 for none) or one
+    // bitmap nibble (support lists), the values only then
+    constexpr int G = 4;
     const uint32_t ext = (uint32_t)(hi - lo);
     const uint32_t oh = mode == M_GREEDY ? (uint32_t)rs.argmax - (uint32_t)lo : 0xFFFFFFFFu;
 #pragma unroll
-    for (int u = 0; u < CV; ++u) {
-      const uint32_t o0 = (uint32_t)((u * CT + tid) * n);
+    for (int u = 0; u < CHE / G / CT; ++u) {
+      const uint32_t o0 = (uint32_t)((u * CT + tid) * G);
       if (o0 >= ext) continue;
       const int64_t j0 = lo + o0;
-      float x[n];
+      float x[G];
 #pragma unroll
-      for (int e = 0; e < n; ++e) x[e] = 0.f;
+      for (int e = 0; e < G; ++e) x[e] = 0.f;
       if (mode == M_GREEDY) {
         const uint32_t e1 = oh - o0;
-        if (e1 < (uint32_t)n) {
+        if (e1 < (uint32_t)G) {
 #pragma unroll
-          for (int e = 0; e < n; ++e) x[e] = (uint32_t)e == e1 ? 1.f : 0.f;
+          for (int e = 0; e < G; ++e) x[e] = (uint32_t)e == e1 ? 1.f : 0.f;
         }
       } else if (mode == M_LIST) {
-        const uint32_t bits = (s_bm[o0 >> 5] >> (o0 & 31)) & ((1u << n) - 1u);
+        const uint32_t bits = (s_bm[o0 >> 5] >> (o0 & 31)) & ((1u << G) - 1u);
         if (bits) {
 #pragma unroll
-          for (int e = 0; e < n; ++e) {
+          for (int e = 0; e < G; ++e) {
             if (!((bits >> e) & 1u)) continue;
             const int64_t j = j0 + e;
             for (int q = 0; q < nl; ++q)
@@ -3121,7 +3125,13 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
           }
         }
       }
-      store_vec(j0, x);
+      if (j0 + G <= hi) {
+        *reinterpret_cast<float4*>(orow + j0) = make_float4(x[0], x[1], x[2], x[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+          if (j0 + e < hi) orow[j0 + e] = x[e];
+      }
     }
     return;
   }
