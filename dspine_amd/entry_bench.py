@@ -16,6 +16,8 @@ Algorithmic bytes (the least any implementation moves):
                    per request (read once, reused by the request's rows)
   chain_on_probs   P of the accepted row read once for the bonus draw (4 bytes per element);
                    the draft tests read one value a row
+Two torch references give this part's practical rates: a fill of P (write only) and a copy of
+the logits (read + write).
 The planner, the commit, the uniforms and the window index move KBs and are timed only.
 """
 
@@ -117,6 +119,9 @@ def main():
     info_pen = SimpleNamespace(acc_additive_penalties=pen)
     us = timed(lambda: adjust_logits(work.view(bs, T, V), info_pen, None), args.calls)
     line("adjust_logits", us, n_logits * 4 + bs * V * 4, shape=[bs, T, V], op="additive")
+    # the read + write rate of this part for reference: torch's copy of the same logits
+    us = timed(lambda: work.copy_(logits), args.calls)
+    line("copy_logits_reference", us, n_logits * 4, shape=[rows, V], logits="bf16")
     rtr = torch.arange(rows, device=dev) // T
     us = timed(lambda: adjust_logits(work, info_pen, rtr), args.calls)
     line("adjust_logits_row_map", us, n_logits * 4 + bs * V * 4, shape=[rows, V], op="additive")
