@@ -64,8 +64,8 @@ def test_commit_matches_oracle(device, mode, bs):
 
 
 def test_commit_with_double_buffered_rounds(device):
-    """Two sampled rounds through the worker: round 1's outputs (the buffers the commit reads)
-    keep their values while round 2 is verified into the other set, and each round's commit
+    """Two sampled verify rounds through the worker: the first verify's outputs (the buffers the
+    commit reads) keep their values while the second is verified into the other set, and each commit
     matches the oracle's closed form on that round's accept lengths."""
     from dspine_amd.runtime import worker as Wk
     from dspine_amd.verify import verify_step
@@ -85,7 +85,7 @@ def test_commit_with_double_buffered_rounds(device):
         rounds.append((outs, tuple(t.clone() for t in outs), batch))
     (o1, saved1, b1), (o2, _, _) = rounds
     assert all(a.data_ptr() != b.data_ptr() for a, b in zip(o1, o2))
-    for live, saved in zip(o1, saved1):  # round 1's buffers were not touched by round 2
+    for live, saved in zip(o1, saved1):  # the first verify's buffers were not touched by the second
         assert torch.equal(live, saved)
     table = torch.zeros((bs, 4200), dtype=torch.int32, device=device)
     seq = torch.zeros(bs, dtype=torch.int64, device=device)
