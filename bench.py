@@ -13,10 +13,15 @@ Other workloads (parity cases of the same path, timed the same way):
   --config 3   rejection: 32 x 17 x 151936 fp32, top-k 20, top-p 0.95, sparse q (--sigma)
   --config 5   ragged: 32 requests x U{4..16} rows x 262144 bf16 Student-t, top-p 0.9
 
+  --config 1   greedy: 1 x 17 x 151936 fp32, argmax acceptance with one seeded mismatch
+  --config 4 --accept deep   the serving step with a planted likely token per row, so that a
+               mean of ~6.5 of the 16 drafts is accepted
+
 The logits of each step come from one of several identical copies in turn (together >= 661 MB,
-so no step reads data the previous steps left in the 256 MB Infinity Cache).  K steps are
-timed as plain stream launches and as HIP-graph replays, each bracketed by device
-synchronisation; the faster is the step time.
+so no step reads data the previous steps left in the 256 MB Infinity Cache).  One HIP graph per
+copy holds one step; the step time is the median of K single-step replays (each bracketed by its
+own HIP events, the K bracketed by device synchronisation), reported with p90.  All K steps in
+one graph and K plain stream launches are reported beside it as labelled fields.
 
 Prints ONE JSON line (metric: verified rows/s) with the roofline of the dominant kernel -- the
 chunk pass k_chunk, which reads every logit once; its launches are bracketed by HIP events on
@@ -30,6 +35,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -37,6 +43,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "verify rows/sec at B=64x17x151936 bf16; achieved HBM GB/s vs peak"
+DEEP_PEAK = 16.0  # the planted logit of --accept deep (mean accepted length ~6.5 of 16)
 PEAK_GBPS = 8000.0  # MI355X HBM3E
 ROTATE_BYTES = 661 << 20  # logits copies read in turn: more than twice the 256 MB Infinity Cache
 
@@ -97,13 +104,34 @@ def time_eager(step, steps, warmup, torch):
     return e0.elapsed_time(e1) / steps
 
 
-def time_graph(step, steps, warmup, nbuf, torch):
-    """One graph holds all `steps` steps (the logits copies in turn), replayed once untimed and
-    once timed: the GPU idles ~9 us between two replays of a graph, which a graph of a few steps
-    would charge to every few steps."""
+def time_replays(step, steps, warmup, nbuf, torch):
+    """Per-step latency as a serving loop pays it: one HIP graph per logits copy, each holding
+    one step, replayed in turn `steps` times after `warmup` untimed replays; every replay is
+    bracketed by its own HIP events on the replay stream.  Returns the per-step times (ms)."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
+    graphs = []
+    for i in range(nbuf):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(i)
+        graphs.append(g)
+    for i in range(max(warmup, nbuf)):
+        graphs[i % nbuf].replay()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i, (s, e) in enumerate(ev):
+        s.record()
+        graphs[i % nbuf].replay()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in ev], graphs
+
+
+def time_one_graph(step, steps, nbuf, torch):
+    """All `steps` steps captured in one graph (the logits copies in turn), replayed once untimed
+    and once timed: the device-side floor of back-to-back steps without a replay boundary."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(steps):
@@ -115,7 +143,13 @@ def time_graph(step, steps, warmup, nbuf, torch):
     g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, g
+    return start.elapsed_time(end) / steps
+
+
+def percentile(xs, q):
+    xs = sorted(xs)
+    i = min(len(xs) - 1, max(0, int(math.ceil(q * len(xs))) - 1))
+    return xs[i]
 
 
 def copies(t, torch):
@@ -124,66 +158,80 @@ def copies(t, torch):
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
-def cpu_verify_baseline(batch, min_seconds=10.0, max_seconds=30.0):
-    """The CPU oracle (torch on the host) on a bounded sample of the same workload: passes over
-    the requests, one request per call, until at least ``min_seconds`` of work (capped at
-    ``max_seconds``)."""
-    import numpy as np
+def _cpu_median(run, runs=10, warm=2):
+    """Median wall time (s) of `runs` calls of run() after `warm` untimed ones, on every core this
+    process may use (torch.set_num_threads), and that thread count."""
     import torch
-
-    import oracle.verify_oracle as O
 
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
+    for _ in range(warm):
+        run()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], n, times
+
+
+def cpu_verify_baseline(batch, requests=8, sparse_joint=False, backend="pytorch"):
+    """The CPU oracle (torch on the host) on a bounded sample of the same workload: the first
+    `requests` requests verified in one oracle call, median of 10 calls after 2 warm-ups."""
+    import numpy as np
+
+    import oracle.verify_oracle as O
+
     bs, T = batch["candidates"].shape
     lens = batch.get("verify_lens")
     lens = np.full(bs, T) if lens is None else lens.numpy()
     offs = batch.get("row_offsets")
     V = batch["logits"].shape[1]
-    calls, rows, t0 = 0, 0, time.perf_counter()
-    done = False
-    while not done:
-        for b in range(bs):
-            O.verify_step(
-                batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
-                q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(), verify_lens=lens,
-                uniforms=batch["uniforms"].numpy(), uniform_final=batch["uniform_final"].numpy(),
-                prefix_lens=batch["prefix_lens"].numpy(), hist_ids=batch.get("hist_ids"),
-                presence=batch.get("presence"), repetition=batch.get("repetition"),
-                page_table=batch.get("page_table"), row_offsets=None if offs is None else offs.numpy(),
-                requests=[b])
-            calls += 1
-            rows += int(lens[b])
-            if time.perf_counter() - t0 > max_seconds:
-                done = True
-                break
-        if time.perf_counter() - t0 >= min_seconds:
-            done = True
-    dt = time.perf_counter() - t0
-    return {"value": rows / dt, "unit": "rows/s", "cores": n, "kind": "port",
-            "sample": f"{calls} request verifications ({calls / bs:.2f} passes over the {bs} requests, "
-                      f"{rows} rows x {V}) of the same workload, one request per oracle call, {dt:.1f} s"}
+    sub = list(range(min(requests, bs)))
+    rows = int(sum(int(lens[b]) for b in sub))
+
+    def run():
+        O.verify_step(
+            batch["logits"], batch["info"], candidates=batch["candidates"].numpy(),
+            q_ids=batch["q_ids"].numpy(), q_values=batch["q_values"].numpy(), verify_lens=lens,
+            uniforms=batch["uniforms"].numpy(), uniform_final=batch["uniform_final"].numpy(),
+            prefix_lens=batch["prefix_lens"].numpy(), hist_ids=batch.get("hist_ids"),
+            presence=batch.get("presence"), repetition=batch.get("repetition"),
+            page_table=batch.get("page_table"), row_offsets=None if offs is None else offs.numpy(),
+            sampling_backend=backend, requests=sub, sparse_joint=sparse_joint)
+
+    med, n, times = _cpu_median(run)
+    return {"value": rows / med, "unit": "rows/s", "cores": n, "kind": "port", "ms_per_sample": med * 1e3,
+            "sample": f"requests 0..{len(sub) - 1} of the same workload ({rows} rows x {V}) in one oracle call, "
+                      f"median of {len(times)} calls after 2 warm-ups ({sum(times):.1f} s timed)"}
 
 
-def cpu_topk_baseline(x, k, min_seconds=10.0, max_seconds=30.0):
-    """The CPU oracle's top-k (stable descending sort) on bounded 64-row slices of the rows."""
-    import torch
-
+def cpu_topk_baseline(x, k, rows=64):
+    """The CPU oracle's top-k (stable descending sort) on the first `rows` rows, median of 10."""
     import oracle.verify_oracle as O
 
-    n = len(os.sched_getaffinity(0))
-    torch.set_num_threads(n)
-    rows, t0, i = 0, time.perf_counter(), 0
-    while time.perf_counter() - t0 < min_seconds:
-        sl = x[(i * 64) % x.shape[0]: (i * 64) % x.shape[0] + 64]
-        O.topk(sl.float(), k)
-        rows += sl.shape[0]
-        i += 1
-        if time.perf_counter() - t0 > max_seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": rows / dt, "unit": "rows/s", "cores": n, "kind": "port",
-            "sample": f"{rows} rows x {x.shape[1]} (64-row slices of the same rows), k={k}, {dt:.1f} s"}
+    sl = x[:rows].float()
+    med, n, times = _cpu_median(lambda: O.topk(sl, k))
+    return {"value": rows / med, "unit": "rows/s", "cores": n, "kind": "port", "ms_per_sample": med * 1e3,
+            "sample": f"rows 0..{rows - 1} x {x.shape[1]}, k={k}, median of {len(times)} calls after 2 warm-ups "
+                      f"({sum(times):.1f} s timed)"}
+
+
+def cpu_greedy_baseline(batch):
+    """The CPU oracle's greedy verify (argmax + first mismatch) of the whole 1 x 17 round,
+    median of 10 after 2 warm-ups."""
+    import oracle.verify_oracle as O
+
+    bs, T = batch["candidates"].shape
+
+    def run():
+        top1 = O.argmax_rows(batch["logits"])
+        O.greedy_accept(top1, batch["candidates"].numpy(), [T] * bs, batch["prefix_lens"].numpy())
+
+    med, n, times = _cpu_median(run)
+    return {"value": bs * T / med, "unit": "rows/s", "cores": n, "kind": "port", "ms_per_sample": med * 1e3,
+            "sample": f"the whole round ({bs * T} rows x {batch['logits'].shape[1]} fp32), median of {len(times)} "
+                      f"calls after 2 warm-ups"}
 
 
 def setup_verify(config, args, torch, dev):
@@ -192,9 +240,12 @@ def setup_verify(config, args, torch, dev):
     from dspine_amd.verify import History, Workspace, new_outputs, verify_step
 
     if config == 4:
-        batch = W.serving_round()
-        name, workload = "serving", ("full verify step (penalties, temperature softmax, top-k/top-p filter, "
-                                     "chain rejection with sparse q, residual resample, compaction + KV slots)")
+        deep = args.accept == "deep"
+        batch = W.serving_round(peak=DEEP_PEAK if deep else None)
+        name = "serving_deep" if deep else "serving"
+        workload = ("full verify step (penalties, temperature softmax, top-k/top-p filter, chain rejection with "
+                    "sparse q, residual resample, compaction + KV slots)"
+                    + (f"; one planted logit per row at {DEEP_PEAK:g} +- 1 (deep acceptance)" if deep else ""))
     elif config == 3:
         batch = W.rejection_round(sigma_draft=args.sigma)
         name, workload = "rejection", (f"verify step, fp32 target, T=1, top-k 20, top-p 0.95, sparse q from "
@@ -237,6 +288,35 @@ def setup_verify(config, args, torch, dev):
     return step, facts
 
 
+def setup_greedy(args, torch, dev):
+    """Greedy verify of the 1 x 17 x 151936 fp32 round (argmax acceptance, capped at 17)."""
+    from dspine_amd import workloads as W
+    from dspine_amd.verification.caps import accept_greedy
+
+    batch = W.greedy_round()
+    rows, V = batch["logits"].shape
+    cand = batch["candidates"].to(dev)
+    prefix = batch["prefix_lens"].to(dev)
+    bufs = copies(batch["logits"].to(dev), torch)
+    outs = (torch.empty(1, device=dev, dtype=torch.int32), torch.empty(1, device=dev, dtype=torch.int32),
+            torch.empty(1, device=dev, dtype=torch.int64), torch.empty((1, rows), device=dev, dtype=torch.int64),
+            torch.empty(1, device=dev, dtype=torch.int32))
+
+    def step(i):
+        accept_greedy(candidates=cand, next_token_logits=bufs[i % len(bufs)], prefix_lens=prefix, cap=rows,
+                      outputs=outs)
+
+    logits = rows * V * 4
+    small = rows * 8 + 4 + (4 + 4 + 8 + rows * 8 + 4)
+    facts = dict(name="greedy", batch=batch, rows=rows, total=logits + small, chunk=logits, dtype="f32",
+                 kernel=f"k_chunk (greedy pass: {rows} rows x {math.ceil(V / 12288)} chunks of 12288 fp32)",
+                 config={"workload": "greedy verify (argmax acceptance), temperature 0, one seeded mismatch",
+                         "requests": 1, "rows_per_request": rows, "rows": rows, "vocab": V, "logits_dtype": "fp32",
+                         "logits_copies": len(bufs)},
+                 accept=lambda: outs[0].float().mean().item())
+    return step, facts
+
+
 def setup_topk(args, torch, dev):
     from dspine_amd import workloads as W
     from dspine_amd.kernels.dspine import topk
@@ -266,8 +346,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5),
-                    help="workload: 4 = the serving verify step (default); 2 top-k, 3 rejection, 5 ragged")
+    ap.add_argument("--config", type=int, default=4, choices=(1, 2, 3, 4, 5),
+                    help="workload: 4 = the serving verify step (default); 1 greedy, 2 top-k, 3 rejection, 5 ragged")
+    ap.add_argument("--accept", default="low", choices=("low", "deep"),
+                    help="drafts of --config 4: low (the seeded workload as generated) or deep (a planted likely "
+                         "token per row: a mean accepted length near 6.5)")
     ap.add_argument("--k", type=int, default=64, choices=(1, 20, 64), help="top-k of --config 2")
     ap.add_argument("--sigma", type=float, default=0.5, choices=(0.5, 1.5), help="draft noise of --config 3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -296,7 +379,9 @@ def main():
 
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
-    if args.config == 2:
+    if args.config == 1:
+        step, f = setup_greedy(args, torch, dev)
+    elif args.config == 2:
         step, f = setup_topk(args, torch, dev)
     else:
         step, f = setup_verify(args.config, args, torch, dev)
@@ -304,22 +389,29 @@ def main():
     print(f"[bench] config {args.config} ready in {time.perf_counter() - t0:.1f} s ({nbuf} logits copies)",
           file=sys.stderr, flush=True)
 
+    # the headline: the median of `steps` single-step graph replays
+    times, _graphs = time_replays(step, args.steps, args.warmup, nbuf, torch)
+    ms = statistics.median(times)
+    p90 = percentile(times, 0.9)
+    # labelled side figures: every step in one graph (no replay boundary), and plain launches
+    one_graph_ms = time_one_graph(step, args.steps, nbuf, torch)
     eager_ms = time_eager(step, args.steps, args.warmup, torch)
-    graph_ms, _g = time_graph(step, args.steps, args.warmup, nbuf, torch)
-    ms = min(graph_ms, eager_ms)
-    mode = "graph" if graph_ms <= eager_ms else "eager"
     kern_ms = time_kernel_events(step, args.steps, _lib.load(), torch)
     total_bytes, chunk_bytes = f["total"], f["chunk"]
     achieved = chunk_bytes / (kern_ms * 1e-3) / 1e9
     step_gbps = total_bytes / (ms * 1e-3) / 1e9
     acc = f["accept"]() if f["accept"] else None
-    print(f"[bench] graph {graph_ms * 1e3:.1f} us/step, eager {eager_ms * 1e3:.1f} us/step, k_chunk "
+    print(f"[bench] step p50 {ms * 1e3:.1f} us, p90 {p90 * 1e3:.1f} us ({args.steps} single-step graph replays); "
+          f"one graph of all steps {one_graph_ms * 1e3:.1f} us/step, eager {eager_ms * 1e3:.1f} us/step; k_chunk "
           f"{kern_ms * 1e3:.1f} us ({achieved / PEAK_GBPS:.3f} of peak), step {step_gbps:.0f} GB/s "
           f"({step_gbps / PEAK_GBPS:.3f} of peak)" + (f", mean accept {acc:.2f}" if acc is not None else ""),
           file=sys.stderr, flush=True)
     cfg = dict(f["config"])
-    cfg.update({"timed_launch": mode, "eager_ms_per_step": eager_ms, "graph_ms_per_step": graph_ms,
+    cfg.update({"timed_launch": "median of single-step graph replays", "p50_ms": ms, "p90_ms": p90,
+                "min_ms": min(times), "one_graph_ms_per_step": one_graph_ms, "eager_ms_per_step": eager_ms,
                 "step_GBps_algorithmic": step_gbps, "step_algorithmic_bytes": total_bytes})
+    if acc is not None:
+        cfg["mean_accept"] = acc
     line = {
         "metric": METRIC,
         "value": f["rows"] / (ms * 1e-3),
@@ -342,7 +434,9 @@ def main():
         },
     }
     if not args.no_cpu_baseline:
-        if args.config == 2:
+        if args.config == 1:
+            line["cpu_baseline"] = cpu_greedy_baseline(f["batch"])
+        elif args.config == 2:
             line["cpu_baseline"] = cpu_topk_baseline(f["x"], args.k)
         else:
             line["cpu_baseline"] = cpu_verify_baseline(f["batch"])

@@ -45,6 +45,7 @@ class VerifyArgs(ctypes.Structure):
         ("backend", i32),
         ("temperatures", vp), ("top_ks", vp), ("top_ps", vp), ("min_ps", vp),
         ("filter", i32), ("need_min_p", i32), ("any_greedy", i32), ("max_top_k", i32),
+        ("sparse_joint", i32), ("pad0", i32),
         ("hist_ids", vp), ("hist_len", i32), ("pad1", i32), ("presence", vp), ("repetition", vp),
         ("candidates", vp), ("q_ids", vp), ("q_ids_i64", i32), ("K", i32), ("q_values", vp),
         ("uniforms", vp), ("uniform_final", vp), ("prefix_lens", vp),

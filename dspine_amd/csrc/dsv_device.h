@@ -64,6 +64,8 @@ constexpr int NCHK = 32;             // most chunks a row may have (per-row chun
 constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
 constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram
+constexpr int FLAG_SCAN_DRAW = 4;    // dense row whose bonus draw k_final plans from a scan of every chunk
+constexpr int SJ_CAP = 32;           // packed capacity of the sparse joint target (sampling/target.py:84-87)
 
 template <int DT>
 struct Elems {
@@ -116,6 +118,7 @@ __device__ __forceinline__ int row_mode(const dsv_verify_args& a, int b, int for
   if (force_greedy) return M_GREEDY;
   const int k = a.top_ks[b];
   if (a.any_greedy && k <= 1) return M_GREEDY;
+  if (a.sparse_joint) return M_LIST;  // (every top-k <= SJ_CAP; the filter applies whatever the flags)
   if (!a.filter) return M_UNF;
   if (k <= DSV_LIST_K) return M_LIST;
   const float mp = (a.need_min_p && a.min_ps) ? a.min_ps[b] : 0.f;

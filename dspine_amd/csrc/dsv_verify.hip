@@ -130,6 +130,21 @@ __device__ __noinline__ int refill_candidates(const uint32_t* cbits, const char*
   return nb < CAND_CAP ? nb : CAND_CAP;
 }
 
+// The thread's share of the chunk's values whose key is `key` (cbits: the chunk's history bits),
+// re-read from memory: the tie count of a sparse joint row's chunk whose candidate buffer was
+// refilled.
+template <int DT>
+__device__ __noinline__ int count_key_chunk(const uint32_t* cbits, const char* rowp, int64_t lo, int64_t hi,
+                                            uint32_t key, float pres, float rep) {
+  int cnt = 0;
+  for (int64_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
+    float x = load_elem<DT>(rowp, j);
+    if (cbits && ((cbits[(j - lo) >> 5] >> (j & 31)) & 1u)) x = penalize<DT>(x, pres, rep);
+    cnt += key_of<DT>(x) == key;
+  }
+  return cnt;
+}
+
 // ---------------------------------------------------------------------------------------
 // Bonus draw machinery (used by the row merge and k_final; see the bonus section below)
 // ---------------------------------------------------------------------------------------
@@ -419,15 +434,20 @@ __device__ __forceinline__ void for_span(const KParams& P, int b, const char* ro
 }
 
 // Support-list draw (wave 0): entries sh.lst[0, sh.nlist) sorted by id; q staged when resid.
+// Sparse joint rows are packed P in the reference: the residual at an id subtracts the clamped q
+// of every lane holding it (sampling/sparse/accept.py:186-193); other rows the last lane's.
 __device__ __forceinline__ int64_t list_draw(const dsv_verify_args& a, bool resid, float uf, const DrawShared& sh) {
   const int lane = threadIdx.x & (WAVE - 1);
   const bool live = lane < sh.nlist;
   const ListEntry e = live ? sh.lst[lane] : ListEntry{INT_MAX, 0.f};
   const double Pi = (double)e.P;
   double w = Pi;
-  if (resid && live)
+  if (resid && live) {
+    double qs = 0.0;
     for (int l = 0; l < a.K; ++l)
-      if (sh.qlast[l] && sh.qid[l] == (int64_t)e.id) w = fmax(Pi - (double)sh.qv[l], 0.0);
+      if (sh.qid[l] == (int64_t)e.id && (a.sparse_joint || sh.qlast[l])) qs += (double)sh.qv[l];
+    w = fmax(Pi - qs, 0.0);
+  }
   double lo, hi;
   double mass = wave_tiles(w, lo, hi);
   if (!resid || !(mass > 0.0)) mass = wave_tiles(Pi, lo, hi);
@@ -734,7 +754,8 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
   const ChunkStat* cs = pre.cs;
   int kk = 0;
   if (mode == M_LIST) {
-    const int K = pre.top_k < 1 ? 1 : pre.top_k;
+    // (sparse joint rows rank the capacity + 1 largest, whatever their top-k <= capacity)
+    const int K = a.sparse_joint ? SJ_CAP + 1 : (pre.top_k < 1 ? 1 : pre.top_k);
     if (tid == 0) {
       int o = 0;
       for (int c = 0; c < C; ++c) {
@@ -886,16 +907,62 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
     const double S_all = wave_tiles((double)p, lo_p, hi_p);
     const float top_p = pre.top_p;
     const float min_p = pre.min_p;
-    bool keep = live && lane < pre.top_k && (!nz || !topp_fails(a.backend, lo_p, p, top_p));
-    if (a.need_min_p) {
-      if (a.backend == DSV_BACKEND_FLASHINFER) {
-        // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
-        double lo_a, hi_a;
-        wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
-        keep = live && lane < pre.top_k && lo_a <= (double)top_p;
+    bool keep;
+    if (a.sparse_joint) {
+      // The reference's sparse joint target (sampling/sparse/target.py:156-178): of the row's
+      // capacity + 1 largest, keep p > 0, p >= p_(k) (every value tied with the k-th) and the
+      // nucleus -- the mass of the strictly larger p below top_p, or top_p >= 1.  Equal p are
+      // adjacent here, so that mass is the prefix at the first lane holding the lane's p.
+      const float p_prev = __shfl(p, lane > 0 ? lane - 1 : 0, WAVE);
+      const uint64_t starts = __ballot(live && (lane == 0 || p_prev != p)) | 1ull;
+      const uint64_t upto = lane == WAVE - 1 ? ~0ull : (2ull << lane) - 1ull;
+      const int first = 63 - __clzll((long long)(starts & upto));
+      const double higher = __shfl(lo_p, first, WAVE);
+      const int kidx = (pre.top_k < 1 ? 1 : (pre.top_k > kk ? kk : pre.top_k)) - 1;
+      const float p_k = readlane_at(p, kidx);
+      keep = live && p > 0.f && p >= p_k && (top_p >= 1.f || higher < (double)top_p);
+      if (__popcll(__ballot(keep)) > SJ_CAP) {
+        // More kept than the packed capacity: the (capacity+1)-th kept value ties the k-th, so
+        // the nucleus keeps every p >= p_(k) -- a dense row cut at the k-th key with all of its
+        // ties (sparse/target.py:56-76).  Its values at the cut key: those in the chunks' lists
+        // (read again: a rare path) and those each list left out (counted by the chunk pass).
+        const uint32_t kcut = readlane_at(unpack_key(pk), kidx);
+        int32_t nt = 0;
+        for (int c = 0; c < C; ++c) {
+          const uint64_t* src = P.cand + (r * C + c) * (int64_t)P.kcand;
+          const int nc = cs[c].ncand;
+          for (int i = lane; i < nc; i += WAVE) nt += unpack_key(src[i]) == kcut;
+          if (lane == 0 && unpack_key(ms.cmin[c]) == kcut) nt += cs[c].tieq;
+        }
+        nt = wave_sum(nt);
+        const double S = wave_sum(live && unpack_key(pk) > kcut ? (double)p : 0.0) + (double)nt * (double)p_k;
+        rs.mode = M_HIST;
+        rs.vcut = kcut;
+        rs.ktie = INT_MAX;
+        rs.flags = FLAG_SCAN_DRAW;
+        rs.S_kept = S;
+        rs.S_f = (float)S;
+        rs.p_draft = (tok >= 0 && tok < a.vocab && key_of<DT>(xt) >= kcut) ? prob_of(xt, T, m_f, invZ) / rs.S_f : 0.f;
+        const int32_t ok = tok >= 0 ? step_accept_lds(ds, a.K, tok, rs.p_draft, pre.u) : 0;
+        if (lane == 0) {
+          ro->rs = rs;
+          ro->ok = ok;
+          ro->nuc = 0;
+        }
+        return;
       }
-      const float thr = readlane<0>(p) * min_p;
-      if (p < thr) keep = false;
+    } else {
+      keep = live && lane < pre.top_k && (!nz || !topp_fails(a.backend, lo_p, p, top_p));
+      if (a.need_min_p) {
+        if (a.backend == DSV_BACKEND_FLASHINFER) {
+          // sequential branch: renormalise over the top-k, top-p on that mass, then min-p
+          double lo_a, hi_a;
+          wave_tiles(live ? (double)p / S_all : 0.0, lo_a, hi_a);
+          keep = live && lane < pre.top_k && lo_a <= (double)top_p;
+        }
+        const float thr = readlane<0>(p) * min_p;
+        if (p < thr) keep = false;
+      }
     }
     const double Sk = wave_sum(keep ? (double)p : 0.0);
     const float S_f = (float)Sk;
@@ -1926,6 +1993,7 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
   __shared__ uint32_t s_pb[CHE / 32];  // the chunk's slice of the request's history bitmap
   __shared__ int32_t s_cnt, s_nq;
   __shared__ uint32_t s_wlo;
+  __shared__ uint32_t s_kth;  // list rows: the key of the chunk's K-th largest value
   __shared__ float s_xtok;
   __shared__ int32_t s_arg;  // the chunk's first argmax id, from the thread that holds it
   const dsv_verify_args& a = P.a;
@@ -1997,7 +2065,7 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
   if (P.softmax && !P.force_greedy) {
     if (mode != M_GREEDY) T = a.temperatures[b];
     topk = a.top_ks[b];
-    if (a.filter) top_p = a.top_ps[b];
+    if (a.filter || a.sparse_joint) top_p = a.top_ps[b];
     if (pen) {
       pres = a.presence ? a.presence[b] : 0.f;
       rep = a.repetition ? a.repetition[b] : 1.f;
@@ -2242,7 +2310,8 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
       out.kx = kx;
     }
   } else if (mode == M_LIST) {
-    int K = topk;
+    // (sparse joint rows: the capacity + 1 largest, whatever the request's top-k <= capacity)
+    int K = (P.softmax && a.sparse_joint) ? SJ_CAP + 1 : topk;
     K = K < 1 ? 1 : (K > P.kcand ? P.kcand : K);
     // admission bound: min over the 4 waves of each wave's ceil(K/4)-th largest thread-max key,
     // so that at least K values of the chunk are at or above it
@@ -2374,10 +2443,12 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
     }
     __syncthreads();
     int nb = __builtin_amdgcn_readfirstlane(s_cnt);
+    bool refilled = false;
     if (nq > STAGE_VECS || nb > CAND_CAP) {
       // too many vectors to stage, or too many admitted values: re-read the chunk
       nb = refill_candidates<DT>(pen ? s_pb : nullptr, rowp, lo, hi, K, pres, rep, cbuf,
                                  hist256, su, &s_cnt, nq > STAGE_VECS ? ((uint64_t)thr << 32) | 1ull : 0ull);
+      refilled = true;
     }
     const int kk = K < nb ? K : nb;
     uint64_t* dst = P.cand + (r * C + c) * (int64_t)P.kcand;
@@ -2400,6 +2471,7 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
             ahead += o > v_i;
           }
           take = key_i > kth || (key_i == kth && lane < nb && ahead < need);
+          if (lane == 0) s_kth = kth;
         }
         const uint64_t tb = __ballot(take);
         if (take)
@@ -2411,9 +2483,28 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
         int rank = 0;
         for (int j = 0; j < nb; ++j) rank += cbuf[j] > v_i;
         if (rank < kk) dst[rank] = v_i;
+        if (rank == kk - 1) s_kth = unpack_key(v_i);
       }
     }
     out.ncand = kk;
+    if (P.softmax && a.sparse_joint && nb > K) {
+      // Sparse joint rows keep every value tied with the row's k-th, so the row merge needs the
+      // chunk's values at its list's smallest key that the list left out: all the values at that
+      // key (every one reached the admission bound; a refilled buffer may miss some, then the
+      // chunk is counted again from memory) less those in the list (the list holds every value
+      // above that key).
+      __syncthreads();
+      const uint32_t kth = s_kth;
+      int eq = 0, gt = 0;
+      for (int i = tid; i < nb; i += CT) {
+        const uint32_t key = unpack_key(cbuf[i]);
+        eq += key == kth;
+        gt += key > kth;
+      }
+      if (refilled) eq = count_key_chunk<DT>(pen ? s_pb : nullptr, rowp, lo, hi, kth, pres, rep);
+      const int32_t eg = block_sum<CT / WAVE>(eq | (gt << 20), reinterpret_cast<int32_t*>(sd));
+      out.tieq = (eg & 0xFFFFF) - (kk - (eg >> 20));
+    }
   }
   // The statistics: thread 0 writes all but the argmax id and the draft token's value, which
   // their owners store from their own LDS writes (no barrier: the fields are disjoint).
@@ -2694,7 +2785,7 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
     bonus = rs.argmax;
   } else if (rs.mode == M_LIST) {
     bonus = tid < WAVE ? list_draw(a, resid, pre.uf, ds) : 0;
-  } else if (rs.flags & FLAG_FULL_HIST) {
+  } else if (rs.flags & (FLAG_FULL_HIST | FLAG_SCAN_DRAW)) {
     bonus = BONUS_LATER;
   } else {
     // dense rows: the chunk and threshold; k_final scans the chunk when this row is the accepted
@@ -3411,8 +3502,14 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
   if (!a.row_offsets && a.rows != (int64_t)a.bs * a.T)
     DSV_FAIL(DSV_ERR_INVALID, "%s: dense layout needs rows == bs*T (%lld != %d*%d)", what, (long long)a.rows, a.bs,
              a.T);
-  if (!a.logits || !a.temperatures || !a.top_ks || (a.filter && !a.top_ps) || !a.workspace)
+  if (!a.logits || !a.temperatures || !a.top_ks || ((a.filter || a.sparse_joint) && !a.top_ps) || !a.workspace)
     DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
+  if (a.sparse_joint &&
+      (!drafts || a.backend != DSV_BACKEND_FLASHINFER || a.need_min_p || a.any_greedy || a.max_top_k < 1 ||
+       a.max_top_k > SJ_CAP || a.max_top_k > a.vocab))
+    DSV_FAIL(DSV_ERR_INVALID,
+             "%s: the sparse joint target needs the verify step, the flashinfer backend, no min-p, no greedy "
+             "rows and 1 <= max_top_k <= %d (<= vocab)", what, SJ_CAP);
   if (drafts) {
     if (!a.top_ps || !a.candidates || !a.q_ids || !a.q_values || !a.uniforms || !a.uniform_final || !a.prefix_lens ||
         !a.accept || !a.commit || !a.bonus || !a.output || !a.new_seq)
@@ -3528,7 +3625,7 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   // dense row (unfiltered or nucleus: only when a top-k above the support list, or no filter,
   // can occur), and requests whose ragged row offsets leave rows outside the logits.
   const bool all_greedy = a.any_greedy && a.max_top_k <= 1;
-  const bool dense_possible = !all_greedy && (!a.filter || a.max_top_k > DSV_LIST_K);
+  const bool dense_possible = !all_greedy && (!a.filter || a.max_top_k > DSV_LIST_K || a.sparse_joint);
   P.only_deferred = (stages & 1) ? 1 : 0;
   if (stages & 1) {
     const int rc2 = launch_rows(P, hist_possible, true, stream);
@@ -3625,7 +3722,12 @@ static int greedy_launch(const void* logits, int32_t dtype, int64_t rows, int64_
   P.aligned = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esize) % 16 == 0) &&
               vocab * (int64_t)esize >= 16;
   P.force_greedy = 1;
+  const bool prof = g_prof_start && g_prof_stop;
+  if (prof && hipEventRecord(g_prof_start, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_greedy_verify: cannot record the profiling start event");
   launch_chunk(P, dtype, (unsigned)(rows * P.C), stream);
+  if (prof && hipEventRecord(g_prof_stop, stream) != hipSuccess)
+    DSV_FAIL(DSV_ERR_LAUNCH, "dsv_greedy_verify: cannot record the profiling stop event");
   DSV_CHECK_LAUNCH("k_chunk");
   hipLaunchKernelGGL(k_greedy_accept, dim3((bs + 63) / 64), dim3(64), 0, stream, P.cstat, P.C, candidates,
                      verify_lens, cap, prefix_lens, bs, T, accept, commit, bonus, output, new_seq, top1_out);

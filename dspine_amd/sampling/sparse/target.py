@@ -46,6 +46,17 @@ def _row_indices(logits, info, row_to_request, row_offsets, block_size):
     return index // block_size
 
 
+def sparse_eligible(info, sampling_backend: str, vocab: int, capacity: int = 32) -> bool:
+    """Whether build_sparse_target takes the batch (sparse/target.py:106-116): the flashinfer
+    backend, no min-p, no greedy rows and a host-known max top-k in [1, capacity] (<= vocab)."""
+    max_k = getattr(info, "max_top_k", None)
+    return (sampling_backend == "flashinfer"
+            and not getattr(info, "need_min_p_sampling", False)
+            and not getattr(info, "is_any_greedy", False)
+            and isinstance(max_k, int) and 1 <= max_k <= capacity
+            and vocab >= 1 and max_k <= vocab)
+
+
 def build_sparse_target(logits, info, *, row_to_request=None, row_offsets=None, verify_lens=None,
                         block_size=16, capacity=32, sampling_backend="flashinfer"):
     """SparseTarget, or None when the ordinary dense path is required (sparse/target.py:95-178).

@@ -2,7 +2,10 @@
 
 ``sample_prefix`` verifies a round in one fused HIP pass (``dsv_verify``): the target
 distribution of each verified row is computed and consumed in registers/LDS, never written to
-HBM.  ``dense`` materialises P for callers that need it.
+HBM.  Batches the reference sends through ``build_sparse_target`` get its sparse joint target
+(every value tied with the k-th kept, the nucleus on the strictly larger mass, rows keeping more
+than 32 values dense); the others the backend filter of ``build_dspine_target_probs``.  ``dense``
+materialises P for callers that need it.
 """
 
 from __future__ import annotations
@@ -12,7 +15,18 @@ import copy
 import torch
 
 from dspine_amd.sampling.random import verification_uniforms
+from dspine_amd.sampling.sparse.target import sparse_eligible
 from dspine_amd.verify import Workspace, verify_step
+
+SPARSE_Q_WIDTH = 16  # the q width of the reference's sparse-q path (sampling/target.py:53-54)
+
+
+def sparse_route(info, sampling_backend: str, vocab: int, q_width: int) -> bool:
+    """Whether ``sample_prefix`` verifies against the sparse joint target: the reference's
+    sparse-q path (K = 16 q lanes, sampling/target.py:53-54) with a batch that
+    ``build_sparse_target`` accepts (sampling/target.py:58-66, sparse/target.py:106-116).  Other
+    batches use the backend filter of ``build_dspine_target_probs``."""
+    return q_width == SPARSE_Q_WIDTH and sparse_eligible(info, sampling_backend, vocab)
 
 
 class TargetDistribution:
@@ -57,9 +71,11 @@ class TargetDistribution:
         q_values = sampler.q_out[:bs]
         if q_values.dtype != torch.float32:
             q_values = q_values.float()
+        backend = self.worker.sampling_backend
+        sparse = sparse_route(sampling_info, backend, next_token_logits.shape[-1], q_ids.shape[-1])
         verify_step(logits=next_token_logits, sampling_info=sampling_info, candidates=candidates,
                     q_ids=q_ids.contiguous(), q_values=q_values.contiguous(), uniforms=uniforms,
                     uniform_final=final, prefix_lens=prefix_lens.to(torch.int32), verify_lens=verify_lens,
-                    row_offsets=row_offsets, outputs=outputs, sampling_backend=self.worker.sampling_backend,
-                    workspace=self.scratch)
+                    row_offsets=row_offsets, outputs=outputs, sampling_backend=backend,
+                    sparse_joint=sparse, workspace=self.scratch)
         return outputs

@@ -92,8 +92,8 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
                 verify_lens: torch.Tensor | None = None, row_offsets: torch.Tensor | None = None,
                 history: History | None = None, page_table: torch.Tensor | None = None,
                 outputs=None, kv_slots: torch.Tensor | None = None,
-                sampling_backend: str = "pytorch", workspace: Workspace | None = None,
-                _stages: int = 0):
+                sampling_backend: str = "pytorch", sparse_joint: bool = False,
+                workspace: Workspace | None = None, _stages: int = 0):
     """Verify one round.  Returns ``(outputs, kv_slots)`` where outputs is the 5-tuple
     ``(accept, commit, bonus, output, new_seq)``.
 
@@ -103,7 +103,10 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
     prefix_lens [bs] int32; verify_lens [bs] int32 in [1, T] (default T).  ``sampling_info``
     supplies temperatures, top_ks (>= 2^30 = off), top_ps, min_ps and the need_* /
     is_any_greedy flags, as SGLang's SamplingBatchInfo does.  Rows of requests with top_k <= 1
-    are greedy when ``is_any_greedy``.  Contract violations raise ValueError before any launch.
+    are greedy when ``is_any_greedy``.  ``sparse_joint`` selects the reference's sparse joint
+    target (sampling/sparse/target.py:95-178; the flashinfer backend, no min-p, no greedy rows,
+    max_top_k <= 32) in place of the backend filter.  Contract violations raise ValueError before
+    any launch.
     """
     lib = _lib.load()
     dev = _lib.require_cuda(logits, candidates, q_ids, q_values, uniforms, uniform_final,
@@ -192,6 +195,7 @@ def verify_step(*, logits: torch.Tensor, sampling_info, candidates: torch.Tensor
     a.kv_slots = _lib.ptr(kv_slots)
     a.workspace, a.workspace_bytes = wbuf.data_ptr(), wbuf.numel()
     a.stages = int(_stages)
+    a.sparse_joint = int(bool(sparse_joint))
     _lib.check(lib.dsv_verify(a, _lib.stream_of(dev)), "dsv_verify")
     del keep
     return outputs, kv_slots

@@ -138,9 +138,15 @@ def rejection_round(bs=32, T=17, V=151936, sigma_draft=0.5, seed=3, top_k=20, to
 
 
 def serving_round(bs=64, T=17, V=151936, seed=4, K=16, hist_len=512, dtype=torch.bfloat16, sigma=2.5,
-                  presence=0.5, repetition=1.1):
+                  presence=0.5, repetition=1.1, peak=None):
+    """``peak``: one planted logit per row at U[peak - 1, peak + 1] (a likely next token that the
+    draft's noisy top-K also ranks first), which raises the drafts' acceptance."""
     g = torch.Generator().manual_seed(seed)
-    logits = (torch.randn(bs * T, V, generator=g) * sigma).to(dtype)
+    x = torch.randn(bs * T, V, generator=g) * sigma
+    if peak is not None:
+        at = torch.randint(0, V, (bs * T,), generator=g)
+        x[torch.arange(bs * T), at] = peak - 1.0 + 2.0 * torch.rand(bs * T, generator=g)
+    logits = x.to(dtype)
     temps = torch.tensor([0.0, 0.6, 1.0])[torch.randint(0, 3, (bs,), generator=g)]
     ks = torch.tensor([0, 20])[torch.randint(0, 2, (bs,), generator=g)]
     ps = torch.tensor([1.0, 0.95])[torch.randint(0, 2, (bs,), generator=g)]
@@ -166,6 +172,41 @@ def serving_round(bs=64, T=17, V=151936, seed=4, K=16, hist_len=512, dtype=torch
         q_values=q.view(bs, T - 1, K).float(), uniforms=u[:, : T - 1].contiguous(),
         uniform_final=u[:, T - 1].contiguous(), prefix_lens=prefix, hist_ids=hist,
         presence=pres, repetition=rep, page_table=page,
+    )
+
+
+def sparse_round(bs=24, T=16, V=151936, seed=6, K=16, hist_len=64, dtype=torch.bfloat16, sigma=2.5,
+                 coarse_every=4):
+    """A batch that the reference verifies against its sparse joint target (flashinfer backend,
+    no min-p, no greedy rows, top-k <= 32): temperature {0.6, 1.0}, top-k {8, 20, 32}, top-p
+    {1.0, 0.95, 0.6}, bf16 logits N(0, sigma^2) -- at top-k 20 most rows tie at the k-th value
+    -- and every ``coarse_every``-th request with integer-valued logits N(0, 1) rounded, whose
+    rows hold hundreds of ties at the k-th value (more than 32 kept: dense rows).  Presence /
+    repetition penalties over a short history; sparse q [bs, T-1, K] from noisy target rows."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(bs * T, V, generator=g) * sigma
+    for b in range(0, bs, max(1, coarse_every)):
+        x[b * T:(b + 1) * T] = torch.round(torch.randn(T, V, generator=g))
+    logits = x.to(dtype)
+    temps = torch.tensor([0.6, 1.0])[torch.randint(0, 2, (bs,), generator=g)]
+    ks = torch.tensor([8, 20, 32])[torch.randint(0, 3, (bs,), generator=g)]
+    ps = torch.tensor([1.0, 0.95, 0.6])[torch.randint(0, 3, (bs,), generator=g)]
+    info = sampling_info(temps, ks, ps)
+    hist = torch.randint(0, V, (bs, hist_len), generator=g, dtype=torch.int64).to(torch.int32)
+    noisy = logits.view(bs, T, V)[:, : T - 1].float() + 0.5 * torch.randn(bs, T - 1, V, generator=g)
+    vals, ids = torch.topk(noisy.reshape(-1, V), K, dim=-1)
+    order = ids.argsort(-1)
+    q_ids = ids.gather(-1, order)
+    q = torch.softmax(vals.gather(-1, order), -1)
+    lanes = _sample_lanes(q, g)
+    drafts = q_ids.gather(1, lanes[:, None]).view(bs, T - 1)
+    cand = torch.cat((torch.randint(0, V, (bs, 1), generator=g), drafts), 1)
+    u = philox_uniforms(seed, bs, T)
+    return dict(
+        logits=logits, info=info, candidates=cand, q_ids=q_ids.view(bs, T - 1, K),
+        q_values=q.view(bs, T - 1, K).float(), uniforms=u[:, : T - 1].contiguous(),
+        uniform_final=u[:, T - 1].contiguous(), prefix_lens=torch.full((bs,), 300, dtype=torch.int32),
+        hist_ids=hist, presence=torch.full((bs,), 0.5), repetition=torch.full((bs,), 1.1),
     )
 
 

@@ -97,6 +97,14 @@ typedef struct dsv_verify_args {
   int32_t need_min_p;
   int32_t any_greedy;            /* rows of requests with top_k <= 1 are one-hot at argmax */
   int32_t max_top_k;             /* host-known bound on top_ks (SamplingBatchInfo.max_top_k) */
+  /* 1: the reference's sparse joint target (sampling/sparse/target.py:95-178), the route        */
+  /* TargetDistribution.sample_prefix takes for flashinfer batches build_sparse_target accepts   */
+  /* (sampling/target.py:53-66): keep every p >= the k-th largest p (all its ties) whose         */
+  /* strictly larger p hold less than top_p; a row keeping more than 32 becomes a dense row of    */
+  /* every p >= the k-th.  Requires the flashinfer backend, no min-p, no greedy rows and         */
+  /* 1 <= max_top_k <= 32 (the filter applies whatever the need_* flags).  dsv_verify only.      */
+  int32_t sparse_joint;
+  int32_t pad0;
   /* optional presence / repetition penalty over a token history [bs, hist_len] (-1 = pad) */
   const int32_t* hist_ids;
   int32_t hist_len, pad1;
@@ -127,9 +135,10 @@ typedef struct dsv_verify_args {
 int64_t dsv_verify_workspace_bytes(int64_t rows, int32_t bs, int32_t T, int64_t vocab);
 int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream);
 
-/* Profiling aid with no counterpart in the reference: the calling thread's later dsv_verify   */
-/* and dsv_topk calls record `start` / `stop` (hipEvent_t, timing enabled) on their stream     */
-/* right before and after the chunk-pass kernel, so a benchmark can time that kernel alone.    */
+/* Profiling aid with no counterpart in the reference: the calling thread's later dsv_verify,  */
+/* dsv_greedy_verify and dsv_topk calls record `start` / `stop` (hipEvent_t, timing enabled)   */
+/* on their stream right before and after the chunk-pass kernel, so a benchmark can time that */
+/* kernel alone.                                                                               */
 /* NULL, NULL: off.                                                                            */
 int dsv_profile_events(void* start, void* stop);
 

@@ -815,14 +815,36 @@ def request_of_rows(bs, T, verify_lens=None, row_offsets=None, rows=None):
     return np.searchsorted(offs, np.arange(total), side="right") - 1
 
 
+SPARSE_CAPACITY = 32  # packed capacity of the sparse joint target (sampling/target.py:84-87)
+
+
+def sparse_route(info, sampling_backend, vocab, q_width, capacity=SPARSE_CAPACITY) -> bool:
+    """Whether TargetDistribution.sample_prefix verifies against the sparse joint target:
+    its sparse-q path needs K = 16 q lanes (sampling/target.py:53-54) and build_sparse_target
+    takes only flashinfer batches without min-p or greedy rows whose host-known max top-k lies in
+    [1, capacity] and within the vocabulary (sampling/sparse/target.py:106-116)."""
+    max_k = getattr(info, "max_top_k", None)
+    return (int(q_width) == 16 and sampling_backend == "flashinfer"
+            and not getattr(info, "need_min_p_sampling", False)
+            and not getattr(info, "is_any_greedy", False)
+            and isinstance(max_k, int) and 1 <= max_k <= capacity and 1 <= vocab and max_k <= vocab)
+
+
 def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, uniforms,
                 uniform_final, prefix_lens, hist_ids=None, presence=None, repetition=None,
                 page_table=None, row_offsets=None, sampling_backend="pytorch", requests=None,
-                exact_softmax=False):
+                exact_softmax=False, sparse_joint=False):
     """The fused verify step on the CPU: history penalties -> target P per verified row ->
     sparse-q chain rejection -> compaction + KV slots.  ``logits`` is [rows, V] (bf16/fp32) in
     the dense ``b*T+s`` layout or ragged with ``row_offsets``.  ``requests`` (optional) limits
     the work to a subset of requests (outputs of the others are left zero).
+
+    ``sparse_joint``: the route TargetDistribution.sample_prefix takes for batches that
+    build_sparse_target accepts (``sparse_route``; sampling/target.py:58-121): the softmax rows'
+    sparse joint target (``sparse_target``, capacity 32) as packed P, its overflow rows dense,
+    then accept_sparse on them (packed rows: lanes summed at an id, sampling/sparse/accept.py:
+    179-204; dense rows: the last lane).  Otherwise the backend filter of
+    build_dspine_target_probs (runtime/worker.py:440-508).
 
     Returns a dict with accept/commit/bonus/output/new_seq/kv_slots/margins and ``probs``
     (dict row -> float32 target row) for the verified rows that were built."""
@@ -845,8 +867,24 @@ def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, unifo
         adjust_logits(x, SimpleNamespace(acc_additive_penalties=add, acc_scaling_penalties=scl),
                       owner_t)
     rinfo = row_info(info, owner_t)
-    P = build_target_probs(x, rinfo, 1, len(rows), sampling_backend,
-                           exact_softmax=exact_softmax).reshape(len(rows), V)
+    packed = None
+    if sparse_joint:
+        p = softmax_temp(x, rinfo.temperatures.view(-1), exact=exact_softmax)
+        ids, vals, lens, ovf, dense = sparse_target(p, rinfo.top_ks, rinfo.top_ps, SPARSE_CAPACITY)
+        P = dense
+        # packed P indexed by the logits row, as accept_sparse reads it
+        total = int(logits.shape[0])
+        g_ids = np.full((total, SPARSE_CAPACITY), -1, np.int32)
+        g_vals = np.zeros((total, SPARSE_CAPACITY), np.float32)
+        g_lens = np.zeros(total, np.int32)
+        g_ovf = np.zeros(total, np.int32)
+        idx = np.asarray(rows, dtype=np.int64)
+        g_ids[idx], g_vals[idx] = ids.numpy(), vals.numpy()
+        g_lens[idx], g_ovf[idx] = lens.numpy(), ovf.numpy()
+        packed = (g_ids, g_vals, g_lens, g_ovf)
+    else:
+        P = build_target_probs(x, rinfo, 1, len(rows), sampling_backend,
+                               exact_softmax=exact_softmax).reshape(len(rows), V)
     probs = {r: P[i].numpy() for i, r in enumerate(rows)}
     sub = np.asarray(reqs, dtype=np.int64)
     qi = None if q_ids is None else np.asarray(q_ids)[sub]
@@ -855,7 +893,7 @@ def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, unifo
     sub_base = np.array([base[b] for b in reqs], dtype=np.int64)
     acc = chain_accept(lambda r: probs[r], cand[sub], qi, qv, caps[sub],
                        np.asarray(uniforms)[sub], np.asarray(uniform_final)[sub],
-                       np.asarray(prefix_lens)[sub], row_offsets=sub_base)
+                       np.asarray(prefix_lens)[sub], row_offsets=sub_base, packed=packed)
     accept = np.zeros(bs, np.int32)
     commit = np.zeros(bs, np.int32)
     bonus = np.zeros(bs, np.int64)
@@ -872,4 +910,4 @@ def verify_step(logits, info, *, candidates, q_ids, q_values, verify_lens, unifo
         for j, b in enumerate(reqs):
             slots[b] = ks[j]
     return dict(accept=accept, commit=commit, bonus=bonus, output=output, new_seq=new_seq,
-                kv_slots=slots, margins=margins, probs=probs, adjusted=dict(zip(rows, x)))
+                kv_slots=slots, margins=margins, probs=probs, adjusted=dict(zip(rows, x)), packed=packed)

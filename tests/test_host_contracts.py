@@ -129,6 +129,27 @@ def test_sparse_target_eligibility():
         build_sparse_target(logits[None], info)
 
 
+def test_sample_prefix_route_rule():
+    """The sparse joint route (sampling/target.py:53-66, sparse/target.py:106-116): the host rule
+    and the oracle's restatement agree, and each condition alone turns it off."""
+    import oracle.verify_oracle as O
+    from dspine_amd import workloads as W
+    from dspine_amd.sampling.target import sparse_route
+
+    info = W.sampling_info([1.0, 0.6], [20, 8], [0.95, 1.0])
+    for backend, vocab, K in (("flashinfer", 1000, 16), ("pytorch", 1000, 16), ("flashinfer", 1000, 8),
+                              ("flashinfer", 10, 16)):
+        assert sparse_route(info, backend, vocab, K) == O.sparse_route(info, backend, vocab, K)
+    assert sparse_route(info, "flashinfer", 1000, 16)
+    assert not sparse_route(info, "flashinfer", 10, 16)  # max top-k above the vocabulary
+    for bad in (W.sampling_info([1.0, 0.0], [20, 8], [0.95, 1.0]),               # a greedy row
+                W.sampling_info([1.0, 0.6], [20, 0], [0.95, 1.0]),               # top-k off
+                W.sampling_info([1.0, 0.6], [20, 8], [0.95, 1.0], [0.1, 0.0]),   # min-p
+                W.sampling_info([1.0, 0.6], [40, 8], [0.95, 1.0])):              # top-k above 32
+        assert not sparse_route(bad, "flashinfer", 1000, 16)
+        assert not O.sparse_route(bad, "flashinfer", 1000, 16)
+
+
 def test_worker_refuses_stale_rounds():
     """runtime/worker.py:1030-1037 and sampling/target.py:45-49."""
     from dspine_amd.runtime import worker as Wk
