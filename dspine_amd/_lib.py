@@ -71,6 +71,7 @@ class ChainArgs(ctypes.Structure):
         ("dense_q", vp), ("q_stride", i64),
         ("q_ids", vp), ("q_ids_i64", i32), ("pad3", i32), ("q_values", vp),
         ("accept", vp), ("commit", vp), ("bonus", vp), ("output", vp), ("new_seq", vp),
+        ("overflow_read", vp),
     ]
 
 

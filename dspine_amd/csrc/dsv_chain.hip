@@ -474,6 +474,15 @@ __global__ __launch_bounds__(CH_THREADS) void k_chain(dsv_chain_args a) {
   const int acc = sh.acc;
   const bool all = acc == cap - 1;
   const int64_t row = chain_row(a, b, acc);
+  if (a.overflow_read && tid < WAVE) {
+    // rows 0..acc were read (the draft tests and the bonus row): any flagged overflow without a
+    // dense fallback is reported
+    bool bad = false;
+    if (!a.dense_p && a.p_overflow)
+      for (int s = lane; s <= acc; s += WAVE) bad |= a.p_overflow[chain_row(a, b, s)] != 0;
+    const bool any = __ballot(bad) != 0ull;
+    if (lane == 0) a.overflow_read[b] = any ? 1 : 0;
+  }
   const float uf = a.uniform_final[b];
   int64_t bonus = V - 1;
   // the sparse q of the rejected step

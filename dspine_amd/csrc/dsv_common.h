@@ -42,8 +42,14 @@ __device__ __forceinline__ T ld_dev(const T* p) {
   return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this thread's memory accesses have completed (s_waitcnt vmcnt(0); the other
-// counters are left at their maxima: expcnt 7, lgkmcnt 15).
-__device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// counters are left at their maxima: expcnt 7, lgkmcnt 15).  The compiler treats the wait as
+// touching no memory, so compiler-only barriers on both sides keep the publishing stores before
+// it and the counter's atomic after it (no instruction is emitted for them).
+__device__ __forceinline__ void publish_wait() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
 
 // ---------------------------------------------------------------------------------------
 // Order-preserving keys.  -0.0 is folded onto +0.0 so that equal values share one key, as

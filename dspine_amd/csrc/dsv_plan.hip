@@ -178,8 +178,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_sps_plan(const float* raw, int
     const int n = lens[b];
     if (raw) lens_io[b] = n;
     if (qo_out) qo_out[b] = start;
+    // (given lengths that do not sum to the budget -- a caller's error -- write only the
+    // index's `budget` entries; qo_indptr[bs] reports their total)
     if (index_out)
-      for (int d = 0; d < n; ++d) index_out[start + d] = (int64_t)b * full + d;
+      for (int d = 0; d < n; ++d)
+        if ((unsigned)(start + d) < (unsigned)budget) index_out[start + d] = (int64_t)b * full + d;
     start += n;
   }
   if (qo_out && tid == 0) qo_out[bs] = total;
@@ -205,6 +208,7 @@ extern "C" int dsv_sps_plan(const float* raw, int64_t raw_stride, int32_t bs, in
     if (boundaries && (n_boundaries < 0 || n_boundaries > n_bins - 1))
       DSV_FAIL(DSV_ERR_INVALID, "dsv_sps_plan: %d boundaries for %d bins", n_boundaries, n_bins);
   }
+  if (!raw && window_index && budget < 0) DSV_FAIL(DSV_ERR_INVALID, "dsv_sps_plan: negative budget %d", budget);
   const int64_t lds = ((raw ? N : 0) + bs) * 4;
   if (lds > PLAN_LDS_MAX)
     DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_sps_plan: bs %d x gamma %d exceeds one workgroup's LDS", bs, gamma);

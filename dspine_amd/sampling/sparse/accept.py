@@ -120,7 +120,7 @@ def fill_sparse_q(a, q_ids, q_values, bs, t):
 
 def accept_sparse(torch, *, candidates, dense_p, packed, q_ids, q_values, verify_lens, uniforms,
                   uniform_final, prefix_lens, outputs, scratch=None, denominator=None,
-                  raw_fallback=False, row_offsets=None, vocab_size=None):
+                  raw_fallback=False, row_offsets=None, vocab_size=None, overflow_read=None):
     """Chain rejection with sparse q (sparse/accept.py:463-543); writes and returns ``outputs``
     = (accept int32 [bs], commit int32 [bs], bonus int64 [bs], output int64 [bs, T],
     new_seq int32 [bs]).
@@ -132,7 +132,12 @@ def accept_sparse(torch, *, candidates, dense_p, packed, q_ids, q_values, verify
     row subtracts the clamped q of the last lane with an id, that of a packed row the clamped q
     summed over the lanes with the id.  ``scratch`` is accepted for the reference's signature
     (the HIP kernel keeps its tiles in LDS).  T >= 2 and K <= 64 (the reference is fixed at
-    T = K = 16)."""
+    T = K = 16).
+
+    ``overflow_read`` (optional int32 [bs], written on the device): 1 for a request that read a
+    packed row flagged overflow with no ``dense_p`` to fall back on -- where the reference stops
+    on the device (sparse/accept.py:257, :291), its outputs come from the row's packed prefix --
+    else 0."""
     del torch, scratch
     bs, t = candidates.shape
     if dense_p is None:
@@ -184,6 +189,11 @@ def accept_sparse(torch, *, candidates, dense_p, packed, q_ids, q_values, verify
         _lib.require_cuda(*packed)
         a.p_ids, a.p_values, a.p_lengths = ids.data_ptr(), vals.data_ptr(), lens.data_ptr()
         a.p_overflow, a.p_cap = overflow.data_ptr(), ids.shape[1]
+    if overflow_read is not None:
+        if (overflow_read.shape != (bs,) or overflow_read.dtype != _torch.int32 or not overflow_read.is_contiguous()
+                or overflow_read.device != candidates.device):
+            raise ValueError("overflow_read must be a contiguous device int32 [bs] tensor")
+        a.overflow_read = overflow_read.data_ptr()
     if bs:
         _lib.check(_lib.load().dsv_accept_chain(a, _lib.stream_of(dev)), "dsv_accept_chain")
     del keep

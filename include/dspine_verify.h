@@ -264,6 +264,10 @@ typedef struct dsv_chain_args {
   int64_t* bonus;             /* [bs] */
   int64_t* output;            /* [bs, T] */
   int32_t* new_seq;           /* [bs] */
+  /* [bs] or NULL: 1 where the request read a packed row flagged overflow with no dense P to  */
+  /* fall back on (the reference stops on the device there, sampling/sparse/accept.py:257,   */
+  /* :291; the outputs then come from the row's packed prefix), else 0                       */
+  int32_t* overflow_read;
 } dsv_chain_args;
 int dsv_accept_chain(const dsv_chain_args* args, dsv_stream_t stream);
 
@@ -285,7 +289,9 @@ int dsv_sample_chain(const float* table, int64_t n, int32_t K, int32_t block_siz
 /* request's root: verify_lens [bs] int32 (1 + selected positions), qo_indptr [bs + 1] int32  */
 /* (exclusive prefix, may be NULL), window_index [budget] int64 (b * (gamma + 1) + d, may be  */
 /* NULL).  bs <= budget <= bs * (gamma + 1).  raw == NULL: verify_lens is an input and only   */
-/* the layout (qo_indptr, window_index) is written.  bs * gamma + bs <= 38912.               */
+/* the layout (qo_indptr, window_index) is written; window_index holds budget entries, and    */
+/* lengths summing past it write only those (qo_indptr[bs] is their sum).                    */
+/* bs * gamma + bs <= 38912.                                                                  */
 int dsv_sps_plan(const float* raw, int64_t raw_stride, int32_t bs, int32_t gamma, const float* probabilities,
                  int64_t prob_stride, int32_t n_bins, int64_t prob_rows, const int64_t* depth,
                  const double* boundaries, int32_t n_boundaries, int32_t budget, int32_t* verify_lens,

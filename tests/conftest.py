@@ -19,10 +19,12 @@ def pytest_terminal_summary(terminalreporter):
     if not parity.RECORDS:
         return
     tr = terminalreporter
-    tr.section(f"parity vs oracle (near-margin: oracle margin < {parity.MARGIN:g})")
+    tr.section(f"parity vs oracle (near-margin: oracle margin < {parity.MARGIN:g}; literal fp32 softmax rows: "
+               f"< {parity.LITERAL_MARGIN:g})")
     total = [0, 0, 0]
     for tag, compared, near, differing in parity.RECORDS:
-        tr.write_line(f"{tag}: compared {compared}, near-margin {near}, differing {len(differing)} {differing}")
+        tr.write_line(f"{tag}: compared {compared}, near-margin {near}, differing {len(differing)} "
+                      f"{parity._fmt(differing)}")
         total[0] += compared
         total[1] += near
         total[2] += len(differing)

@@ -88,7 +88,7 @@ def _compare(name, z, got, names):
         if not same:
             assert margins is not None and margins[b] < MARGIN, (name, b, {k: got[k][b] for k in names},
                                                                  {k: z["expect_" + k][b] for k in names})
-            differing.append(b)
+            differing.append((b, float(margins[b])))
     near = 0 if margins is None else int((margins < MARGIN).sum())
     parity.record(f"golden {name}", n, near, differing)
 

@@ -42,7 +42,8 @@ def _check_chain(outs, ref, tag, max_near=0):
             assert ref[5][b] < MARGIN, (tag, b, {n: g[b] for n, g in zip(names, got)},
                                         {n: r[b] for n, r in zip(names, ref)}, ref[5][b])
             near.append(b)
-    parity.record(tag, got[0].shape[0], int((np.asarray(ref[5]) < MARGIN).sum()), near)
+    parity.record(tag, got[0].shape[0], int((np.asarray(ref[5]) < MARGIN).sum()),
+                  [(b, float(ref[5][b])) for b in near])
     assert len(near) <= max_near, (tag, near)
 
 
@@ -141,6 +142,31 @@ def test_accept_sparse_compact_packed(device, bs, kind):
     _check_chain(outs, ref, f"packed {kind} bs={bs}")
     if bs > 1:
         assert int(outs[0][0]) == 15  # u = 0 accepts every draft
+
+
+@pytest.mark.parametrize("bs", [9, 65])
+def test_accept_sparse_reports_overflow_without_dense(device, bs):
+    """Packed rows flagged overflow with no dense P to fall back on (where the reference stops on
+    the device, sparse/accept.py:257, :291): overflow_read marks the requests whose walk read one
+    (the draft tests' rows and the bonus row); with the dense fallback nothing is marked."""
+    from dspine_amd.sampling.sparse.accept import accept_sparse, compress_probs
+
+    c = _compact_case(bs, "overflow")
+    d = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in c.items()}
+    packed = compress_probs(torch, d["p"], capacity=32)
+    status = torch.full((bs,), -1, dtype=torch.int32, device=device)
+    for dense in (None, d["p"]):
+        outs = _outputs(bs, 16, device)
+        accept_sparse(torch, candidates=d["cand"], dense_p=dense, packed=packed, q_ids=d["qids"], q_values=d["qvals"],
+                      verify_lens=d["caps"], uniforms=d["u"], uniform_final=d["uf"], prefix_lens=d["prefix"],
+                      outputs=outs, row_offsets=d["offsets"], vocab_size=c["vocab"], overflow_read=status)
+        torch.cuda.synchronize()
+        acc = outs[0].cpu().tolist()
+        ovf = packed[3].cpu().tolist()
+        offs = c["offsets"].tolist()
+        want = [int(dense is None and any(ovf[offs[b] + s] for s in range(acc[b] + 1))) for b in range(bs)]
+        assert status.cpu().tolist() == want
+        assert any(want) == (dense is None)
 
 
 @pytest.mark.parametrize("bs", [1, 17, 65])
@@ -724,7 +750,8 @@ def test_worker_seam_fused_equals_explicit(device):
             if a[i] != ref[name][i] or b[i] != ref[name][i]:
                 assert ref["margins"][i] < MARGIN, (name, i, a[i], b[i], ref[name][i])
                 differing.add(i)
-    parity.record("worker seam (fused, explicit P)", bs, int((ref["margins"] < MARGIN).sum()), sorted(differing))
+    parity.record("worker seam (fused, explicit P)", bs, int((ref["margins"] < MARGIN).sum()),
+                  [(i, float(ref["margins"][i])) for i in sorted(differing)])
     assert len(differing) <= 1, differing
     Wk.set_active_worker(None)
 

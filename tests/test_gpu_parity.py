@@ -456,33 +456,40 @@ def test_verify_unfiltered(device):
     assert len(compare_outputs(gpu, ref, range(bs), "unfiltered")) <= 1
 
 
-def test_verify_serving_round_full(device):
-    """The benchmark's serving workload (64 x 17 x 151936 bf16, penalties, mixed modes, KV
-    slots): every request against the oracle."""
-    batch = W.serving_round()
+def _full(batch, device, tag):
+    """Every request against the oracle with its exact softmax (the parity bound), then against
+    its literal float32 softmax (recorded, tests/parity.py)."""
     bs = batch["candidates"].shape[0]
     gpu = run_gpu_verify(batch, device)
     ref = run_oracle(batch, list(range(bs)))
-    compare_outputs(gpu, ref, range(bs), "serving 64x17x151936 bf16")
+    compare_outputs(gpu, ref, range(bs), tag)
+    literal = run_oracle(batch, list(range(bs)), exact_softmax=False)
+    parity.compare_literal(gpu, literal, ref, range(bs), tag)
+    return gpu, ref
+
+
+def test_verify_serving_round_full(device):
+    """The benchmark's serving workload (64 x 17 x 151936 bf16, penalties, mixed modes, KV
+    slots): every request against the oracle."""
+    _full(W.serving_round(), device, "serving 64x17x151936 bf16")
+
+
+def test_verify_serving_round_deep_accept(device):
+    """The serving workload with a planted likely token per row (the bench's --accept deep):
+    deep accepted prefixes, so the accepted row and the bonus draw lie far down the requests."""
+    gpu, ref = _full(W.serving_round(peak=16.0), device, "serving deep-accept 64x17x151936 bf16")
+    assert ref["accept"].mean() > 4.0, ref["accept"].mean()
 
 
 @pytest.mark.parametrize("sigma", [0.5, 1.5])
 def test_verify_rejection_round_full(device, sigma):
     """The rejection workload (32 x 17 x 151936 fp32, top-k 20, top-p 0.95): every request."""
-    batch = W.rejection_round(sigma_draft=sigma)
-    bs = batch["candidates"].shape[0]
-    gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, list(range(bs)))
-    compare_outputs(gpu, ref, range(bs), f"rejection 32x17x151936 fp32 sigma={sigma}")
+    _full(W.rejection_round(sigma_draft=sigma), device, f"rejection 32x17x151936 fp32 sigma={sigma}")
 
 
 def test_verify_ragged_round_full(device):
     """The ragged workload (32 requests x U{4..16} rows x 262144 bf16, Student-t): every request."""
-    batch = W.ragged_round()
-    bs = batch["candidates"].shape[0]
-    gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, list(range(bs)))
-    compare_outputs(gpu, ref, range(bs), "ragged 32x(4..16)x262144 bf16")
+    _full(W.ragged_round(), device, "ragged 32x(4..16)x262144 bf16")
 
 
 def test_topk_rows_full(device):
@@ -508,7 +515,7 @@ def test_target_p_error_bounds_margin(device):
     """The dense target P of the HIP path against the float64 softmax (rounded once) and
     against CPU torch's float32 softmax on the serving workload's rows (all four modes): the
     largest relative error against the exact softmax on entries >= 1e-6 of the row max stays
-    below a quarter of MARGIN, so a decision further than MARGIN from its boundary (as the
+    below half of MARGIN, so a decision further than MARGIN from its boundary (as the
     oracle's exact softmax places it) cannot come out differently."""
     from dspine_amd.runtime.worker import build_dspine_target_probs
 
@@ -536,9 +543,9 @@ def test_target_p_error_bounds_margin(device):
           f"vs CPU torch float32 {errs[False][0]:.3g} ({errs[False][1]} rows with another cut)", flush=True)
     # the parity tests compare against the exact softmax: the HIP path's P must sit well inside
     # MARGIN of it, with the same cut on every row
-    assert errs[True][0] < MARGIN / 4, errs
+    assert errs[True][0] < MARGIN / 2, errs
     assert errs[True][1] == 0, errs
     # CPU torch's float32 normaliser is itself ~1e-5 off on these 151936-wide rows and cuts
     # some top-p rows inside a bf16 tie group elsewhere (the reason the oracle's exact softmax
     # is the parity reference); bounded here only to keep the figure on record
-    assert errs[False][0] < 1e-4, errs
+    assert errs[False][0] < parity.LITERAL_MARGIN, errs

@@ -145,3 +145,23 @@ def test_plan_tp_synchronised_lengths(device):
     assert torch.equal(layout.verify_lens.cpu(), leader)
     assert np.array_equal(layout.qo_indptr_device.cpu().numpy(), qo_ref)
     assert np.array_equal(index.cpu().numpy(), idx_ref)
+
+
+def test_plan_given_lengths_past_the_budget(device):
+    """Given lengths (the TP-synchronised path) that sum past the budget write only the index's
+    budget entries: the entries after it keep their sentinel, and qo_indptr[bs] reports the sum."""
+    from dspine_amd.verification.sps import _plan
+
+    bs, gamma, budget = 6, 7, 20
+    lens = torch.tensor([8, 8, 1, 8, 8, 8], dtype=torch.int32, device=device)  # 41 > 20
+    qo = torch.empty(bs + 1, dtype=torch.int32, device=device)
+    store = torch.full((budget + 64,), -7, dtype=torch.int64, device=device)
+    index = store[:budget]
+    depth = torch.arange(1, gamma + 1, dtype=torch.int64, device=device)
+    _plan(None, None, depth, budget, None, lens, qo, index)
+    torch.cuda.synchronize()
+    full = gamma + 1
+    want = [b * full + d for b, n in enumerate(lens.tolist()) for d in range(n)][:budget]
+    assert store[:budget].tolist() == want
+    assert (store[budget:] == -7).all()
+    assert qo.tolist() == [0, 8, 16, 17, 25, 33, 41]

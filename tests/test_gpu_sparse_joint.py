@@ -43,7 +43,7 @@ def _gpu(batch, device, sparse_joint=True, backend="flashinfer"):
     return {n: t.cpu().numpy() for n, t in zip(NAMES, outs)}
 
 
-def _oracle(batch, sparse_joint=True):
+def _oracle(batch, sparse_joint=True, exact_softmax=True):
     O = _O()
     bs, T = batch["candidates"].shape
     lens = batch.get("verify_lens")
@@ -54,7 +54,7 @@ def _oracle(batch, sparse_joint=True):
         uniform_final=batch["uniform_final"].numpy(), prefix_lens=batch["prefix_lens"].numpy(),
         hist_ids=batch.get("hist_ids"), presence=batch.get("presence"), repetition=batch.get("repetition"),
         row_offsets=None if batch.get("row_offsets") is None else batch["row_offsets"].numpy(),
-        sampling_backend="flashinfer", exact_softmax=True, sparse_joint=sparse_joint)
+        sampling_backend="flashinfer", exact_softmax=exact_softmax, sparse_joint=sparse_joint)
 
 
 def _tie_stats(ref, batch):
@@ -83,8 +83,9 @@ def test_sparse_joint_full_vocab(device):
     tied, dense = _tie_stats(ref, batch)
     assert tied > 100 and dense > 20, (tied, dense)  # the case exercises both
     got = _gpu(batch, device)
-    parity.compare_requests(got, ref, range(bs), f"sparse joint 24x16x151936 bf16 (tied rows {tied}, dense {dense})",
-                            extra=())
+    tag = f"sparse joint 24x16x151936 bf16 (tied rows {tied}, dense {dense})"
+    parity.compare_requests(got, ref, range(bs), tag, extra=())
+    parity.compare_literal(got, _oracle(batch, exact_softmax=False), ref, range(bs), tag)
     # the route matters: the rank-based flashinfer filter differs on some of these requests
     rank = _oracle(batch, sparse_joint=False)
     assert any(not np.array_equal(rank[n], ref[n]) for n in ("accept", "bonus")), "the case should tell the routes apart"
