@@ -994,9 +994,10 @@ __device__ __forceinline__ void merge_row(const KParams& P, int64_t r, int b, in
 // Nucleus rows (a top-p / min-p cut with top-k > 64).
 //
 // The chunk pass counts, per chunk, the values whose key lies in a window [wlo, kmax] below the
-// chunk max, where wlo is the lowest key whose probability bound exp((x - m_c) / T) / s_c (the
-// chunk's own softmax sum understates Z, so the bound is an upper bound on p) reaches half of
-// the row floor eps.  The row merge knows Z and the exact floor eps = (sum p - top_p - 1e-6) / V:
+// chunk max, where wlo is the lowest key whose probability estimate (the chunk's values other than
+// its maximum standing for each other chunk's mass) reaches 2 (1 - top_p) / V; the estimate is a
+// heuristic, the merge checks what the windows cover.  The row merge knows Z and the exact floor
+// eps = (sum p - top_p - 1e-6) / V:
 // the values with p < eps hold less than sum p - top_p together, so the cut -- the first value
 // in (value desc, id asc) order that top-k, min-p or top-p removes -- is at or above the first
 // value below the lowest key kb with p(kb) >= eps.  When every chunk window reaches down to kb
@@ -2214,16 +2215,19 @@ __global__ __launch_bounds__(CT, ALIGNED ? (DT == DSV_BF16 ? 7 : 6) : 5) void k_
     if constexpr (DT == DSV_BF16) {
       // counts of the values in the window [wlo, kmax] where the row's cut is expected: wlo is
       // the higher of kmax - (HWIN - 1) and the lowest key whose probability estimate
-      // exp((x - m) / T) / (s * C) (this chunk's sum standing for each of the row's C chunks)
-      // reaches 2 (1 - top_p) / V.  The row merge takes the cut from the counts when it lies
-      // in every chunk's window, and the full-histogram path otherwise.
+      // exp((x - m) / T) / (s + (C - 1)(s - 1)) reaches 2 (1 - top_p) / V -- the chunk's values
+      // other than its maximum (whose term is 1) standing for each of the row's other chunks, so
+      // that a chunk holding a dominant peak does not take the peak for every chunk's mass.  The
+      // row merge takes the cut from the counts when it lies in every chunk's window, and the
+      // full-histogram path otherwise.
       uint32_t* cnt = reinterpret_cast<uint32_t*>(big);
       if (wid == 0) {
         uint32_t wlo = WIN_EMPTY;
         if (cbest) {
           const uint32_t kmax = unpack_key(cbest);
           uint32_t kb = 0x80u;  // the lowest finite key
-          const float floor_e = 2.f * (1.f - top_p) / (float)V * (float)(out.s * (double)C);
+          const double z_est = out.s * (double)C - (double)(C - 1);
+          const float floor_e = 2.f * (1.f - top_p) / (float)V * (float)(z_est > 1.0 ? z_est : 1.0);
           if (floor_e > 0.f && kmax > 0x80u) {
             const float c2 = log2e_over(T);
             // the closed form's key, x = m + log2(floor) / c2, as the search's guess
