@@ -60,7 +60,11 @@ PINNED = {
     "packed_bonus": "packed == dense identity on the same P and coins "
     "(tests/test_sparse_accept_compact.py:58-105, whose pure-Python reference :22-53 is the spec)",
     "sparse_target": "equals the full-vocabulary joint filter (flashinfer restatement) on unique "
-    "scores, closed-form overflow densification; tie order at the k-th place unpinned",
+    "scores; hand-computed ties at the k-th place and the strict nucleus of sampling/sparse/target.py:"
+    "158-165; a brute-force restatement of the support's definition on rows of many ties; closed-form "
+    "overflow densification",
+    "sparse_route": "the eligibility rules of sampling/target.py:53-54 and sampling/sparse/target.py:"
+    "106-116, each turned off alone",
 }
 
 

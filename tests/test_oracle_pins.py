@@ -513,6 +513,55 @@ def test_sparse_target_overflow_rows_are_densified():
     torch.testing.assert_close(dense[0], expect / expect.sum(), rtol=1e-6, atol=0)
 
 
+def test_sparse_target_ties_known_answers():
+    """The reference's CPU branch (sampling/sparse/target.py:158-165) by hand: every p tied with
+    the k-th is kept, and the nucleus tests the mass of the strictly larger p (p = [.3, .2, .2,
+    .2, .1], k = 2)."""
+    p = torch.tensor([[0.3, 0.2, 0.2, 0.2, 0.1]] * 4)
+    ks = torch.tensor([2, 2, 2, 2])
+    ps = torch.tensor([1.0, 0.4, 0.3, 0.31])
+    ids, vals, lens, ovf, dense = O.sparse_target(p, ks, ps, 8)
+    assert lens.tolist() == [4, 4, 1, 4] and ovf.tolist() == [0, 0, 0, 0]
+    for r in (0, 1, 3):  # the three ties of the 2nd value are kept: 0.3 < top_p, or top_p = 1
+        assert ids[r, :4].tolist() == [0, 1, 2, 3]
+        torch.testing.assert_close(vals[r, :4], torch.tensor([0.3, 0.2, 0.2, 0.2]) / 0.9, rtol=1e-6, atol=0)
+    assert ids[2, :1].tolist() == [0] and float(vals[2, 0]) == 1.0  # mass 0.3 ahead of the ties: not < 0.3
+
+
+def test_sparse_target_brute_force_definition():
+    """Rows with many ties: the support is, by definition, every p > 0 with fewer than k values
+    strictly larger and (top_p >= 1 or their mass < top_p); packed ids ascending with p / sum,
+    overflow when more than the capacity are kept (then the dense row holds them)."""
+    g = torch.Generator().manual_seed(11)
+    rows, V, cap = 40, 60, 8
+    levels = torch.randint(0, 6, (rows, V), generator=g).float()
+    p = torch.softmax(levels * 0.7, -1)
+    ks = torch.randint(1, 8, (rows,), generator=g)
+    ps = torch.tensor([1.0, 0.9, 0.5, 0.3, 0.05])[torch.randint(0, 5, (rows,), generator=g)]
+    ids, vals, lens, ovf, dense = O.sparse_target(p, ks, ps, cap)
+    n_ovf = 0
+    for r in range(rows):
+        row = p[r].double()
+        keep = []
+        for j in range(V):
+            larger = row > row[j]
+            if row[j] > 0 and int(larger.sum()) < int(ks[r]) and (
+                    float(ps[r]) >= 1 or float(row[larger].sum()) < float(ps[r])):
+                keep.append(j)
+        total = float(row[keep].sum())
+        if len(keep) > cap:
+            n_ovf += 1
+            assert int(ovf[r]) == 1
+            want = torch.zeros(V, dtype=torch.float64)
+            want[keep] = row[keep] / total
+            torch.testing.assert_close(dense[r].double(), want, rtol=2e-6, atol=0)
+        else:
+            assert int(ovf[r]) == 0 and int(lens[r]) == len(keep)
+            assert ids[r, :len(keep)].tolist() == keep
+            torch.testing.assert_close(vals[r, :len(keep)].double(), row[keep] / total, rtol=2e-6, atol=0)
+    assert 0 < n_ovf < rows
+
+
 def test_sample_chain_confidence_known_answers():
     """tests/test_sampled_confidence.py:169-196: confidence is max p before filtering, also when
     the filter leaves q one-hot; greedy requests leave it untouched."""
