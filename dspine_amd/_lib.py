@@ -27,6 +27,8 @@ EXPORTS = (
     "dsv_logits_padding", "dsv_window_index", "dsv_target_probs", "dsv_compress",
     "dsv_accept_chain", "dsv_sample_chain", "dsv_pack_joint", "dsv_sps_plan",
     "dsv_greedy_verify_noalloc", "dsv_commit_accept", "dsv_rs_table", "dsv_rs_table_workspace_bytes",
+    "dsv_factor_table", "dsv_factor_direct", "dsv_factor_workspace_doubles", "dsv_factor_widen",
+    "dsv_factor_gemm",
 )
 DSV_ADJ_ADD, DSV_ADJ_SCALE = 0, 1
 
@@ -72,6 +74,21 @@ class ChainArgs(ctypes.Structure):
         ("q_ids", vp), ("q_ids_i64", i32), ("pad3", i32), ("q_values", vp),
         ("accept", vp), ("commit", vp), ("bonus", vp), ("output", vp), ("new_seq", vp),
         ("overflow_read", vp),
+    ]
+
+
+class FactorArgs(ctypes.Structure):
+    """Mirror of ``dsv_factor_args``."""
+
+    _fields_ = [
+        ("n", i64), ("K", i32), ("T", i32), ("H", i32), ("R", i32), ("vocab", i64),
+        ("raw", vp), ("raw_dtype", i32), ("query_dtype", i32), ("raw_stride", i64),
+        ("rms", vp), ("query", vp), ("query_stride", i64), ("anchors", vp), ("cand", vp),
+        ("W", vp), ("gram", vp), ("G", vp), ("Vm", vp), ("TG", vp), ("bias", vp), ("norm", vp),
+        ("head", vp), ("candidate_head", vp), ("head_dtype", i32), ("pad0", i32), ("head_stride", i64),
+        ("eps", _c.c_double), ("out", vp), ("base_out", vp), ("x", vp), ("scale", vp), ("first", vp),
+        ("message", vp), ("tg", vp), ("safe", vp), ("d", vp), ("magnitude", vp), ("y", vp),
+        ("gemm_ws", vp), ("gemm_ws_doubles", i64),
     ]
 
 
@@ -144,6 +161,16 @@ def load():
         lib.dsv_commit_accept.restype = i32
         lib.dsv_commit_accept.argtypes = [i32, i32, vp, vp, vp, i32, vp, i32, vp, i64, i64, vp, vp, vp, i32, vp, vp,
                                           vp]
+        lib.dsv_factor_workspace_doubles.restype = i64
+        lib.dsv_factor_workspace_doubles.argtypes = [i64, i32, i32, i32]
+        lib.dsv_factor_table.restype = i32
+        lib.dsv_factor_table.argtypes = [ctypes.POINTER(FactorArgs), vp]
+        lib.dsv_factor_direct.restype = i32
+        lib.dsv_factor_direct.argtypes = [ctypes.POINTER(FactorArgs), vp]
+        lib.dsv_factor_widen.restype = i32
+        lib.dsv_factor_widen.argtypes = [vp, i32, i64, i64, i64, _c.c_double, vp, vp, vp]
+        lib.dsv_factor_gemm.restype = i32
+        lib.dsv_factor_gemm.argtypes = [vp, i64, i64, vp, i64, i64, vp, i64, i64, i64, i32, vp]
         lib.dsv_sps_plan.restype = i32
         lib.dsv_sps_plan.argtypes = [vp, i64, i32, i32, vp, i64, i32, i64, vp, vp, i32, i32, vp, vp, vp, vp]
         _lib = lib

@@ -9,7 +9,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 OUT = os.path.join(os.path.dirname(HERE), "libdspine_verify.so")
 SOURCES = ["dsv_misc.hip", "dsv_verify.hip", "dsv_chain.hip", "dsv_plan.hip", "dsv_commit.hip",
-           "dsv_table.hip"]
+           "dsv_table.hip", "dsv_factor.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -1,0 +1,459 @@
+// Factorized draft q table for gfx950 (sampling/factorized/{kernels,cancellation,weights}.py):
+// the table of the serial last-write refinement, out[n, j, c] =
+//   head[c] . (y / sqrt(mean(y^2) + eps) * norm),   y = x[n] + a[n] * (W m[n, j]),
+// evaluated in float64 from a per-model cache so that no [n, K, H] vector is formed:
+//   numerator   = base[n, c] + a * (m[n, j] . TG[cand c])     base = (x * norm) . head[c]
+//   d = |y|^2   = first + 2 a (x W) . m + a^2 m^T (W^T W) m   first = |x|^2
+//   out         = numerator / sqrt(d / H + eps)
+// and, where d cancels (d < 2^-24 of |first| + |2a cross| + |a^2 quad|, or not finite), the
+// direct form above for that (n, j).  Launches:
+//   k_fx_prep     x = raw[state row] (float64), a, first, base (one workgroup a block row)
+//   k_fx_msg      m = sigmoid(query + G[sender] + bias) * V[sender], tg = TG[candidate]
+//   k_fx_gemm     x W (split over H) and m Gram on the float64 matrix cores
+//                 (v_mfma_f64_16x16x4f64, tiles staged in LDS)
+//   k_fx_final    m . tg[c] (16 x 16 on the matrix cores), the cross and quadratic terms, the
+//                 cancellation test, out
+//   k_fx_direct   the direct form for the (n, j) the test rejected (others return at once)
+// The cache (weights.py build_cache) is made by k_fx_widen (rows to float64, scaled) and the same
+// GEMM with strided operands.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "dsv_common.h"
+
+namespace dsv {
+
+typedef double d4 __attribute__((ext_vector_type(4)));
+
+constexpr int FX_THREADS = 256;
+constexpr int GT = 64;   // GEMM tile (rows and columns of C a workgroup computes)
+constexpr int GK = 16;   // k depth a tile stage holds
+constexpr int FX_KMAX = 64;
+constexpr int FX_SPLIT_MAX = 16;
+
+__device__ __forceinline__ double ld_any(const void* p, int dt, int64_t i) {
+  if (dt == DSV_BF16) return (double)__uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+  return (double)reinterpret_cast<const float*>(p)[i];
+}
+
+// Block-wide sum in a fixed order (waves by lane tree, then waves in index order).
+__device__ __forceinline__ double fx_block_sum(double v, double* sh) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (WAVE - 1), wid = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane == 0) sh[wid] = v;
+  __syncthreads();
+  double s = 0.0;
+  for (int i = 0; i < FX_THREADS / WAVE; ++i) s += sh[i];
+  return s;
+}
+
+// ---------------------------------------------------------------------------------------------
+// C[M, N] (one split's part) = A[M, K] . B[K, N], float64.  A(m, k) = A[m * am + k * ak],
+// B(k, n) = B[k * bk + n * bn]; split z of gridDim.z takes k in [z * kchunk, (z + 1) * kchunk)
+// and writes (accumulate: adds to) C + z * M * N (row-major, ldc = N).  A 64 x 64 tile a
+// workgroup; each wave a 32 x 32
+// quarter as 2 x 2 blocks of 16 x 16.  MFMA operands (v_mfma_f64_16x16x4f64): lane l supplies
+// A[l % 16][l / 16] and B[l / 16][l % 16] of the 16 x 4 / 4 x 16 step and receives
+// D[4v + l / 16][l % 16], v = 0..3.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(FX_THREADS) void k_fx_gemm(const double* __restrict__ A, int64_t am, int64_t ak,
+                                                       const double* __restrict__ B, int64_t bk, int64_t bn,
+                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                       int64_t kchunk, int accumulate) {
+  __shared__ double As[GT][GK + 1];
+  __shared__ double Bs[GK][GT + 1];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+  const int64_t m0 = (int64_t)blockIdx.y * GT, n0 = (int64_t)blockIdx.x * GT;
+  const int64_t k_lo = (int64_t)blockIdx.z * kchunk;
+  const int64_t k_hi = k_lo + kchunk < K ? k_lo + kchunk : K;
+  const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
+  const int li = lane & 15, lg = lane >> 4;
+  d4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = d4{0.0, 0.0, 0.0, 0.0};
+  for (int64_t k0 = k_lo; k0 < k_hi; k0 += GK) {
+    // stage: 64 x 16 of A and 16 x 64 of B, four elements a thread each (zero outside)
+#pragma unroll
+    for (int e = 0; e < (GT * GK) / FX_THREADS; ++e) {
+      const int idx = e * FX_THREADS + tid;
+      const int r = idx / GK, kk = idx % GK;
+      const int64_t gm = m0 + r, gk = k0 + kk;
+      As[r][kk] = (gm < M && gk < k_hi) ? A[gm * am + gk * ak] : 0.0;
+      const int kb = idx / GT, cc = idx % GT;
+      const int64_t gk2 = k0 + kb, gn = n0 + cc;
+      Bs[kb][cc] = (gk2 < k_hi && gn < N) ? B[gk2 * bk + gn * bn] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < GK / 4; ++s) {
+      double a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = As[wm + 16 * i + li][4 * s + lg];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = Bs[4 * s + lg][wn + 16 * j + li];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  double* Cz = C + (int64_t)blockIdx.z * M * N;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t gm = m0 + wm + 16 * i + 4 * v + lg, gn = n0 + wn + 16 * j + li;
+        if (gm < M && gn < N) Cz[gm * N + gn] = accumulate ? Cz[gm * N + gn] + acc[i][j][v] : acc[i][j][v];
+      }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per-round kernels
+// ---------------------------------------------------------------------------------------------
+struct FxP {
+  dsv_factor_args a;
+  int split;        // parts of x W (over H)
+  double* xw_part;  // [split, n, R]
+  double* mg;       // [n K, R]
+};
+
+// the state row (of bs * T) block row i refines: kernels.py:19-21
+__device__ __forceinline__ int64_t fx_source(const dsv_factor_args& a, int64_t i) {
+  return i / (a.T - 1) * a.T + i % (a.T - 1) + 1;
+}
+__device__ __forceinline__ const void* fx_head_row(const dsv_factor_args& a, int64_t i, int c, int64_t& off) {
+  if (a.candidate_head) {
+    off = (i * a.K + c) * a.head_stride;
+    return a.candidate_head;
+  }
+  int64_t cid = a.cand[i * a.K + c];
+  cid = cid < 0 ? 0 : (cid >= a.vocab ? a.vocab - 1 : cid);
+  off = cid * a.head_stride;
+  return a.head;
+}
+
+// x, a, first (kernels.py:15-27) and base (weights.py:12-31): one workgroup a block row, the
+// candidates in groups of 16 (the raw row read again for each group)
+__global__ __launch_bounds__(FX_THREADS) void k_fx_prep(FxP P) {
+  __shared__ double red[FX_THREADS / WAVE];
+  const dsv_factor_args& a = P.a;
+  const int64_t i = blockIdx.x;
+  const int64_t src = fx_source(a, i);
+  for (int c0 = 0; c0 < a.K; c0 += 16) {
+    double first = 0.0;
+    double base[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) base[c] = 0.0;
+    for (int h = threadIdx.x; h < a.H; h += FX_THREADS) {
+      const double xv = ld_any(a.raw, a.raw_dtype, src * a.raw_stride + h);
+      if (c0 == 0) {
+        a.x[i * a.H + h] = xv;
+        first += xv * xv;
+      }
+      const double nv = a.norm[h];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        if (c0 + c < a.K) {
+          int64_t off;
+          const void* hr = fx_head_row(a, i, c0 + c, off);
+          base[c] += xv * ld_any(hr, a.head_dtype, off + h) * nv;
+        }
+      }
+    }
+    if (c0 == 0) {
+      first = fx_block_sum(first, red);
+      if (threadIdx.x == 0) {
+        a.first[i] = first;
+        a.scale[i] = (double)a.rms[src];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      if (c0 + c < a.K) {
+        const double s = fx_block_sum(base[c], red);
+        if (threadIdx.x == 0) a.base_out[i * a.K + c0 + c] = s;
+      }
+    }
+  }
+}
+
+// m and tg of every (i, j) (kernels.py:30-67): one workgroup a block row
+__global__ __launch_bounds__(FX_THREADS) void k_fx_msg(FxP P) {
+  const dsv_factor_args& a = P.a;
+  const int64_t i = blockIdx.x;
+  const int64_t req = i / (a.T - 1), pos = i % (a.T - 1);
+  const int64_t src = req * a.T + pos + 1;
+  for (int idx = threadIdx.x; idx < a.K * a.R; idx += FX_THREADS) {
+    const int j = idx / a.R, r = idx % a.R;
+    int64_t sid = pos == 0 ? a.anchors[req] : a.cand[(i - 1) * a.K + j];
+    int64_t cid = a.cand[i * a.K + j];
+    sid = sid < 0 ? 0 : (sid >= a.vocab ? a.vocab - 1 : sid);
+    cid = cid < 0 ? 0 : (cid >= a.vocab ? a.vocab - 1 : cid);
+    const double q = ld_any(a.query, a.query_dtype, src * a.query_stride + r);
+    const double gate = q + a.G[sid * a.R + r] + a.bias[r];
+    const double sig = 1.0 / (1.0 + exp(-gate));
+    a.message[(i * a.K + j) * a.R + r] = sig * a.Vm[sid * a.R + r];
+    a.tg[(i * a.K + j) * a.R + r] = a.TG[cid * a.R + r];
+  }
+}
+
+// The finalize (kernels.py:70-123): product m . tg on the matrix cores, cross and quadratic on
+// the vector units, the cancellation test, out.  One workgroup a block row (K <= 16 on the matrix
+// path; wider K on the vector units).
+__global__ __launch_bounds__(FX_THREADS) void k_fx_final(FxP P) {
+  __shared__ double xw[1024];
+  __shared__ double prod[16 * 16 * (FX_THREADS / WAVE)];
+  __shared__ double den_s[FX_KMAX];
+  const dsv_factor_args& a = P.a;
+  const int64_t i = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+  const int K = a.K, R = a.R;
+  // x W for this row: the split parts summed in order
+  for (int r = tid; r < R; r += FX_THREADS) {
+    double s = 0.0;
+    for (int z = 0; z < P.split; ++z) s += P.xw_part[((int64_t)z * a.n + i) * R + r];
+    xw[r] = s;
+  }
+  const double* msg = a.message + i * K * R;
+  const double* tgr = a.tg + i * K * R;
+  // product[j][c] = m_j . tg_c: 16 x 16 from R in steps of 4, the R range split over the waves
+  if (K <= 16) {
+    const int li = lane & 15, lg = lane >> 4;
+    d4 acc = {0.0, 0.0, 0.0, 0.0};
+    const int per = (R + 4 * (FX_THREADS / WAVE) - 1) / (4 * (FX_THREADS / WAVE)) * 4;
+    const int r_lo = w * per, r_hi = r_lo + per < R ? r_lo + per : R;
+    for (int r0 = r_lo; r0 < r_hi; r0 += 4) {
+      const int r = r0 + lg;
+      const double av = (li < K && r < r_hi) ? msg[(int64_t)li * R + r] : 0.0;
+      const double bv = (li < K && r < r_hi) ? tgr[(int64_t)li * R + r] : 0.0;
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) prod[w * 256 + (4 * v + lg) * 16 + li] = acc[v];
+  }
+  __syncthreads();
+  // cross_j = xw . m_j and quad_j = mg_j . m_j: 16 lanes a j (K <= 16), the R range split
+  const int grp = tid / 16, gl = tid % 16;
+  for (int j0 = 0; j0 < K; j0 += FX_THREADS / 16) {
+    const int j = j0 + grp;
+    double cr = 0.0, qd = 0.0;
+    if (j < K) {
+      const double* mj = msg + (int64_t)j * R;
+      const double* gj = P.mg + (i * K + j) * R;
+      for (int r = gl; r < R; r += 16) {
+        const double mv = mj[r];
+        cr += xw[r] * mv;
+        qd += gj[r] * mv;
+      }
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+      cr += __shfl_xor(cr, o, 16);
+      qd += __shfl_xor(qd, o, 16);
+    }
+    if (j < K && gl == 0) {
+      const double sc = a.scale[i], first = a.first[i];
+      const double second = 2.0 * sc * cr;
+      const double third = sc * sc * qd;
+      const double d = first + second + third;
+      const double mag = fabs(first) + fabs(second) + fabs(third);
+      const bool safe = isfinite(d) && isfinite(mag) && d >= 0.0 && (mag == 0.0 || d > 0x1p-24 * mag);
+      a.safe[i * K + j] = safe ? 1 : 0;
+      a.d[i * K + j] = d;
+      a.magnitude[i * K + j] = mag;
+      den_s[j] = sqrt(d / (double)a.H + a.eps);
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < K * K; idx += FX_THREADS) {
+    const int j = idx / K, c = idx % K;
+    double pr;
+    if (K <= 16) {
+      pr = 0.0;
+      for (int q = 0; q < FX_THREADS / WAVE; ++q) pr += prod[q * 256 + j * 16 + c];
+    } else {
+      pr = 0.0;
+      for (int r = 0; r < R; ++r) pr += msg[(int64_t)j * R + r] * tgr[(int64_t)c * R + r];
+    }
+    const double num = a.base_out[i * K + c] + a.scale[i] * pr;
+    a.out[(i * K + j) * K + c] = (float)(num / den_s[j]);
+  }
+}
+
+// The direct form (cancellation.py:16-79) for the (i, j) the test rejected; one workgroup each.
+__global__ __launch_bounds__(FX_THREADS) void k_fx_direct(FxP P) {
+  __shared__ double red[FX_THREADS / WAVE];
+  __shared__ double m[1024];
+  const dsv_factor_args& a = P.a;
+  const int64_t ij = blockIdx.x;
+  if (a.safe[ij]) return;
+  const int64_t i = ij / a.K;
+  const int K = a.K, R = a.R, H = a.H;
+  for (int r = threadIdx.x; r < R; r += FX_THREADS) m[r] = a.message[ij * R + r];
+  __syncthreads();
+  const double sc = a.scale[i];
+  double sq = 0.0;
+  double* y = a.y + ij * H;
+  for (int h = threadIdx.x; h < H; h += FX_THREADS) {
+    double delta = 0.0;
+    const double* wr = a.W + (int64_t)h * R;
+    for (int r = 0; r < R; ++r) delta += wr[r] * m[r];
+    const double yv = a.x[i * H + h] + sc * delta;
+    y[h] = yv;
+    sq += yv * yv;
+  }
+  sq = fx_block_sum(sq, red);
+  const double den = sqrt(sq / (double)H + a.eps);
+  for (int c = 0; c < K; ++c) {
+    int64_t off;
+    const void* hr = fx_head_row(a, i, c, off);
+    double v = 0.0;
+    for (int h = threadIdx.x; h < H; h += FX_THREADS) v += y[h] / den * a.norm[h] * ld_any(hr, a.head_dtype, off + h);
+    v = fx_block_sum(v, red);
+    if (threadIdx.x == 0) a.out[ij * K + c] = (float)v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cache rows (weights.py:34-80): out[r, :] = scale * widen(src[r, :]) (* mul[:] when given)
+// ---------------------------------------------------------------------------------------------
+__global__ void k_fx_widen(const void* src, int dt, int64_t stride, int64_t rows, int64_t cols, double scale,
+                           const double* mul, double* out) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    double v = scale * ld_any(src, dt, r * stride + c);
+    if (mul) v = v * mul[c];
+    out[e] = v;
+  }
+}
+
+}  // namespace dsv
+
+using namespace dsv;
+
+// the most parts x W's depth H is cut into (parts of >= 256)
+static int fx_split_cap(int32_t H) {
+  int s = 1;
+  while (s < FX_SPLIT_MAX && H / (2 * s) >= 256) s *= 2;
+  return s;
+}
+static int fx_split(int64_t n, int32_t R, int32_t H) {
+  // enough workgroups over n x R tiles to fill the part
+  const int64_t tiles = ((n + GT - 1) / GT) * ((R + GT - 1) / GT);
+  int s = 1;
+  while (s < fx_split_cap(H) && tiles * s < 512) s *= 2;
+  return s;
+}
+
+// (a bound that grows with n: a buffer sized for n serves every smaller n)
+extern "C" int64_t dsv_factor_workspace_doubles(int64_t n, int32_t K, int32_t H, int32_t R) {
+  return (int64_t)fx_split_cap(H) * n * R + n * (int64_t)K * R;
+}
+
+static void fx_gemm(const double* A, int64_t am, int64_t ak, const double* B, int64_t bk, int64_t bn, double* C,
+                    int64_t M, int64_t N, int64_t K, int split, int accumulate, hipStream_t stream) {
+  int64_t kchunk = (K + split - 1) / split;
+  kchunk = (kchunk + GK - 1) / GK * GK;
+  const dim3 grid((unsigned)((N + GT - 1) / GT), (unsigned)((M + GT - 1) / GT), (unsigned)split);
+  hipLaunchKernelGGL(k_fx_gemm, grid, dim3(FX_THREADS), 0, stream, A, am, ak, B, bk, bn, C, M, N, K, kchunk,
+                     accumulate);
+}
+
+static int fx_check_layout(const dsv_factor_args* args, const char* what) {
+  if (!args) DSV_FAIL(DSV_ERR_INVALID, "%s: null arguments", what);
+  const dsv_factor_args& a = *args;
+  if (a.n < 0 || a.K < 1 || a.K > FX_KMAX || a.T < 2 || a.n % (a.T - 1) || a.H < 1 || a.R < 1 || a.vocab < 1)
+    DSV_FAIL(DSV_ERR_INVALID, "%s: layout mismatch (n %lld, K %d, T %d, H %d, R %d)", what, (long long)a.n, a.K, a.T,
+             a.H, a.R);
+  if (a.R > 1024) DSV_FAIL(DSV_ERR_UNSUPPORTED, "%s: rank R %d above 1024", what, a.R);
+  if (a.head_dtype != DSV_BF16 && a.head_dtype != DSV_F32)
+    DSV_FAIL(DSV_ERR_INVALID, "%s: the head must be bf16 or float32", what);
+  if ((!a.head && !a.candidate_head) || a.head_stride < a.H || !a.cand || !a.W || !a.norm || !a.out || !a.x ||
+      !a.scale || !a.message || !a.safe || !a.y)
+    DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
+  return DSV_OK;
+}
+
+// The direct form alone (cancellation.py:82-147 apply_direct_fallback) for the (n, j) whose
+// safe flag is 0, from x, a, m and the cache's W / norm / head.
+extern "C" int dsv_factor_direct(const dsv_factor_args* args, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int rc = fx_check_layout(args, "dsv_factor_direct");
+  if (rc != DSV_OK) return rc;
+  if (args->n == 0) return DSV_OK;
+  FxP P;
+  memset(&P, 0, sizeof(P));
+  P.a = *args;
+  hipLaunchKernelGGL(k_fx_direct, dim3((unsigned)(args->n * args->K)), dim3(FX_THREADS), 0, stream, P);
+  DSV_CHECK_LAUNCH("k_fx_direct");
+  return DSV_OK;
+}
+
+extern "C" int dsv_factor_table(const dsv_factor_args* args, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int rc = fx_check_layout(args, "dsv_factor_table");
+  if (rc != DSV_OK) return rc;
+  const dsv_factor_args& a = *args;
+  if (a.n == 0) return DSV_OK;
+  for (int dt : {a.raw_dtype, a.query_dtype, a.head_dtype})
+    if (dt != DSV_BF16 && dt != DSV_F32) DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_table: operands must be bf16 or float32");
+  if (!a.raw || !a.rms || !a.query || !a.anchors || !a.cand || !a.W || !a.gram || !a.G || !a.Vm || !a.TG || !a.bias ||
+      !a.norm || (!a.head && !a.candidate_head) || !a.out || !a.base_out || !a.x || !a.scale || !a.first ||
+      !a.message || !a.tg || !a.safe || !a.d || !a.magnitude || !a.y || !a.gemm_ws)
+    DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_table: required pointer is null");
+  if (a.raw_stride < a.H || a.query_stride < a.R || a.head_stride < a.H)
+    DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_table: row strides below the row widths");
+  if (a.gemm_ws_doubles < dsv_factor_workspace_doubles(a.n, a.K, a.H, a.R))
+    DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_factor_table: GEMM workspace too small");
+  FxP P;
+  memset(&P, 0, sizeof(P));
+  P.a = a;
+  P.split = fx_split(a.n, a.R, a.H);
+  P.xw_part = a.gemm_ws;
+  P.mg = a.gemm_ws + (int64_t)P.split * a.n * a.R;
+  const unsigned n = (unsigned)a.n;
+  hipLaunchKernelGGL(k_fx_prep, dim3(n), dim3(FX_THREADS), 0, stream, P);
+  hipLaunchKernelGGL(k_fx_msg, dim3(n), dim3(FX_THREADS), 0, stream, P);
+  DSV_CHECK_LAUNCH("k_fx_prep / k_fx_msg");
+  // x W [n, R] (split over H) and m Gram [n K, R]
+  fx_gemm(a.x, a.H, 1, a.W, a.R, 1, P.xw_part, a.n, a.R, a.H, P.split, 0, stream);
+  fx_gemm(a.message, a.R, 1, a.gram, a.R, 1, P.mg, a.n * a.K, a.R, a.R, 1, 0, stream);
+  DSV_CHECK_LAUNCH("k_fx_gemm");
+  hipLaunchKernelGGL(k_fx_final, dim3(n), dim3(FX_THREADS), 0, stream, P);
+  hipLaunchKernelGGL(k_fx_direct, dim3((unsigned)(a.n * a.K)), dim3(FX_THREADS), 0, stream, P);
+  DSV_CHECK_LAUNCH("k_fx_final / k_fx_direct");
+  return DSV_OK;
+}
+
+extern "C" int dsv_factor_widen(const void* src, int32_t dtype, int64_t stride, int64_t rows, int64_t cols,
+                                double scale, const double* mul, double* out, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!src || !out || rows < 0 || cols < 0 || stride < cols || (dtype != DSV_BF16 && dtype != DSV_F32))
+    DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_widen: invalid operands");
+  if (rows == 0 || cols == 0) return DSV_OK;
+  const int64_t total = rows * cols;
+  const unsigned grid = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  hipLaunchKernelGGL(k_fx_widen, dim3(grid), dim3(256), 0, stream, src, dtype, stride, rows, cols, scale, mul, out);
+  DSV_CHECK_LAUNCH("k_fx_widen");
+  return DSV_OK;
+}
+
+extern "C" int dsv_factor_gemm(const double* A, int64_t am, int64_t ak, const double* B, int64_t bk, int64_t bn,
+                               double* C, int64_t M, int64_t N, int64_t K, int32_t accumulate, dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!A || !B || !C || M < 0 || N < 0 || K < 0) DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_gemm: invalid operands");
+  if (M == 0 || N == 0) return DSV_OK;
+  if (K == 0) DSV_FAIL(DSV_ERR_INVALID, "dsv_factor_gemm: empty inner dimension");
+  fx_gemm(A, am, ak, B, bk, bn, C, M, N, K, 1, accumulate ? 1 : 0, stream);
+  DSV_CHECK_LAUNCH("k_fx_gemm");
+  return DSV_OK;
+}

@@ -32,6 +32,9 @@
  *                         build_sparse_target)
  *   dsv_sample_chain      kernels/dspine.py:616-772 (serial_sample_chain)
  *   dsv_rs_table          kernels/dspine.py:505-613 (serial_rs_table)
+ *   dsv_factor_table      sampling/factorized/kernels.py:179-300 (factor_table) with
+ *                         sampling/factorized/cancellation.py:82-147 (apply_direct_fallback);
+ *                         dsv_factor_widen / dsv_factor_gemm: weights.py:34-80 (build_cache)
  *   dsv_window_index      verification/sps.py:27-32,87-98 (_indices)
  *   dsv_sps_plan          verification/sps.py:35-58 (allocate_verify_lens) and :61-99
  *                         (device_plan: lengths, layout row pointer, _indices)
@@ -277,6 +280,67 @@ int dsv_sample_chain(const float* table, int64_t n, int32_t K, int32_t block_siz
                      const int32_t* top_k, const float* top_p, const float* min_p, const int32_t* greedy,
                      const float* u, const int64_t* cand, const int64_t* greedy_tok, int64_t* out_tok,
                      float* out_q, float* confidence, dsv_stream_t stream);
+
+/* Factorized draft q table (sampling/factorized/kernels.py:179-300 factor_table, with the     */
+/* cancellation fallback of sampling/factorized/cancellation.py:82-147), float64:              */
+/* out[n, j, c] = (base[n, c] + a m.TG[c]) / sqrt(d / H + eps), d = first + 2a (xW).m +        */
+/* a^2 m.Gram.m, and the direct form head[c].(y / sqrt(mean(y^2) + eps) * norm), y = x + a W m, */
+/* where d cancels (d < 2^-24 (|first| + |2a cross| + |a^2 quad|) or not finite).  The cache   */
+/* (sampling/factorized/weights.py:34-80 build_cache) holds W [H, R], Gram = W^T W [R, R],      */
+/* G, V, TG [vocab, R], bias [R] and norm [H] in float64; head [vocab, H] (bf16 / float32) or  */
+/* candidate_head [n K, H].  The workspace arrays are the reference's Workspace fields;        */
+/* gemm_ws holds dsv_factor_workspace_doubles(n, K, H, R) doubles.                              */
+typedef struct dsv_factor_args {
+  int64_t n;                   /* block rows, bs * (T - 1) */
+  int32_t K, T, H, R;
+  int64_t vocab;
+  const void* raw;             /* [bs * T, H] (row stride raw_stride) */
+  int32_t raw_dtype, query_dtype;
+  int64_t raw_stride;
+  const float* rms;            /* [bs * T] */
+  const void* query;           /* [bs * T, R] (row stride query_stride) */
+  int64_t query_stride;
+  const int64_t* anchors;      /* [bs] */
+  const int64_t* cand;         /* [n, K] */
+  const double* W;             /* cache */
+  const double* gram;
+  const double* G;
+  const double* Vm;
+  const double* TG;
+  const double* bias;
+  const double* norm;
+  const void* head;            /* [vocab, H] (row stride head_stride) or NULL with candidate_head */
+  const void* candidate_head;  /* [n * K, H] or NULL */
+  int32_t head_dtype, pad0;
+  int64_t head_stride;
+  double eps;
+  float* out;                  /* [n, K, K] */
+  double* base_out;            /* [n, K] */
+  double* x;                   /* [n, H] */
+  double* scale;               /* [n] */
+  double* first;               /* [n] */
+  double* message;             /* [n, K, R] */
+  double* tg;                  /* [n, K, R] */
+  uint8_t* safe;               /* [n, K] */
+  double* d;                   /* [n, K] */
+  double* magnitude;           /* [n, K] */
+  double* y;                   /* [n, K, H] (the direct form's rows) */
+  double* gemm_ws;
+  int64_t gemm_ws_doubles;
+} dsv_factor_args;
+int64_t dsv_factor_workspace_doubles(int64_t n, int32_t K, int32_t H, int32_t R);
+int dsv_factor_table(const dsv_factor_args* args, dsv_stream_t stream);
+/* The direct form alone (sampling/factorized/cancellation.py:82-147, apply_direct_fallback): */
+/* for each (n, j) with safe[n, j] == 0, from x, scale, message and W / norm / head.           */
+int dsv_factor_direct(const dsv_factor_args* args, dsv_stream_t stream);
+/* The cache's building blocks (weights.py:34-80): out[r, c] = scale * src[r, c] (* mul[c] when */
+/* mul is given) widened to float64 (src bf16 / float32, row stride `stride`), and             */
+/* C[M, N] (+)= A . B in float64 on the matrix cores, A(m, k) = A[m am + k ak],               */
+/* B(k, n) = B[k bk + n bn], C row-major (accumulate != 0: added to C).                         */
+int dsv_factor_widen(const void* src, int32_t dtype, int64_t stride, int64_t rows, int64_t cols, double scale,
+                     const double* mul, double* out, dsv_stream_t stream);
+int dsv_factor_gemm(const double* A, int64_t am, int64_t ak, const double* B, int64_t bk, int64_t bn, double* C,
+                    int64_t M, int64_t N, int64_t K, int32_t accumulate, dsv_stream_t stream);
 
 /* SPS verify-length plan (verification/sps.py:35-99: allocate_verify_lens, the calibration   */
 /* table lookup it does, the ragged layout's row pointer and _indices), one launch.           */

@@ -63,6 +63,9 @@ PINNED = {
     "scores; hand-computed ties at the k-th place and the strict nucleus of sampling/sparse/target.py:"
     "158-165; a brute-force restatement of the support's definition on rows of many ties; closed-form "
     "overflow densification",
+    "factor_table": "equals the direct float64 table of rs_table (pinned by tests/ref_utils.py:52-76) "
+    "within float64 rounding on the reference's shapes, the cancellation rows included; the direct "
+    "form is the one taken where the factors cancel",
     "sparse_route": "the eligibility rules of sampling/target.py:53-54 and sampling/sparse/target.py:"
     "106-116, each turned off alone",
 }
@@ -790,6 +793,59 @@ def rs_table(raw, rms, query, anchors, cand, codebook, pg, pv, gb, w_last, norm_
     normalized = ref / torch.sqrt(ref.square().mean(-1, keepdim=True) + eps) * norm_w.to(d)
     hd = (head.to(d)[torch.as_tensor(cand)] if candidate_head is None else candidate_head.to(d))  # [n, K, H]
     return torch.einsum("njh,nch->njc", normalized, hd)
+
+
+def factor_cache(codebook, pred, prev, bias, W, norm, head, res_emb=None, res_proj=None) -> dict:
+    """sampling/factorized/weights.py:34-80 in float64: W, norm, bias, Gram = W^T W, and per
+    vocabulary row G = e pred^T, V = e prev^T (+ res_emb res_proj^T), TG = (head * norm) W with
+    e = sqrt(C) codebook."""
+    c = codebook.shape[1]
+    wd, pd, vd, nd, bd = (z.double() for z in (W, pred, prev, norm, bias))
+    e = math.sqrt(c) * codebook.double()
+    value = e @ vd.T
+    if res_emb is not None:
+        value = value + res_emb.double() @ res_proj.double().T
+    return {"W": wd, "norm": nd, "bias": bd, "Gram": wd.T @ wd, "head": head, "G": e @ pd.T, "V": value,
+            "TG": head.double() * nd @ wd}
+
+
+def factor_table(raw, rms, query, anchors, cand, cache, eps, T, candidate_head=None):
+    """sampling/factorized/kernels.py:15-300 with cancellation.py:82-147, float64 on the CPU.
+    Returns (out float32 [n, K, K], base float64 [n, K], safe bool [n, K], out64 float64)."""
+    d = torch.float64
+    n, k = cand.shape
+    h, r = raw.shape[1], query.shape[1]
+    bs = anchors.numel()
+    rows = torch.tensor([i // (T - 1) * T + i % (T - 1) + 1 for i in range(n)])
+    x = raw[rows].to(d)
+    a = rms[rows].to(d)
+    first = (x * x).sum(-1)
+    cand = torch.as_tensor(cand)
+    # the sender of (i, j): the anchor on a request's first block row, else candidate j of row i-1
+    sid = torch.cat((torch.as_tensor(anchors).view(bs, 1, 1).expand(bs, 1, k),
+                     cand.view(bs, T - 1, k)[:, :-1, :]), 1).reshape(n, k)
+    gate = query[rows].to(d)[:, None, :] + cache["G"][sid] + cache["bias"]
+    message = 1.0 / (1.0 + torch.exp(-gate)) * cache["V"][sid]                    # [n, K, R]
+    tg = cache["TG"][cand]                                                       # [n, K, R]
+    heads = cache["head"][cand].to(d) if candidate_head is None else candidate_head.reshape(n, k, h).to(d)
+    base = (x[:, None, :] * heads * cache["norm"]).sum(-1)                       # [n, K]
+    product = torch.einsum("njr,ncr->njc", message, tg)
+    xw = x @ cache["W"]
+    mg = message @ cache["Gram"]
+    cross = (xw[:, None, :] * message).sum(-1)
+    quadratic = (mg * message).sum(-1)
+    second = 2.0 * a[:, None] * cross
+    third = a[:, None] * a[:, None] * quadratic
+    dd = first[:, None] + second + third
+    magnitude = first[:, None].abs() + second.abs() + third.abs()
+    safe = (torch.isfinite(dd) & torch.isfinite(magnitude) & (dd >= 0)
+            & ((magnitude == 0) | (dd > 2.0 ** (-24) * magnitude)))
+    out64 = (base[:, None, :] + a[:, None, None] * product) / torch.sqrt(dd / h + eps)[..., None]
+    for ni, ji in (~safe).nonzero().tolist():
+        y = x[ni] + a[ni] * (cache["W"] @ message[ni, ji])
+        z = y / torch.sqrt(y.square().mean() + eps) * cache["norm"]
+        out64[ni, ji] = heads[ni] @ z
+    return out64.float(), base, safe, out64
 
 
 def make_info(temperatures, top_ks, top_ps, min_ps=None, *, need_top_k=None, need_top_p=None,

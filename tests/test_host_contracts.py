@@ -367,3 +367,19 @@ def test_sps_plan_contracts():
         allocate_verify_lens(raw, table, depth, 10, torch.linspace(0.1, 0.9, 8, dtype=torch.float64))
     with pytest.raises(ValueError, match="device"):  # CPU tensors never reach the HIP library
         allocate_verify_lens(raw, table, depth, 10)
+
+
+def test_proposal_capture_sizes_and_factor_contracts():
+    """graph.py's capture-size rule (sizes that at least double, the largest configured size
+    closing the list) and factor_table's contract checks before any launch."""
+    from dspine_amd.sampling.factorized.graph import _capture_sizes
+    from dspine_amd.sampling.factorized.kernels import factor_table
+
+    assert _capture_sizes([1, 2, 4, 8, 16, 32], 33) == [1, 2, 4, 8, 16, 32]
+    assert _capture_sizes([1, 3, 5, 6, 12, 13], 12) == [1, 3, 6, 12]
+    assert _capture_sizes([4, 5, 7], 64) == [7]  # the largest replaces the last kept size
+    assert _capture_sizes([0, 100], 64) == []
+    raw = torch.zeros(32, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="bs \\* \\(t - 1\\)"):
+        factor_table(raw, torch.ones(32), torch.zeros(32, 8, dtype=torch.bfloat16), torch.zeros(2, dtype=torch.int64),
+                     torch.zeros(29, 16, dtype=torch.int64), {}, 1e-6, 16, None, None, None)

@@ -39,7 +39,8 @@ def test_library_exports_every_declared_symbol():
     assert set(_lib.EXPORTS) == set(declared_functions())
 
 
-@pytest.mark.parametrize("cls_name, c_name", [("VerifyArgs", "dsv_verify_args"), ("ChainArgs", "dsv_chain_args")])
+@pytest.mark.parametrize("cls_name, c_name", [("VerifyArgs", "dsv_verify_args"), ("ChainArgs", "dsv_chain_args"),
+                                              ("FactorArgs", "dsv_factor_args")])
 def test_args_struct_layout_matches_c(tmp_path, cls_name, c_name):
     """ctypes field offsets == offsetof() of the C struct compiled by gcc."""
     from dspine_amd import _lib

@@ -777,3 +777,51 @@ def test_rs_table_closed_forms():
         want = d["head"][d["cand"][nn]].double() @ xn
         for j in range(got.shape[1]):
             torch.testing.assert_close(got[nn, j], want, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------
+# Factorized q table (sampling/factorized/kernels.py:179-300, cancellation.py:82-147)
+# ------------------------------------------------------------------------------------------
+def _factor_inputs(seed, bs=3, T=5, H=64, R=8, C=16, V=64, k=16, f32=False):
+    g = torch.Generator().manual_seed(seed)
+    dt = torch.float32 if f32 else torch.bfloat16
+    rand = lambda *shape: torch.randn(*shape, generator=g) * 0.1  # noqa: E731
+    m, n = bs * T, bs * (T - 1)
+    return dict(raw=rand(m, H).to(dt), rms=(torch.rand(m, generator=g) + 0.5).float(), query=rand(m, R).to(dt),
+                anchors=torch.randint(0, V, (bs,), generator=g),
+                cand=torch.stack([torch.randperm(V, generator=g)[:k] for _ in range(n)]),
+                codebook=rand(V, C).bfloat16(), pred=rand(R, C), prev=rand(R, C), bias=rand(R), W=rand(H, R),
+                norm=1.0 + rand(H), head=rand(V, H).bfloat16())
+
+
+def test_factor_table_equals_direct_table():
+    """The factorized float64 table equals the direct formula of rs_table (pinned by the
+    explicit loops of tests/ref_utils.py:52-76) to float64 rounding."""
+    d = _factor_inputs(1)
+    T = 5
+    cache = O.factor_cache(d["codebook"], d["pred"], d["prev"], d["bias"], d["W"], d["norm"], d["head"])
+    out, base, safe, out64 = O.factor_table(d["raw"], d["rms"], d["query"], d["anchors"], d["cand"], cache, 1e-6, T)
+    direct = O.rs_table(d["raw"], d["rms"], d["query"], d["anchors"], d["cand"], d["codebook"], d["pred"], d["prev"],
+                        d["bias"], d["W"], d["norm"], d["head"], 1e-6, T)
+    assert bool(safe.all())
+    torch.testing.assert_close(out64, direct, rtol=1e-9, atol=1e-12)
+
+
+def test_factor_table_cancellation_takes_the_direct_form():
+    """State rows that cancel a lane's write (x = -a W m in float32) fail the 2^-24 test; those
+    entries take the direct form, which still equals the direct table."""
+    d = _factor_inputs(2, f32=True)
+    T = 5
+    cache = O.factor_cache(d["codebook"], d["pred"], d["prev"], d["bias"], d["W"], d["norm"], d["head"])
+    # cancel lane 3 of block rows 1 and 6: raw[state row] = -rms * (W m)
+    for i, j in ((1, 3), (6, 3)):
+        src = i // (T - 1) * T + i % (T - 1) + 1
+        sid = int(d["anchors"][i // (T - 1)]) if i % (T - 1) == 0 else int(d["cand"][i - 1, j])
+        gate = d["query"][src].double() + cache["G"][sid] + cache["bias"]
+        m = torch.sigmoid(gate) * cache["V"][sid]
+        d["raw"][src] = (-d["rms"][src].double() * (cache["W"] @ m)).float()
+    out, base, safe, out64 = O.factor_table(d["raw"], d["rms"], d["query"], d["anchors"], d["cand"], cache, 1e-6, T)
+    assert not bool(safe[1, 3]) and not bool(safe[6, 3]) and int((~safe).sum()) == 2
+    direct = O.rs_table(d["raw"], d["rms"], d["query"], d["anchors"], d["cand"], d["codebook"], d["pred"], d["prev"],
+                        d["bias"], d["W"], d["norm"], d["head"], 1e-6, T)
+    torch.testing.assert_close(out64, direct, rtol=1e-9, atol=1e-12)
