@@ -29,7 +29,7 @@ typedef double d4 __attribute__((ext_vector_type(4)));
 
 constexpr int FX_THREADS = 256;
 constexpr int GT = 64;   // GEMM tile (rows and columns of C a workgroup computes)
-constexpr int GK = 16;   // k depth a tile stage holds
+constexpr int GK = 32;   // k depth a tile stage holds
 constexpr int FX_KMAX = 64;
 constexpr int FX_SPLIT_MAX = 16;
 
@@ -63,6 +63,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_gemm(const double* __restrict
                                                        const double* __restrict__ B, int64_t bk, int64_t bn,
                                                        double* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                        int64_t kchunk, int accumulate) {
+  constexpr int PER = (GT * GK) / FX_THREADS;  // elements of each operand a thread stages
   __shared__ double As[GT][GK + 1];
   __shared__ double Bs[GK][GT + 1];
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
@@ -76,19 +77,35 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_gemm(const double* __restrict
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = d4{0.0, 0.0, 0.0, 0.0};
-  for (int64_t k0 = k_lo; k0 < k_hi; k0 += GK) {
-    // stage: 64 x 16 of A and 16 x 64 of B, four elements a thread each (zero outside)
+  // the next stage's operands, loaded into registers while the current stage is multiplied.
+  // Thread t stages A rows t / GK + e * (256 / GK) at depth t % GK, and B depths
+  // t / GT + e * (256 / GT) at column t % GT: one base address each, fixed strides over e.
+  static_assert(FX_THREADS % GK == 0 && FX_THREADS % GT == 0, "staging strides");
+  constexpr int ARS = FX_THREADS / GK, BKS = FX_THREADS / GT;
+  const int a_r = tid / GK, a_k = tid % GK, b_k = tid / GT, b_n = tid % GT;
+  const int64_t gn_b = n0 + b_n;
+  const double* a_base = A + (m0 + a_r) * am + (k_lo + a_k) * ak;
+  const double* b_base = B + (k_lo + b_k) * bk + gn_b * bn;
+  double ra[PER], rb[PER];
+  auto fetch = [&](int64_t kofs) {
+    const bool ka = k_lo + kofs + a_k < k_hi;
 #pragma unroll
-    for (int e = 0; e < (GT * GK) / FX_THREADS; ++e) {
-      const int idx = e * FX_THREADS + tid;
-      const int r = idx / GK, kk = idx % GK;
-      const int64_t gm = m0 + r, gk = k0 + kk;
-      As[r][kk] = (gm < M && gk < k_hi) ? A[gm * am + gk * ak] : 0.0;
-      const int kb = idx / GT, cc = idx % GT;
-      const int64_t gk2 = k0 + kb, gn = n0 + cc;
-      Bs[kb][cc] = (gk2 < k_hi && gn < N) ? B[gk2 * bk + gn * bn] : 0.0;
+    for (int e = 0; e < PER; ++e) {
+      const bool ina = ka && m0 + a_r + e * ARS < M;
+      ra[e] = ina ? a_base[e * ARS * am + kofs * ak] : 0.0;
+      const bool inb = gn_b < N && k_lo + kofs + b_k + e * BKS < k_hi;
+      rb[e] = inb ? b_base[(e * BKS + kofs) * bk] : 0.0;
+    }
+  };
+  if (k_lo < k_hi) fetch(0);
+  for (int64_t k0 = k_lo; k0 < k_hi; k0 += GK) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      As[a_r + e * ARS][a_k] = ra[e];
+      Bs[b_k + e * BKS][b_n] = rb[e];
     }
     __syncthreads();
+    if (k0 + GK < k_hi) fetch(k0 + GK - k_lo);
 #pragma unroll
     for (int s = 0; s < GK / 4; ++s) {
       double a[2], b[2];
@@ -140,48 +157,105 @@ __device__ __forceinline__ const void* fx_head_row(const dsv_factor_args& a, int
   return a.head;
 }
 
-// x, a, first (kernels.py:15-27) and base (weights.py:12-31): one workgroup a block row, the
-// candidates in groups of 16 (the raw row read again for each group)
+template <typename T, int VEC>
+struct alignas(sizeof(T) * VEC) FxVec {
+  T v[VEC];
+};
+__device__ __forceinline__ double fx_widen(uint16_t v) { return (double)__uint_as_float((uint32_t)v << 16); }
+__device__ __forceinline__ double fx_widen(float v) { return (double)v; }
+
+// x, a, first (kernels.py:15-27) and base (weights.py:12-31): one workgroup a block row.  Each
+// thread takes VEC consecutive h at a time (one 8- or 16-byte load of the raw row and of each of
+// the 16 candidates' head rows in flight together); the 16 dot products of a group of candidates
+// are reduced with one barrier pair.  RT / HT are uint16_t (bf16 bits) or float.
+template <typename RT, typename HT, int VEC>
 __global__ __launch_bounds__(FX_THREADS) void k_fx_prep(FxP P) {
-  __shared__ double red[FX_THREADS / WAVE];
+  __shared__ double red[FX_THREADS / WAVE][16];
   const dsv_factor_args& a = P.a;
   const int64_t i = blockIdx.x;
   const int64_t src = fx_source(a, i);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+  const RT* raw = reinterpret_cast<const RT*>(a.raw) + src * a.raw_stride;
+  double* xrow = a.x + i * a.H;
+  double first = 0.0;
   for (int c0 = 0; c0 < a.K; c0 += 16) {
-    double first = 0.0;
+    const HT* hrow[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      int64_t off = 0;
+      const void* hr = fx_head_row(a, i, c0 + c < a.K ? c0 + c : c0, off);
+      hrow[c] = reinterpret_cast<const HT*>(hr) + off;
+    }
     double base[16];
 #pragma unroll
     for (int c = 0; c < 16; ++c) base[c] = 0.0;
-    for (int h = threadIdx.x; h < a.H; h += FX_THREADS) {
-      const double xv = ld_any(a.raw, a.raw_dtype, src * a.raw_stride + h);
-      if (c0 == 0) {
-        a.x[i * a.H + h] = xv;
-        first += xv * xv;
-      }
-      const double nv = a.norm[h];
+    for (int h = tid * VEC; h < a.H; h += FX_THREADS * VEC) {
+      const FxVec<RT, VEC> rv = *reinterpret_cast<const FxVec<RT, VEC>*>(raw + h);
+      FxVec<HT, VEC> hv[16];
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
+      for (int c = 0; c < 16; ++c)
+        if (c0 + c < a.K) hv[c] = *reinterpret_cast<const FxVec<HT, VEC>*>(hrow[c] + h);
+      double xn[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const double xv = fx_widen(rv.v[e]);
+        if (c0 == 0) first += xv * xv;
+        xn[e] = xv * a.norm[h + e];
+        if (c0 == 0) xrow[h + e] = xv;
+      }
+#pragma unroll
+      for (int c = 0; c < 16; ++c)
         if (c0 + c < a.K) {
-          int64_t off;
-          const void* hr = fx_head_row(a, i, c0 + c, off);
-          base[c] += xv * ld_any(hr, a.head_dtype, off + h) * nv;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) base[c] += xn[e] * fx_widen(hv[c].v[e]);
         }
-      }
-    }
-    if (c0 == 0) {
-      first = fx_block_sum(first, red);
-      if (threadIdx.x == 0) {
-        a.first[i] = first;
-        a.scale[i] = (double)a.rms[src];
-      }
     }
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      if (c0 + c < a.K) {
-        const double s = fx_block_sum(base[c], red);
-        if (threadIdx.x == 0) a.base_out[i * a.K + c0 + c] = s;
-      }
+      const double s = wave_sum(base[c]);
+      if (lane == 0) red[w][c] = s;
     }
+    __syncthreads();
+    if (tid < 16 && c0 + tid < a.K) {
+      double s = 0.0;
+#pragma unroll
+      for (int q = 0; q < FX_THREADS / WAVE; ++q) s += red[q][tid];
+      a.base_out[i * a.K + c0 + tid] = s;
+    }
+    __syncthreads();
+  }
+  first = fx_block_sum(first, &red[0][0]);
+  if (tid == 0) {
+    a.first[i] = first;
+    a.scale[i] = (double)a.rms[src];
+  }
+}
+
+// the prep instance for the operand dtypes: 8 or 4 elements a load when every row start and
+// stride allows it, one element a load otherwise
+static void fx_launch_prep(const FxP& P, hipStream_t stream) {
+  const dsv_factor_args& a = P.a;
+  const void* heads = a.candidate_head ? a.candidate_head : a.head;
+  const int vec = (a.raw_dtype == DSV_BF16 && a.head_dtype == DSV_BF16) ? 8 : 4;
+  const int rsz = a.raw_dtype == DSV_BF16 ? 2 : 4, hsz = a.head_dtype == DSV_BF16 ? 2 : 4;
+  const bool aligned = a.H % vec == 0 && a.raw_stride % vec == 0 && a.head_stride % vec == 0 &&
+                       (uintptr_t)a.raw % (rsz * vec) == 0 && (uintptr_t)heads % (hsz * vec) == 0;
+  const dim3 grid((unsigned)a.n), block(FX_THREADS);
+  const bool rb = a.raw_dtype == DSV_BF16, hb = a.head_dtype == DSV_BF16;
+  if (aligned && vec == 8) {
+    hipLaunchKernelGGL((k_fx_prep<uint16_t, uint16_t, 8>), grid, block, 0, stream, P);
+  } else if (aligned) {
+    if (rb) hipLaunchKernelGGL((k_fx_prep<uint16_t, float, 4>), grid, block, 0, stream, P);
+    else if (hb) hipLaunchKernelGGL((k_fx_prep<float, uint16_t, 4>), grid, block, 0, stream, P);
+    else hipLaunchKernelGGL((k_fx_prep<float, float, 4>), grid, block, 0, stream, P);
+  } else if (rb && hb) {
+    hipLaunchKernelGGL((k_fx_prep<uint16_t, uint16_t, 1>), grid, block, 0, stream, P);
+  } else if (rb) {
+    hipLaunchKernelGGL((k_fx_prep<uint16_t, float, 1>), grid, block, 0, stream, P);
+  } else if (hb) {
+    hipLaunchKernelGGL((k_fx_prep<float, uint16_t, 1>), grid, block, 0, stream, P);
+  } else {
+    hipLaunchKernelGGL((k_fx_prep<float, float, 1>), grid, block, 0, stream, P);
   }
 }
 
@@ -421,7 +495,7 @@ extern "C" int dsv_factor_table(const dsv_factor_args* args, dsv_stream_t stream
   P.xw_part = a.gemm_ws;
   P.mg = a.gemm_ws + (int64_t)P.split * a.n * a.R;
   const unsigned n = (unsigned)a.n;
-  hipLaunchKernelGGL(k_fx_prep, dim3(n), dim3(FX_THREADS), 0, stream, P);
+  fx_launch_prep(P, stream);
   hipLaunchKernelGGL(k_fx_msg, dim3(n), dim3(FX_THREADS), 0, stream, P);
   DSV_CHECK_LAUNCH("k_fx_prep / k_fx_msg");
   // x W [n, R] (split over H) and m Gram [n K, R]
