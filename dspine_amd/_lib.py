@@ -28,7 +28,7 @@ EXPORTS = (
     "dsv_accept_chain", "dsv_sample_chain", "dsv_pack_joint", "dsv_sps_plan",
     "dsv_greedy_verify_noalloc", "dsv_commit_accept", "dsv_rs_table", "dsv_rs_table_workspace_bytes",
     "dsv_factor_table", "dsv_factor_direct", "dsv_factor_workspace_doubles", "dsv_factor_widen",
-    "dsv_factor_gemm",
+    "dsv_factor_gemm", "dsv_filter_probs", "dsv_filter_workspace_bytes",
 )
 DSV_ADJ_ADD, DSV_ADJ_SCALE = 0, 1
 
@@ -145,6 +145,10 @@ def load():
         lib.dsv_window_index.argtypes = [vp, i32, i32, i32, vp, i64, vp]
         lib.dsv_target_probs.restype = i32
         lib.dsv_target_probs.argtypes = [ctypes.POINTER(VerifyArgs), vp, i64, i32, vp]
+        lib.dsv_filter_probs.restype = i32
+        lib.dsv_filter_probs.argtypes = [ctypes.POINTER(VerifyArgs), vp, i64, vp, i64, i32, i32, vp]
+        lib.dsv_filter_workspace_bytes.restype = i64
+        lib.dsv_filter_workspace_bytes.argtypes = [i64, i64]
         lib.dsv_compress.restype = i32
         lib.dsv_compress.argtypes = [vp, i64, i64, i64, i32, vp, vp, vp, vp, vp]
         lib.dsv_accept_chain.restype = i32

@@ -65,6 +65,7 @@ constexpr int BCT = 256;             // threads of the bonus / finalize kernels
 constexpr int QMAX = 64;             // largest supported sparse-q width K
 constexpr int FLAG_FULL_HIST = 2;    // nucleus row whose cut needs the full value histogram
 constexpr int FLAG_SCAN_DRAW = 4;    // dense row whose bonus draw k_final plans from a scan of every chunk
+constexpr int FLAG_TIES_COUNTED = 8; // full-histogram row whose chunks' counts of cut-key values are in rties
 constexpr int SJ_CAP = 32;           // packed capacity of the sparse joint target (sampling/target.py:84-87)
 
 template <int DT>

@@ -64,6 +64,8 @@ struct KParams {
   uint32_t* req_cnt;      // [bs]: rows merged per request (zeroed by the chunk pass)
   uint32_t* deferred;     // [bs]: 1 until the row merge wrote the request's outputs (set by the chunk pass)
   int32_t only_deferred;  // k_final skips the requests the row merge finished
+  const float* src_p;     // dense target writer with raw_p: kept entries are src_p's values (the
+  int64_t src_stride;     //   probabilities whose logs are the rows: dsv_filter_probs), else NULL
 };
 
 __device__ __forceinline__ const char* row_ptr(const dsv_verify_args& a, int64_t r) {
@@ -1411,6 +1413,7 @@ __device__ __forceinline__ void merge_nucleus(const KParams& P, int64_t r, int b
 // registers; one workgroup per row, persistent over the rows.
 // ---------------------------------------------------------------------------------------
 constexpr int NUC_GRID = 64;  // k_nuc workgroups (persistent over the full-histogram rows)
+constexpr int NUC_GRID_F32 = 256;  // k_nuc workgroups over float32 rows (LDS only: one a CU)
 constexpr int NUC_WAVES = NUC_THREADS / WAVE;
 constexpr int NUC_WPW = HIST_WORDS / NUC_WAVES;  // histogram words per wave
 constexpr int NUC_ITERS = NUC_WPW / WAVE;        // words per lane
@@ -1936,10 +1939,27 @@ __device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucL
     __syncthreads();  // (sh.cut_S read before the next descent)
   }
   const bool found = descend(topk, min_p, top_p_eff);
+  // A cut that keeps only some of the cut key's values: each chunk's count of them, so that the
+  // dense writer ranks a chunk's ties from the earlier chunks' counts
+  const uint32_t cut_key = sh.cut_key;
+  const int32_t cut_tie = sh.cut_tie;
+  const bool count_ties = found && cut_tie > 0 && cut_tie != INT_MAX;
+  if (count_ties) {
+    constexpr int FE = Span<DSV_F32, NUC_THREADS>::FE;
+    for (int c = 0; c < P.C; ++c) {
+      const int64_t jlo = (int64_t)c * Elems<DSV_F32>::chunk + (int64_t)tid * FE;
+      uint64_t t = 0;
+      for_span<DSV_F32, ALIGNED, NUC_THREADS>(P, b, rowp, c, pres, rep, [&](int i, float x) {
+        t += (jlo + i < V && key_of<DSV_F32>(x) == cut_key) ? 1u : 0u;
+      });
+      t = block_sum<NUC_WAVES>(t, sh.u);
+      if (tid == 0) P.rties[r * NCHK + c] = (int32_t)t;
+    }
+  }
   if (tid < WAVE) {
     if (found) {
-      rs.vcut = sh.cut_key;
-      rs.ktie = sh.cut_tie;
+      rs.vcut = cut_key;
+      rs.ktie = cut_tie;
       rs.S_kept = sh.cut_S;
     } else {  // every value is kept
       rs.vcut = 0u;
@@ -1947,6 +1967,7 @@ __device__ __forceinline__ void nuc_row_f32(const KParams& P, int64_t r, F32NucL
       rs.S_kept = (double)(L.pmass[0][0] + L.mass[0][0]) / FX_ONE;
     }
     rs.S_f = (float)rs.S_kept;
+    if (count_ties) rs.flags |= FLAG_TIES_COUNTED;
     nucleus_finish<DSV_F32>(P, r, b, s, rs, T, xt, tok, tie_tok, ro);
   }
   __syncthreads();
@@ -2819,7 +2840,7 @@ __global__ __launch_bounds__(CT, 4) void k_merge(KParams P) {
       if (at < a.rows) P.nuc_rows[1 + at] = (int32_t)r;
     }
   }
-  if (!a.candidates) return;  // (the target-distribution entry writes no outputs)
+  if (!a.candidates) return;  // (the target-distribution entries write no outputs)
   // the row's decision and token have reached the coherence point before the row is counted;
   // the workgroup that completes the request's count writes the request's outputs
   if (tid == 0) {
@@ -3004,24 +3025,18 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
 // that are not 16-byte aligned.
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int64_t out_stride) {
+__device__ __forceinline__ void dense_p_spans(const KParams& P, int64_t r, int c, int b, const RowSum& rs, int mode,
+                                              float* out, int64_t out_stride) {
   constexpr int CV = Elems<DT>::cv, CHE = Elems<DT>::chunk, FE = CV * Elems<DT>::n;
   constexpr int NW = CT / WAVE;
   __shared__ int32_t red_i[NW];
   __shared__ ListEntry lst[DSV_LIST_K];
   __shared__ int32_t s_before;
   const dsv_verify_args& a = P.a;
-  const int C = P.C;
-  const int64_t r = blockIdx.x / C;
-  const int c = (int)(blockIdx.x - r * C);
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
   const int64_t jlo = (int64_t)c * CHE + (int64_t)tid * FE;
   float* orow = out + r * out_stride;
-  int b = 0, s = 0;
-  const bool live_row = row_request(a, r, b, s);
-  const RowSum rs = P.rowsum[r];
-  const int mode = live_row ? rs.mode : M_SKIP;
   // the span's values, four at a time
   float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
   auto put = [&](int i, float v) {
@@ -3059,7 +3074,9 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
         for (int e = 0; e < n; ++e)
           if ((int64_t)lst[e].id == j) {
             v = lst[e].P;
-            if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
+            if (P.raw_p && P.src_p) {  // the input probability itself
+              v = P.src_p[r * P.src_stride + j];
+            } else if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
               float x = load_elem<DT>(row_ptr(a, r), j);
               if (P.pbits && pen_test(P, b, j))
                 x = penalize<DT>(x, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
@@ -3077,6 +3094,9 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
   const char* rowp = row_ptr(a, r);
   const bool hist = mode == M_HIST;
   int32_t tbefore = 0;
+  // the chunks' counts of the cut key's values are in rties (merged rows, and full-histogram rows
+  // whose resolver counted them)
+  const bool ties_known = !(rs.flags & FLAG_FULL_HIST) || (rs.flags & FLAG_TIES_COUNTED);
   if (hist && rs.ktie > 0 && rs.ktie != INT_MAX) {
     // the cut key's values before this thread's span, in id order
     int32_t t = 0;
@@ -3085,14 +3105,14 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
     tbefore = block_excl_scan<NW>(t, red_i, &tot);
     if (tid == 0) {
       int32_t before = 0;
-      if (!(rs.flags & FLAG_FULL_HIST)) {
+      if (ties_known) {
         for (int c2 = 0; c2 < c; ++c2) before += P.rties[r * NCHK + c2];
       } else {
         s_before = 0;
       }
-      if (!(rs.flags & FLAG_FULL_HIST)) s_before = before;
+      if (ties_known) s_before = before;
     }
-    if (rs.flags & FLAG_FULL_HIST) {  // (rare) the earlier chunks' counts by scanning them
+    if (!ties_known) {  // (rare) the earlier chunks' counts by scanning them
       int32_t e = 0;
       for (int c2 = 0; c2 < c; ++c2)
         for_span<DT, ALIGNED, CT>(P, b, rowp, c2, pres, rep, [&](int, float x) { e += key_of<DT>(x) == rs.vcut; });
@@ -3107,7 +3127,10 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
     float v = 0.f;
     const uint32_t k = key_of<DT>(x);
     const bool kept = !hist || k > rs.vcut || (k == rs.vcut && (int64_t)tbefore + seen < (int64_t)rs.ktie);
-    if (kept) v = P.raw_p ? prob_of(x, T, rs.m_f, rs.invZ) : (float)dense_P(rs, T, x);
+    if (kept)
+      v = P.raw_p ? (P.src_p ? (jlo + i < V ? P.src_p[r * P.src_stride + jlo + i] : 0.f)  // (ids past the row: -inf)
+                             : prob_of(x, T, rs.m_f, rs.invZ))
+                  : (float)dense_P(rs, T, x);
     seen += hist && k == rs.vcut;
     if (vec_ok) put(i, v); else put1(i, v);
   });
@@ -3115,15 +3138,18 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, float* out, int6
 
 
 // ---------------------------------------------------------------------------------------
-// k_dense_p: the target distribution written out densely (runtime/worker.py:440-508), one
-// workgroup per (row, chunk).  The chunk's values are laid out as the chunk pass loads them
-// (thread t, vector u: ids (u CT + t) n .. + n), so that a wave's loads and 16-byte stores are
-// contiguous; support-list rows write zeros with the list's values at their ids (an LDS bitmap
-// of the chunk's list ids), greedy rows the one-hot row.  Rows whose cut keeps only some of the
-// values at the cut key, and unaligned outputs, take the ordered path above.
+// The target distribution of one (row, chunk) written out densely (runtime/worker.py:440-508),
+// from the row's summary rs (mode M_SKIP: zeros; b is the row's request).  The chunk's values
+// are laid out as the chunk pass loads them (thread t, vector u: ids (u CT + t) n .. + n), so
+// that a wave's loads and 16-byte stores are contiguous; support-list rows write zeros with the
+// list's values at their ids (an LDS bitmap of the chunk's list ids), greedy rows the one-hot
+// row.  Rows whose cut keeps only some of the values at the cut key (when the chunks' counts of
+// them are unknown), and unaligned outputs, take the ordered path above.  Callers that write
+// several chunks in a row put a barrier between the calls (the LDS arrays are reused).
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
+__device__ __forceinline__ void dense_p_chunk(const KParams& P, int64_t r, int c, int b, const RowSum& rs, int mode,
+                                              float* out, int64_t out_stride) {
   constexpr int n = Elems<DT>::n, CV = Elems<DT>::cv, CHE = Elems<DT>::chunk;
   constexpr int NW = CT / WAVE;
   __shared__ ListEntry lst[DSV_LIST_K];
@@ -3133,22 +3159,15 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
   __shared__ int32_t s_wt[CV * NW];     // partial ties: each wave's cut-key values of vector u
   __shared__ int32_t s_before;          // partial ties: the cut-key values of the earlier chunks
   const dsv_verify_args& a = P.a;
-  const int C = P.C;
-  const int64_t r = blockIdx.x / C;
-  const int c = (int)(blockIdx.x - r * C);
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   const int64_t V = a.vocab;
   float* orow = out + r * out_stride;
-  int b = 0, s = 0;
-  const bool live_row = row_request(a, r, b, s);
-  const RowSum rs = P.rowsum[r];
-  const int mode = live_row ? rs.mode : M_SKIP;
   const bool hist = mode == M_HIST;
   const bool vec_ok = (out_stride % 4 == 0) && ((uintptr_t)out % 16 == 0);
   // a cut that keeps only the first ktie values of the cut key in id order (partial ties)
   const bool part_ties = hist && rs.ktie > 0 && rs.ktie != INT_MAX;
-  if (!vec_ok || (part_ties && (rs.flags & FLAG_FULL_HIST))) {
-    dense_p_spans<DT, ALIGNED>(P, out, out_stride);
+  if (!vec_ok || (part_ties && (rs.flags & FLAG_FULL_HIST) && !(rs.flags & FLAG_TIES_COUNTED))) {
+    dense_p_spans<DT, ALIGNED>(P, r, c, b, rs, mode, out, out_stride);
     return;
   }
   const int64_t lo = (int64_t)c * CHE, hi = lo + CHE < V ? lo + CHE : V;
@@ -3210,7 +3229,9 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
             for (int q = 0; q < nl; ++q)
               if ((int64_t)lst[q].id == j) {
                 x[e] = lst[q].P;
-                if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
+                if (P.raw_p && P.src_p) {  // the input probability itself
+                  x[e] = P.src_p[r * P.src_stride + j];
+                } else if (P.raw_p) {  // the unrenormalised p: recomputed from the adjusted logit
                   float xv = load_elem<DT>(row_ptr(a, r), j);
                   if (P.pbits && pen_test(P, b, j))
                     xv = penalize<DT>(xv, a.presence ? a.presence[b] : 0.f, a.repetition ? a.repetition[b] : 1.f);
@@ -3330,10 +3351,97 @@ __global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t o
       store_vec(j0, x);
     }
   };
-  if (!P.raw_p && (rs.mode == M_HIST || rs.norm))
+  // raw_p with the input probabilities (logs as the rows): the kept entries copied from them
+  auto copy_rows = [&]() {
+    const float* srow = P.src_p + r * P.src_stride;
+#pragma unroll
+    for (int u = 0; u < CV; ++u) {
+      const int64_t j0 = (v0 + (int64_t)u * CT + tid) * n;
+      if (j0 >= hi) continue;
+      float x[n];
+      int32_t seen = 0;
+#pragma unroll
+      for (int e = 0; e < n; ++e) {
+        const uint32_t k = key_of<DT>(vec_elem<DT>(v[u], e));
+        const bool tie = hist && k == rs.vcut;
+        const bool kept = !hist || k > rs.vcut || (tie && (int64_t)rank0[u] + seen < (int64_t)rs.ktie);
+        seen += tie ? 1 : 0;
+        x[e] = kept && j0 + e < hi ? srow[j0 + e] : 0.f;
+      }
+      store_vec(j0, x);
+    }
+  };
+  if (P.raw_p && P.src_p)
+    copy_rows();
+  else if (!P.raw_p && (rs.mode == M_HIST || rs.norm))
     write_rows(std::true_type{});
   else
     write_rows(std::false_type{});
+}
+
+// k_dense_p: P of one (row, chunk) a workgroup, from the row summaries.
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
+  const int C = P.C;
+  const int64_t r = blockIdx.x / C;
+  const int c = (int)(blockIdx.x - r * C);
+  int b = 0, s = 0;
+  const bool live_row = row_request(P.a, r, b, s);
+  const RowSum rs = P.rowsum[r];
+  dense_p_chunk<DT, ALIGNED>(P, r, c, b, rs, live_row ? rs.mode : M_SKIP, out, out_stride);
+}
+
+// ---------------------------------------------------------------------------------------
+// filter_target_probs on probabilities (runtime/worker.py:473-508): each row becomes a request
+// of its own at temperature 1 whose logits are log p (softmax(log p) = p / sum(p), and top-k,
+// min-p and the order of the values are those of p).  One workgroup per row writes log p and
+// the row's float64 mass, and the row's parameters from its request's: the top-p divided by the
+// mass when the backend compares the raw mass ranked ahead with top_p (top_p_over_mass).
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(CT) void k_prob_prep(const float* __restrict__ probs, int64_t pstride, int64_t V,
+                                                  int32_t T, const int32_t* top_ks, const float* top_ps,
+                                                  const float* min_ps, int32_t top_p_over_mass, int32_t vec4,
+                                                  float* __restrict__ logs, int64_t lstride, int32_t* row_k,
+                                                  float* row_p, float* row_minp, float* row_t) {
+  __shared__ double sd[CT / WAVE];
+  const int64_t r = blockIdx.x;
+  const float* prow = probs + r * pstride;
+  float* lrow = logs + r * lstride;
+  double mass = 0.0;
+  if (vec4) {  // rows 16-byte aligned, V a multiple of 4: four 16-byte loads in flight a thread
+    constexpr int U = 4;
+    const int64_t nv = V / 4;
+    for (int64_t q0 = threadIdx.x; q0 < nv; q0 += (int64_t)CT * U) {
+      float4 p[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + (int64_t)u * CT;
+        p[u] = q < nv ? reinterpret_cast<const float4*>(prow)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + (int64_t)u * CT;
+        if (q >= nv) continue;
+        mass += (double)p[u].x + (double)p[u].y + (double)p[u].z + (double)p[u].w;
+        reinterpret_cast<float4*>(lrow)[q] = make_float4(logf(p[u].x), logf(p[u].y), logf(p[u].z), logf(p[u].w));
+      }
+    }
+  } else {
+    for (int64_t j = threadIdx.x; j < V; j += CT) {
+      const float p = prow[j];
+      mass += (double)p;
+      lrow[j] = logf(p);
+    }
+  }
+  mass = block_sum<CT / WAVE>(mass, sd);
+  if (threadIdx.x == 0) {
+    const int64_t b = r / T;
+    const float tp = top_ps ? top_ps[b] : 1.f;
+    row_k[r] = top_ks[b];
+    row_p[r] = top_p_over_mass && mass > 0.0 ? (float)((double)tp / mass) : tp;
+    row_minp[r] = min_ps ? min_ps[b] : 0.f;
+    row_t[r] = 1.f;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -3582,7 +3690,9 @@ static int launch_rows(const KParams& P, bool hist_possible, bool profile, hipSt
   }
   DSV_CHECK_LAUNCH("k_chunk / k_merge");
   if (hist_possible && !P.final_nuc) {  // rows the merge listed: the full histogram (bf16) or radix descent (fp32)
-    const int grid = (int)(a.rows < NUC_GRID ? a.rows : NUC_GRID);
+    // (bf16 workgroups each own a global histogram area; fp32 ones work in LDS alone, one per CU)
+    const int cap = a.logits_dtype == DSV_BF16 ? NUC_GRID : NUC_GRID_F32;
+    const int grid = (int)(a.rows < cap ? a.rows : cap);
     if (a.logits_dtype == DSV_BF16) {
       const size_t nuc_lds = (size_t)HIST_WORDS * 4;
       if (P.aligned) {
@@ -3657,21 +3767,12 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
   return DSV_OK;
 }
 
-extern "C" int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t out_stride, int32_t normalize,
-                                dsv_stream_t stream_) {
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: null arguments");
-  dsv_verify_args a = *args;
-  a.candidates = nullptr;  // no drafts: no accept decisions, no bonus draw
-  if (!out || out_stride < a.vocab) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: output [rows, vocab] required");
-  KParams P;
-  bool hist_possible = false;
-  const int rc = verify_prepare(a, false, "dsv_target_probs", P, hist_possible);
+// The target-distribution entries: the chunk pass, the row merge, the full-histogram rows, then
+// P of every (row, chunk).
+static int launch_target(KParams& P, bool hist_possible, float* out, int64_t out_stride, hipStream_t stream) {
+  const dsv_verify_args& a = P.a;
+  const int rc = launch_rows(P, hist_possible, false, stream);
   if (rc != DSV_OK) return rc;
-  P.raw_p = normalize ? 0 : 1;
-  if (a.rows == 0) return DSV_OK;
-  const int rc2 = launch_rows(P, hist_possible, false, stream);
-  if (rc2 != DSV_OK) return rc2;
   const dim3 grid((unsigned)(a.rows * P.C));
   if (a.logits_dtype == DSV_BF16) {
     if (P.aligned)
@@ -3686,6 +3787,97 @@ extern "C" int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t
   }
   DSV_CHECK_LAUNCH("k_dense_p");
   return DSV_OK;
+}
+
+extern "C" int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t out_stride, int32_t normalize,
+                                dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: null arguments");
+  dsv_verify_args a = *args;
+  a.candidates = nullptr;  // no drafts: no accept decisions, no bonus draw
+  if (!out || out_stride < a.vocab) DSV_FAIL(DSV_ERR_INVALID, "dsv_target_probs: output [rows, vocab] required");
+  KParams P;
+  bool hist_possible = false;
+  const int rc = verify_prepare(a, false, "dsv_target_probs", P, hist_possible);
+  if (rc != DSV_OK) return rc;
+  P.raw_p = normalize ? 0 : 1;
+  if (a.rows == 0) return DSV_OK;
+  return launch_target(P, hist_possible, out, out_stride, stream);
+}
+
+// the log rows' stride (floats), and the layout of the filter workspace: log p, the rows'
+// parameters, then the row kernels' workspace with each row a request of its own
+static int64_t filter_log_stride(int64_t vocab) { return align_up(vocab, 64); }
+static int64_t filter_head_bytes(int64_t rows, int64_t vocab) {
+  return align_up(rows * filter_log_stride(vocab) * 4, 256) + 4 * align_up(rows * 4, 256);
+}
+extern "C" int64_t dsv_filter_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows < 0 || vocab < 1) return -1;
+  return filter_head_bytes(rows, vocab) + dsv_verify_workspace_bytes(rows, (int32_t)(rows > 0 ? rows : 1), 1, vocab);
+}
+
+extern "C" int dsv_filter_probs(const dsv_verify_args* args, const float* probs, int64_t probs_stride, float* out,
+                                int64_t out_stride, int32_t normalize, int32_t top_p_over_mass,
+                                dsv_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (!args) DSV_FAIL(DSV_ERR_INVALID, "dsv_filter_probs: null arguments");
+  const dsv_verify_args& a = *args;
+  if (!probs || !out || probs_stride < a.vocab || out_stride < a.vocab)
+    DSV_FAIL(DSV_ERR_INVALID, "dsv_filter_probs: probabilities and output [rows, vocab] required");
+  if (a.bs <= 0 || a.T < 1 || a.vocab < 1 || a.rows != (int64_t)a.bs * a.T || a.row_offsets)
+    DSV_FAIL(DSV_ERR_INVALID, "dsv_filter_probs: rows must be bs * T whole requests (rows %lld, bs %d, T %d)",
+             (long long)a.rows, a.bs, a.T);
+  if (!a.filter) DSV_FAIL(DSV_ERR_INVALID, "dsv_filter_probs: no filter flag (the input is the result)");
+  if (!a.top_ks || !a.workspace) DSV_FAIL(DSV_ERR_INVALID, "dsv_filter_probs: required pointer is null");
+  if (a.rows > 65535)
+    DSV_FAIL(DSV_ERR_UNSUPPORTED, "dsv_filter_probs: at most 65535 rows per call (%lld)", (long long)a.rows);
+  const int64_t need = dsv_filter_workspace_bytes(a.rows, a.vocab);
+  if (a.workspace_bytes < need)
+    DSV_FAIL(DSV_ERR_WORKSPACE, "dsv_filter_probs: workspace %lld < %lld bytes", (long long)a.workspace_bytes,
+             (long long)need);
+  const int64_t rows = a.rows, lstride = filter_log_stride(a.vocab);
+  char* ws = reinterpret_cast<char*>(a.workspace);
+  float* logs = reinterpret_cast<float*>(ws);
+  char* prm = ws + align_up(rows * lstride * 4, 256);
+  const int64_t pb = align_up(rows * 4, 256);
+  int32_t* row_k = reinterpret_cast<int32_t*>(prm);
+  float* row_p = reinterpret_cast<float*>(prm + pb);
+  float* row_minp = reinterpret_cast<float*>(prm + 2 * pb);
+  float* row_t = reinterpret_cast<float*>(prm + 3 * pb);
+  const int32_t vec4 = (uintptr_t)probs % 16 == 0 && probs_stride % 4 == 0 && a.vocab % 4 == 0;
+  hipLaunchKernelGGL(k_prob_prep, dim3((unsigned)rows), dim3(CT), 0, stream, probs, probs_stride, a.vocab, a.T,
+                     a.top_ks, a.top_ps, a.min_ps, top_p_over_mass, vec4, logs, lstride, row_k, row_p, row_minp,
+                     row_t);
+  DSV_CHECK_LAUNCH("k_prob_prep");
+  // each row a request at temperature 1, no penalties, no drafts
+  dsv_verify_args r = a;
+  r.logits = logs;
+  r.logits_dtype = DSV_F32;
+  r.row_stride = lstride;
+  r.bs = (int32_t)rows;
+  r.T = 1;
+  r.verify_lens = nullptr;  // every row is filtered
+  r.temperatures = row_t;
+  r.top_ks = row_k;
+  r.top_ps = row_p;
+  r.min_ps = a.min_ps ? row_minp : nullptr;
+  r.any_greedy = 0;
+  r.sparse_joint = 0;
+  r.hist_ids = nullptr;
+  r.hist_len = 0;
+  r.presence = nullptr;
+  r.repetition = nullptr;
+  r.candidates = nullptr;
+  r.workspace = ws + filter_head_bytes(rows, a.vocab);
+  r.workspace_bytes = a.workspace_bytes - filter_head_bytes(rows, a.vocab);
+  KParams P;
+  bool hist_possible = false;
+  const int rc = verify_prepare(r, false, "dsv_filter_probs", P, hist_possible);
+  if (rc != DSV_OK) return rc;
+  P.raw_p = normalize ? 0 : 1;
+  P.src_p = normalize ? nullptr : probs;
+  P.src_stride = probs_stride;
+  return launch_target(P, hist_possible, out, out_stride, stream);
 }
 
 // Argument checks shared by the greedy-verify entry points (what: the entry point's name).

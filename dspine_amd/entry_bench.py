@@ -8,6 +8,7 @@ and their fraction of MI355X's 8 TB/s.
 
 Algorithmic bytes (the least any implementation moves):
   target_probs     logits read once + P written: 2 + 4 bytes per bf16 logit
+  filter_target_probs  the given P read once + the filtered P written: 4 + 4 bytes per element
   compress_probs   the P a row's result depends on, 4 bytes per element: the whole row when it
                    keeps at most `capacity` ids (every value is checked for negative, NaN or
                    infinite p), else up to its (capacity + 1)-th kept id, where the row is known
@@ -54,7 +55,7 @@ def line(name, us, nbytes=None, **extra):
 
 def main():
     from dspine_amd import workloads as W
-    from dspine_amd.runtime.worker import chain_on_probs, commit_accept
+    from dspine_amd.runtime.worker import SoftmaxTemp, chain_on_probs, commit_accept, filter_probs
     from dspine_amd.sampling.compact import adjust_history, adjust_logits
     from dspine_amd.sampling.random import seeded_uniforms
     from dspine_amd.sampling.sparse.accept import compress_probs
@@ -87,6 +88,15 @@ def main():
     g_info.temperatures = g_info.temperatures.reshape(-1).contiguous()
     us = timed(lambda: target_probs(logits, g_info, bs=bs, T=T, out=P), args.calls)
     line("target_probs_greedy_rows", us, n_logits * 4 + n_logits * 2, shape=[rows, V])
+
+    # a2: the backend filter on given probabilities (runtime/worker.py:473-508): the softmax of
+    # the same logits (temperatures at least 0.5), filtered with the requests' top-k / top-p
+    temps = torch.repeat_interleave(info.temperatures.clamp_min(0.5), T)
+    probs = SoftmaxTemp.execute(logits=logits, temperatures=temps, rows_per_request=1)
+    F = torch.empty_like(P)
+    us = timed(lambda: filter_probs(probs, info, bs=bs, T=T, sampling_backend="pytorch", out=F), args.calls)
+    line("filter_target_probs", us, n_logits * 8, shape=[rows, V], probs="float32")
+    del probs, F
     target_probs(logits, info, bs=bs, T=T, out=P)
 
     # a9: p > 0 compaction of that P

@@ -20,7 +20,7 @@ import torch
 from dspine_amd import _lib
 from dspine_amd.sampling.random import verification_uniforms
 from dspine_amd.sampling.sparse.accept import fill_chain_args, fill_sparse_q
-from dspine_amd.verify import Workspace, target_probs
+from dspine_amd.verify import Workspace, sampling_fields, target_probs
 
 _active_worker = None
 
@@ -59,12 +59,13 @@ def filter_target_probs(probs, sampling_info, t, bs, sampling_backend, normalize
     """runtime/worker.py:473-508 on given probabilities [bs*t, V]: the backend filter, then
     (``normalize``) renormalised; without a filter flag the input is returned as a view.
 
-    The HIP row kernels take logits: log(p) at temperature 1 has softmax p / sum(p), which
-    renormalises to the same distribution; top-k and min-p (a ratio to the row's top p) select
-    the same ids.  The reference's top-p test compares the raw mass ranked ahead of an id with
-    top_p (:52-67; flashinfer's joint branch likewise, its min-p branch renormalises over the
-    top-k first), so each row runs as a request of its own with top_p divided by the row's
-    mass.  With ``normalize`` False the kept entries are the input values themselves."""
+    One library call (``dsv_filter_probs``): a pre-pass writes log p and each row's float64
+    mass, then the HIP row kernels filter every row as a request of its own at temperature 1
+    (softmax(log p) = p / sum(p), which renormalises to the same distribution; top-k and min-p,
+    a ratio to the row's top p, select the same ids).  The reference's top-p test compares the
+    raw mass ranked ahead of an id with top_p (:52-67; flashinfer's joint branch likewise, its
+    min-p branch renormalises over the top-k first), so those rows' top_p is divided by the
+    row's mass.  With ``normalize`` False the kept entries are the input values themselves."""
     need_k = bool(getattr(sampling_info, "need_top_k_sampling", False))
     need_p = bool(getattr(sampling_info, "need_top_p_sampling", False))
     need_min_p = bool(getattr(sampling_info, "need_min_p_sampling", False))
@@ -75,26 +76,45 @@ def filter_target_probs(probs, sampling_info, t, bs, sampling_backend, normalize
     flat = probs.reshape(bs * t, -1)
     if flat.dtype != torch.float32:
         raise ValueError("filter_target_probs expects float32 probabilities")
-    rows, dev = bs * t, flat.device
-
-    def per_row(x, dtype):  # a request's value for each of its t rows
-        return torch.repeat_interleave(torch.as_tensor(x, device=dev).reshape(-1).to(dtype), t)
-
-    top_ps = per_row(sampling_info.top_ps, torch.float32)
-    if need_p and not (sampling_backend == "flashinfer" and need_min_p):
-        mass = flat.sum(-1, dtype=torch.float64)
-        top_ps = torch.where(mass > 0, top_ps.double() / mass, top_ps.double()).float()
-    info = SimpleNamespace(
-        top_ks=per_row(sampling_info.top_ks, torch.int32), top_ps=top_ps,
-        min_ps=per_row(sampling_info.min_ps, torch.float32) if getattr(sampling_info, "min_ps", None) is not None
-        else None,
-        need_top_k_sampling=need_k, need_top_p_sampling=need_p, need_min_p_sampling=need_min_p,
-        max_top_k=getattr(sampling_info, "max_top_k", None),
-        temperatures=torch.ones(rows, device=dev), is_any_greedy=False)
-    out = target_probs(torch.log(flat), info, bs=rows, T=1, sampling_backend=sampling_backend)
-    if not normalize:
-        out = torch.where(out > 0, flat, torch.zeros((), device=flat.device))
+    if flat.stride(1) != 1:
+        raise ValueError("filter_target_probs expects row-contiguous probabilities")
+    out = filter_probs(flat, sampling_info, bs=bs, T=t, sampling_backend=sampling_backend, normalize=normalize,
+                       top_p_over_mass=need_p and not (sampling_backend == "flashinfer" and need_min_p))
     return out.view(bs, t, -1)
+
+
+def filter_probs(probs, info, *, bs: int, T: int, sampling_backend: str, normalize: bool = True,
+                 top_p_over_mass: bool = True, out: torch.Tensor | None = None,
+                 workspace: Workspace | None = None) -> torch.Tensor:
+    """``dsv_filter_probs`` on float32 probabilities [bs*T, V] with the per-request sampling
+    parameters of ``info``; returns out [bs*T, V] float32."""
+    lib = _lib.load()
+    dev = _lib.require_cuda(probs, out)
+    if probs.ndim != 2 or probs.dtype != torch.float32 or probs.stride(1) != 1:
+        raise ValueError("probabilities must be a row-contiguous float32 [rows, V] tensor")
+    rows, V = probs.shape
+    if bs < 1 or T < 1 or rows != bs * T:
+        raise ValueError(f"probability rows {rows} != bs*T ({bs}*{T})")
+    if out is None:
+        out = torch.empty((rows, V), device=dev, dtype=torch.float32)
+    if out.shape != (rows, V) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be a row-contiguous float32 [rows, V] tensor")
+    a = _lib.VerifyArgs()
+    keep = sampling_fields(a, info, bs, dev, sampling_backend)
+    ws = workspace if workspace is not None else _filter_ws.setdefault(dev, Workspace())
+    wbuf = ws.get(int(lib.dsv_filter_workspace_bytes(rows, V)), dev)
+    a.logits, a.logits_dtype = probs.data_ptr(), _lib.DSV_F32
+    a.rows, a.vocab, a.row_stride = rows, V, probs.stride(0)
+    a.bs, a.T = bs, T
+    a.workspace, a.workspace_bytes = wbuf.data_ptr(), wbuf.numel()
+    _lib.check(lib.dsv_filter_probs(a, probs.data_ptr(), probs.stride(0), out.data_ptr(), out.stride(0),
+                                    int(bool(normalize)), int(bool(top_p_over_mass)), _lib.stream_of(dev)),
+               "dsv_filter_probs")
+    del keep
+    return out
+
+
+_filter_ws: dict = {}
 
 
 def dspine_accept_sampling(*, target_probs=None, candidates, target_logits, candidate_ids, q_rows,

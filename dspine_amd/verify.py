@@ -219,7 +219,7 @@ def sampling_fields(a, info, bs: int, dev, sampling_backend: str):
     if not isinstance(max_top_k, int):
         max_top_k = TOP_K_ALL  # unknown on the host: nucleus rows may occur
     a.backend = _lib.DSV_BACKEND_PYTORCH if sampling_backend == "pytorch" else _lib.DSV_BACKEND_FLASHINFER
-    a.temperatures, a.top_ks, a.top_ps = temps.data_ptr(), top_ks.data_ptr(), top_ps.data_ptr()
+    a.temperatures, a.top_ks, a.top_ps = _lib.ptr(temps), top_ks.data_ptr(), top_ps.data_ptr()
     a.min_ps = _lib.ptr(min_ps)
     a.filter = int(need_k or need_p or need_min_p)
     a.need_min_p = int(need_min_p)

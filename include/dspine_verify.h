@@ -23,7 +23,9 @@
  *   dsv_adjust_history    sampling/compact.py:47-63 with SGLang's presence/repetition penalizers
  *                         given as a per-request token history
  *   dsv_logits_padding    sampling/padding.py:4-12 (logits_padding)
- *   dsv_target_probs      runtime/worker.py:440-508 (build_dspine_target_probs, filter_target_probs)
+ *   dsv_target_probs      runtime/worker.py:440-470 (build_dspine_target_probs)
+ *   dsv_filter_probs      runtime/worker.py:473-508 (filter_target_probs, its backend filter
+ *                         :52-67 on given probabilities)
  *   dsv_accept_chain      sampling/rejection.py:12-153 (_sample_capped_chain,
  *                         sample_capped_chain_from_probs) and sampling/sparse/accept.py:81-543
  *                         (accept_sparse with dense, RAW or packed P)
@@ -218,6 +220,20 @@ int dsv_window_index(const void* qo_indptr, int32_t qo_i64, int32_t bs, int32_t 
 /* uniforms and outputs are ignored.                                                          */
 int dsv_target_probs(const dsv_verify_args* args, float* out, int64_t out_stride, int32_t normalize,
                      dsv_stream_t stream);
+
+/* The backend filter on given probabilities probs [rows, vocab] float32 (row stride           */
+/* probs_stride; runtime/worker.py:473-508 filter_target_probs), rows = bs * T, the sampling   */
+/* parameters per request as in dsv_verify_args (temperatures and the history are ignored:   */
+/* each row is filtered at temperature 1, none is greedy).  out [rows, vocab]: the kept      */
+/* entries renormalised (normalize = 0: the input values themselves), zeros elsewhere.        */
+/* top_p_over_mass = 1 compares the raw mass ranked ahead of an entry with top_p (the         */
+/* pytorch backend, flashinfer's joint branch): each row's top_p is divided by its float64    */
+/* mass.  Requires a filter flag and rows <= 65535; the workspace holds                       */
+/* dsv_filter_workspace_bytes(rows, vocab) bytes.  Entries that round to the same log p tie   */
+/* (broken by the lower id).                                                                  */
+int64_t dsv_filter_workspace_bytes(int64_t rows, int64_t vocab);
+int dsv_filter_probs(const dsv_verify_args* args, const float* probs, int64_t probs_stride, float* out,
+                     int64_t out_stride, int32_t normalize, int32_t top_p_over_mass, dsv_stream_t stream);
 
 /* Per row, the ids with p > 0 in id order up to `capacity` ([rows, capacity] int32 ids /   */
 /* float32 values, unused slots -1 / 0), lengths = min(n, capacity), overflow = n > capacity  */
