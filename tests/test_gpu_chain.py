@@ -319,6 +319,36 @@ def test_build_target_probs_nucleus(device, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nucleus_cut_inside_ties_across_chunks(device, dtype):
+    """A top-p cut inside a group of 40 equal values spread over every chunk of the row (ids
+    1237 apart, 85 % of the mass): the kept ties are the lowest ids, so each chunk's ties rank
+    after the earlier chunks' (the counts the full-row resolver records for float32 rows).  Both
+    the target distribution and the filter on the same rows' probabilities."""
+    from dspine_amd.runtime.worker import build_dspine_target_probs, filter_target_probs
+
+    O = _O()
+    bs, T, V = 2, 2, 50021
+    g = torch.Generator().manual_seed(41)
+    logits = (torch.randn(bs * T, V, generator=g) * 2.5).to(dtype)
+    ids = torch.arange(40) * 1237
+    logits[:, ids] = 12.0
+    info = W.sampling_info([1.0, 1.0], [0, 0], [0.5, 0.3])
+    got = build_dspine_target_probs(next_token_logits=logits.to(device), sampling_info=W.info_to(info, device),
+                                    block_size=T, bs=bs, sampling_backend="pytorch")
+    torch.cuda.synchronize()
+    ref = O.build_target_probs(logits, info, T, bs, "pytorch", exact_softmax=True)
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
+    kept = (ref.view(bs * T, V)[:, ids] > 0).sum(-1)
+    assert int(kept.min()) > 0 and int(kept.max()) < 40  # the cut splits the group in every row
+    probs = O.softmax_temp(logits.float(), torch.ones(bs * T), exact=True)
+    got = filter_target_probs(probs.to(device), W.info_to(info, device), T, bs, "pytorch")
+    torch.cuda.synchronize()
+    ref = O.filter_target_probs(probs.clone(), info, T, bs, "pytorch")
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=1e-9)
+    assert torch.equal(got.cpu() > 0, ref > 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_build_target_probs_flashinfer_min_p(device, dtype):
     """flashinfer's min-p branch on nucleus rows (top-k off or > 64): top-p on the mass
     renormalised over the top-k, then min-p against the max (tests/ref_utils.py:79-108)."""
