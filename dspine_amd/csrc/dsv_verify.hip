@@ -3138,18 +3138,16 @@ __device__ __forceinline__ void dense_p_spans(const KParams& P, int64_t r, int c
 
 
 // ---------------------------------------------------------------------------------------
-// The target distribution of one (row, chunk) written out densely (runtime/worker.py:440-508),
-// from the row's summary rs (mode M_SKIP: zeros; b is the row's request).  The chunk's values
-// are laid out as the chunk pass loads them (thread t, vector u: ids (u CT + t) n .. + n), so
-// that a wave's loads and 16-byte stores are contiguous; support-list rows write zeros with the
-// list's values at their ids (an LDS bitmap of the chunk's list ids), greedy rows the one-hot
-// row.  Rows whose cut keeps only some of the values at the cut key (when the chunks' counts of
-// them are unknown), and unaligned outputs, take the ordered path above.  Callers that write
-// several chunks in a row put a barrier between the calls (the LDS arrays are reused).
+// k_dense_p: the target distribution written out densely (runtime/worker.py:440-508), one
+// workgroup per (row, chunk).  The chunk's values are laid out as the chunk pass loads them
+// (thread t, vector u: ids (u CT + t) n .. + n), so that a wave's loads and 16-byte stores are
+// contiguous; support-list rows write zeros with the list's values at their ids (an LDS bitmap
+// of the chunk's list ids), greedy rows the one-hot row.  Rows whose cut keeps only some of the
+// values at the cut key (when the chunks' counts of them are unknown), and unaligned outputs,
+// take the ordered path above.
 // ---------------------------------------------------------------------------------------
 template <int DT, bool ALIGNED>
-__device__ __forceinline__ void dense_p_chunk(const KParams& P, int64_t r, int c, int b, const RowSum& rs, int mode,
-                                              float* out, int64_t out_stride) {
+__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
   constexpr int n = Elems<DT>::n, CV = Elems<DT>::cv, CHE = Elems<DT>::chunk;
   constexpr int NW = CT / WAVE;
   __shared__ ListEntry lst[DSV_LIST_K];
@@ -3159,9 +3157,16 @@ __device__ __forceinline__ void dense_p_chunk(const KParams& P, int64_t r, int c
   __shared__ int32_t s_wt[CV * NW];     // partial ties: each wave's cut-key values of vector u
   __shared__ int32_t s_before;          // partial ties: the cut-key values of the earlier chunks
   const dsv_verify_args& a = P.a;
+  const int C = P.C;
+  const int64_t r = blockIdx.x / C;
+  const int c = (int)(blockIdx.x - r * C);
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
   const int64_t V = a.vocab;
   float* orow = out + r * out_stride;
+  int b = 0, s = 0;
+  const bool live_row = row_request(a, r, b, s);
+  const RowSum rs = P.rowsum[r];
+  const int mode = live_row ? rs.mode : M_SKIP;
   const bool hist = mode == M_HIST;
   const bool vec_ok = (out_stride % 4 == 0) && ((uintptr_t)out % 16 == 0);
   // a cut that keeps only the first ktie values of the cut key in id order (partial ties)
@@ -3377,18 +3382,6 @@ __device__ __forceinline__ void dense_p_chunk(const KParams& P, int64_t r, int c
     write_rows(std::true_type{});
   else
     write_rows(std::false_type{});
-}
-
-// k_dense_p: P of one (row, chunk) a workgroup, from the row summaries.
-template <int DT, bool ALIGNED>
-__global__ __launch_bounds__(CT) void k_dense_p(KParams P, float* out, int64_t out_stride) {
-  const int C = P.C;
-  const int64_t r = blockIdx.x / C;
-  const int c = (int)(blockIdx.x - r * C);
-  int b = 0, s = 0;
-  const bool live_row = row_request(P.a, r, b, s);
-  const RowSum rs = P.rowsum[r];
-  dense_p_chunk<DT, ALIGNED>(P, r, c, b, rs, live_row ? rs.mode : M_SKIP, out, out_stride);
 }
 
 // ---------------------------------------------------------------------------------------
