@@ -30,6 +30,8 @@ typedef double d4 __attribute__((ext_vector_type(4)));
 constexpr int FX_THREADS = 256;
 constexpr int GT = 64;   // GEMM tile (rows and columns of C a workgroup computes)
 constexpr int GK = 32;   // k depth a tile stage holds
+constexpr int GB = 128;  // the large GEMM tile (grids that fill the part), 16 deep a stage
+constexpr int GKB = 16;
 constexpr int FX_KMAX = 64;
 constexpr int FX_SPLIT_MAX = 16;
 
@@ -125,6 +127,102 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_gemm(const double* __restrict
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t gm = m0 + wm + 16 * i + 4 * v + lg, gn = n0 + wn + 16 * j + li;
+        if (gm < M && gn < N) Cz[gm * N + gn] = accumulate ? Cz[gm * N + gn] + acc[i][j][v] : acc[i][j][v];
+      }
+}
+
+// A raw buffer over [base, base + bytes): loads past its end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fx_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ double fx_load8(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  const auto t = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)voff, (int)soff, 0);
+  return __builtin_bit_cast(double, t);
+}
+// bytes spanned by a rows x cols operand with element strides (rs, cs), float64
+__host__ __device__ __forceinline__ int64_t fx_extent(int64_t rows, int64_t rs, int64_t cols, int64_t cs) {
+  return rows > 0 && cols > 0 ? ((rows - 1) * rs + (cols - 1) * cs + 1) * 8 : 0;
+}
+
+// The same product on 128 x 128 tiles: each wave a 64 x 64 quarter (4 x 4 MFMA tiles, sixteen
+// accumulators), 16-deep stages -- 16 MFMAs a wave for every 8 fragment reads, and a quarter of
+// the 64-tile kernel's operand traffic per flop.  For grids of at least a round of workgroups.
+__global__ __launch_bounds__(FX_THREADS, 2) void k_fx_gemm_big(const double* __restrict__ A, int64_t am, int64_t ak,
+                                                           const double* __restrict__ B, int64_t bk, int64_t bn,
+                                                           double* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                           int64_t kchunk, int accumulate) {
+  constexpr int PER = (GB * GKB) / FX_THREADS;  // 8 elements of each operand a thread stages
+  static_assert(FX_THREADS % GKB == 0 && FX_THREADS % GB == 0, "staging strides");
+  constexpr int ARS = FX_THREADS / GKB, BKS = FX_THREADS / GB;  // 16 rows / 2 depths apart
+  __shared__ double As[GB][GKB + 1];
+  __shared__ double Bs[GKB][GB + 1];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+  const int64_t m0 = (int64_t)blockIdx.y * GB, n0 = (int64_t)blockIdx.x * GB;
+  const int64_t k_lo = (int64_t)blockIdx.z * kchunk;
+  const int64_t k_hi = k_lo + kchunk < K ? k_lo + kchunk : K;
+  const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+  const int li = lane & 15, lg = lane >> 4;
+  d4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = d4{0.0, 0.0, 0.0, 0.0};
+  // thread t stages A rows t / 16 + 16 e at depth t % 16, and B depths t / 128 + 2 e at column
+  // t % 128 (the next stage loaded into registers while the current one is multiplied)
+  // (raw buffers over the operands' extents -- under 2 GB, checked by the launcher: 32-bit lane
+  // offsets, the stage's k offset a scalar one, no 64-bit address arithmetic per element)
+  const int a_r = tid / GKB, a_k = tid % GKB, b_k = tid / GB, b_n = tid % GB;
+  const int64_t gn_b = n0 + b_n;
+  const auto rsa = fx_rsrc(A, fx_extent(M, am, K, ak));
+  const auto rsb = fx_rsrc(B, fx_extent(K, bk, N, bn));
+  const uint32_t a_off = (uint32_t)(((m0 + a_r) * am + (k_lo + a_k) * ak) * 8);
+  const uint32_t b_off = (uint32_t)(((k_lo + b_k) * bk + gn_b * bn) * 8);
+  const uint32_t a_step = (uint32_t)(ARS * am * 8), b_step = (uint32_t)(BKS * bk * 8);
+  double ra[PER], rb[PER];
+  auto fetch = [&](int64_t kofs) {
+    const bool ka = k_lo + kofs + a_k < k_hi;
+    const uint32_t sa = (uint32_t)(kofs * ak * 8), sb = (uint32_t)(kofs * bk * 8);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const bool ina = ka && m0 + a_r + e * ARS < M;
+      const double xa = fx_load8(rsa, a_off + (uint32_t)e * a_step, sa);
+      ra[e] = ina ? xa : 0.0;
+      const bool inb = gn_b < N && k_lo + kofs + b_k + e * BKS < k_hi;
+      const double xb = fx_load8(rsb, b_off + (uint32_t)e * b_step, sb);
+      rb[e] = inb ? xb : 0.0;
+    }
+  };
+  if (k_lo < k_hi) fetch(0);
+  for (int64_t k0 = k_lo; k0 < k_hi; k0 += GKB) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      As[a_r + e * ARS][a_k] = ra[e];
+      Bs[b_k + e * BKS][b_n] = rb[e];
+    }
+    __syncthreads();
+    if (k0 + GKB < k_hi) fetch(k0 + GKB - k_lo);
+#pragma unroll
+    for (int s = 0; s < GKB / 4; ++s) {
+      double a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[wm + 16 * i + li][4 * s + lg];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[4 * s + lg][wn + 16 * j + li];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  double* Cz = C + (int64_t)blockIdx.z * M * N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t gm = m0 + wm + 16 * i + 4 * v + lg, gn = n0 + wn + 16 * j + li;
@@ -265,17 +363,35 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_msg(FxP P) {
   const int64_t i = blockIdx.x;
   const int64_t req = i / (a.T - 1), pos = i % (a.T - 1);
   const int64_t src = req * a.T + pos + 1;
-  for (int idx = threadIdx.x; idx < a.K * a.R; idx += FX_THREADS) {
-    const int j = idx / a.R, r = idx % a.R;
-    int64_t sid = pos == 0 ? a.anchors[req] : a.cand[(i - 1) * a.K + j];
-    int64_t cid = a.cand[i * a.K + j];
-    sid = sid < 0 ? 0 : (sid >= a.vocab ? a.vocab - 1 : sid);
-    cid = cid < 0 ? 0 : (cid >= a.vocab ? a.vocab - 1 : cid);
-    const double q = ld_any(a.query, a.query_dtype, src * a.query_stride + r);
-    const double gate = q + a.G[sid * a.R + r] + a.bias[r];
-    const double sig = 1.0 / (1.0 + exp(-gate));
-    a.message[(i * a.K + j) * a.R + r] = sig * a.Vm[sid * a.R + r];
-    a.tg[(i * a.K + j) * a.R + r] = a.TG[cid * a.R + r];
+  // four elements a thread at a time: their operands loaded together, then computed and stored
+  constexpr int U = 4;
+  const int total = a.K * a.R;
+  for (int idx0 = threadIdx.x; idx0 < total; idx0 += FX_THREADS * U) {
+    double q[U], g[U], bs[U], vm[U], tgv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = idx0 + u * FX_THREADS;
+      const int id = idx < total ? idx : total - 1;
+      const int j = id / a.R, r = id % a.R;
+      int64_t sid = pos == 0 ? a.anchors[req] : a.cand[(i - 1) * a.K + j];
+      int64_t cid = a.cand[i * a.K + j];
+      sid = sid < 0 ? 0 : (sid >= a.vocab ? a.vocab - 1 : sid);
+      cid = cid < 0 ? 0 : (cid >= a.vocab ? a.vocab - 1 : cid);
+      q[u] = ld_any(a.query, a.query_dtype, src * a.query_stride + r);
+      g[u] = a.G[sid * a.R + r];
+      bs[u] = a.bias[r];
+      vm[u] = a.Vm[sid * a.R + r];
+      tgv[u] = a.TG[cid * a.R + r];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = idx0 + u * FX_THREADS;
+      if (idx >= total) continue;
+      const double gate = q[u] + g[u] + bs[u];
+      const double sig = 1.0 / (1.0 + exp(-gate));
+      a.message[i * total + idx] = sig * vm[u];
+      a.tg[i * total + idx] = tgv[u];
+    }
   }
 }
 
@@ -290,10 +406,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_final(FxP P) {
   const int64_t i = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
   const int K = a.K, R = a.R;
-  // x W for this row: the split parts summed in order
+  // x W for this row: the split parts summed in order (eight parts' loads in flight together)
   for (int r = tid; r < R; r += FX_THREADS) {
     double s = 0.0;
-    for (int z = 0; z < P.split; ++z) s += P.xw_part[((int64_t)z * a.n + i) * R + r];
+    int z = 0;
+    for (; z + 8 <= P.split; z += 8) {
+      double pz[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pz[u] = P.xw_part[((int64_t)(z + u) * a.n + i) * R + r];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += pz[u];
+    }
+    for (; z < P.split; ++z) s += P.xw_part[((int64_t)z * a.n + i) * R + r];
     xw[r] = s;
   }
   const double* msg = a.message + i * K * R;
@@ -304,11 +428,19 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_final(FxP P) {
     d4 acc = {0.0, 0.0, 0.0, 0.0};
     const int per = (R + 4 * (FX_THREADS / WAVE) - 1) / (4 * (FX_THREADS / WAVE)) * 4;
     const int r_lo = w * per, r_hi = r_lo + per < R ? r_lo + per : R;
-    for (int r0 = r_lo; r0 < r_hi; r0 += 4) {
-      const int r = r0 + lg;
-      const double av = (li < K && r < r_hi) ? msg[(int64_t)li * R + r] : 0.0;
-      const double bv = (li < K && r < r_hi) ? tgr[(int64_t)li * R + r] : 0.0;
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+    // eight 4-deep steps' operands loaded together, then their products in step order
+    for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
+      double av[8], bv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int r = r0 + 4 * u + lg;
+        const bool in = li < K && r < r_hi;
+        av[u] = in ? msg[(int64_t)li * R + r] : 0.0;
+        bv[u] = in ? tgr[(int64_t)li * R + r] : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (r0 + 4 * u < r_hi) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[u], bv[u], acc, 0, 0, 0);
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) prod[w * 256 + (4 * v + lg) * 16 + li] = acc[v];
@@ -322,10 +454,21 @@ __global__ __launch_bounds__(FX_THREADS) void k_fx_final(FxP P) {
     if (j < K) {
       const double* mj = msg + (int64_t)j * R;
       const double* gj = P.mg + (i * K + j) * R;
-      for (int r = gl; r < R; r += 16) {
-        const double mv = mj[r];
-        cr += xw[r] * mv;
-        qd += gj[r] * mv;
+      // eight steps' loads in flight together, summed in step order
+      for (int r0 = gl; r0 < R; r0 += 128) {
+        double mv[8], gv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int r = r0 + 16 * u;
+          mv[u] = r < R ? mj[r] : 0.0;
+          gv[u] = r < R ? gj[r] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (r0 + 16 * u < R) {
+            cr += xw[r0 + 16 * u] * mv[u];
+            qd += gv[u] * mv[u];
+          }
       }
     }
 #pragma unroll
@@ -421,8 +564,8 @@ static int fx_split_cap(int32_t H) {
   return s;
 }
 static int fx_split(int64_t n, int32_t R, int32_t H) {
-  // enough workgroups over n x R tiles to fill the part
-  const int64_t tiles = ((n + GT - 1) / GT) * ((R + GT - 1) / GT);
+  // enough workgroups over n x R (128-wide) tiles to fill the part
+  const int64_t tiles = ((n + GB - 1) / GB) * ((R + GB - 1) / GB);
   int s = 1;
   while (s < fx_split_cap(H) && tiles * s < 512) s *= 2;
   return s;
@@ -435,11 +578,21 @@ extern "C" int64_t dsv_factor_workspace_doubles(int64_t n, int32_t K, int32_t H,
 
 static void fx_gemm(const double* A, int64_t am, int64_t ak, const double* B, int64_t bk, int64_t bn, double* C,
                     int64_t M, int64_t N, int64_t K, int split, int accumulate, hipStream_t stream) {
+  const int64_t big_tiles = ((N + GB - 1) / GB) * ((M + GB - 1) / GB) * split;
+  // (a round of 128-tile workgroups, two a CU; operands addressed by 32-bit buffer offsets)
+  const bool big = big_tiles >= 240 && fx_extent(M, am, K, ak) < (1ll << 31) && fx_extent(K, bk, N, bn) < (1ll << 31);
+  const int gk = big ? GKB : GK;
   int64_t kchunk = (K + split - 1) / split;
-  kchunk = (kchunk + GK - 1) / GK * GK;
-  const dim3 grid((unsigned)((N + GT - 1) / GT), (unsigned)((M + GT - 1) / GT), (unsigned)split);
-  hipLaunchKernelGGL(k_fx_gemm, grid, dim3(FX_THREADS), 0, stream, A, am, ak, B, bk, bn, C, M, N, K, kchunk,
-                     accumulate);
+  kchunk = (kchunk + gk - 1) / gk * gk;
+  if (big) {
+    const dim3 grid((unsigned)((N + GB - 1) / GB), (unsigned)((M + GB - 1) / GB), (unsigned)split);
+    hipLaunchKernelGGL(k_fx_gemm_big, grid, dim3(FX_THREADS), 0, stream, A, am, ak, B, bk, bn, C, M, N, K, kchunk,
+                       accumulate);
+  } else {
+    const dim3 grid((unsigned)((N + GT - 1) / GT), (unsigned)((M + GT - 1) / GT), (unsigned)split);
+    hipLaunchKernelGGL(k_fx_gemm, grid, dim3(FX_THREADS), 0, stream, A, am, ak, B, bk, bn, C, M, N, K, kchunk,
+                       accumulate);
+  }
 }
 
 static int fx_check_layout(const dsv_factor_args* args, const char* what) {
