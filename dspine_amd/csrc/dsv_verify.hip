@@ -637,9 +637,12 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
   const float vc = hist ? value_of_key<DT>(rs.vcut) : -INFINITY;
   double mt = 0.0;
   int32_t tt = 0;  // the span's values at the cut key
+  float su_prev = 0.f;
 #pragma unroll
   for (int u = 0; u < SV; ++u) {
     float su = 0.f;
+    // one vector's exponentials at a time, after the previous vector's sum: no weights held
+    reg_fence1(sp.v[u], su_prev);
 #pragma unroll
     for (int e = 0; e < n; ++e) {
       const float x = vec_elem<DT>(sp.v[u], e);
@@ -648,6 +651,7 @@ __device__ __forceinline__ int64_t dense_pick(const KParams& P, int b, const cha
       tt += (hist && x == vc) ? 1 : 0;
     }
     mt += (double)su;
+    su_prev = su;
   }
   int32_t tie_tot = 0;
   const int32_t tbefore = sh.tieq + block_excl_scan<NW>(tt, sh.red_i, &tie_tot);
