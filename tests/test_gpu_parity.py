@@ -248,6 +248,19 @@ def test_verify_small_mixed(device, seed, dtype, penalties):
     assert len(near) <= 1
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_small_mixed_flashinfer(device, seed, dtype):
+    """The mixed small batches under the flashinfer backend without min-p (greedy rows present:
+    the joint support by rank, not the sparse joint route), with penalties and verify lengths."""
+    batch = _small_batch(seed, dtype=dtype, penalties=True)
+    bs = batch["candidates"].shape[0]
+    gpu = run_gpu_verify(batch, device, backend="flashinfer")
+    ref = run_oracle(batch, list(range(bs)), backend="flashinfer")
+    near = compare_outputs(gpu, ref, range(bs), f"small flashinfer seed={seed}")
+    assert len(near) <= 1
+
+
 @pytest.mark.parametrize("mix", ["greedy", "lists", "unfiltered", "nucleus", "lists_and_greedy"])
 def test_verify_launch_sets(device, mix):
     """Batches of one kind of request, which launch different kernel sets: greedy-only and
@@ -456,14 +469,14 @@ def test_verify_unfiltered(device):
     assert len(compare_outputs(gpu, ref, range(bs), "unfiltered")) <= 1
 
 
-def _full(batch, device, tag):
+def _full(batch, device, tag, backend="pytorch"):
     """Every request against the oracle with its exact softmax (the parity bound), then against
     its literal float32 softmax (recorded, tests/parity.py)."""
     bs = batch["candidates"].shape[0]
-    gpu = run_gpu_verify(batch, device)
-    ref = run_oracle(batch, list(range(bs)))
+    gpu = run_gpu_verify(batch, device, backend=backend)
+    ref = run_oracle(batch, list(range(bs)), backend=backend)
     compare_outputs(gpu, ref, range(bs), tag)
-    literal = run_oracle(batch, list(range(bs)), exact_softmax=False)
+    literal = run_oracle(batch, list(range(bs)), backend=backend, exact_softmax=False)
     parity.compare_literal(gpu, literal, ref, range(bs), tag)
     return gpu, ref
 
@@ -472,6 +485,13 @@ def test_verify_serving_round_full(device):
     """The benchmark's serving workload (64 x 17 x 151936 bf16, penalties, mixed modes, KV
     slots): every request against the oracle."""
     _full(W.serving_round(), device, "serving 64x17x151936 bf16")
+
+
+def test_verify_serving_round_full_flashinfer(device):
+    """The serving workload under the flashinfer backend: its greedy requests keep the batch off
+    the sparse joint route, so every sampled row takes the joint support by rank (top-k, then the
+    top-p test on the mass ranked ahead); every request against the oracle."""
+    _full(W.serving_round(), device, "serving 64x17x151936 bf16 flashinfer", backend="flashinfer")
 
 
 def test_verify_serving_round_deep_accept(device):
