@@ -91,6 +91,22 @@ def test_sparse_joint_full_vocab(device):
     assert any(not np.array_equal(rank[n], ref[n]) for n in ("accept", "bonus")), "the case should tell the routes apart"
 
 
+def test_sparse_joint_full_vocab_f32(device):
+    """The same route on float32 logits at the full vocabulary (12 requests x 16 rows x 151936,
+    13 chunks a row), a third of the requests integer-valued: every request against the oracle,
+    exact and literal softmax."""
+    batch = W.sparse_round(bs=12, seed=8, coarse_every=3, dtype=torch.float32)
+    bs = batch["candidates"].shape[0]
+    assert _O().sparse_route(batch["info"], "flashinfer", batch["logits"].shape[1], batch["q_ids"].shape[-1])
+    ref = _oracle(batch)
+    tied, dense = _tie_stats(ref, batch)
+    assert dense > 10, (tied, dense)
+    got = _gpu(batch, device)
+    tag = f"sparse joint 12x16x151936 fp32 (tied rows {tied}, dense {dense})"
+    parity.compare_requests(got, ref, range(bs), tag, extra=())
+    parity.compare_literal(got, _oracle(batch, exact_softmax=False), ref, range(bs), tag)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("seed", [1, 2])
 def test_sparse_joint_small(device, dtype, seed):
