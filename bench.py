@@ -175,9 +175,10 @@ def _cpu_median(run, runs=10, warm=2):
     return sorted(times)[len(times) // 2], n, times
 
 
-def cpu_verify_baseline(batch, requests=8, sparse_joint=False, backend="pytorch"):
+def cpu_verify_baseline(batch, requests=32, sparse_joint=False, backend="pytorch"):
     """The CPU oracle (torch on the host) on a bounded sample of the same workload: the first
-    `requests` requests verified in one oracle call, median of 10 calls after 2 warm-ups."""
+    `requests` requests verified in one oracle call (about a second a call on the serving
+    workload), median of 10 calls after 2 warm-ups."""
     import numpy as np
 
     import oracle.verify_oracle as O
@@ -206,8 +207,9 @@ def cpu_verify_baseline(batch, requests=8, sparse_joint=False, backend="pytorch"
                       f"median of {len(times)} calls after 2 warm-ups ({sum(times):.1f} s timed)"}
 
 
-def cpu_topk_baseline(x, k, rows=64):
-    """The CPU oracle's top-k (stable descending sort) on the first `rows` rows, median of 10."""
+def cpu_topk_baseline(x, k, rows=1088):
+    """The CPU oracle's top-k (stable descending sort) on the first `rows` rows (every row of the
+    workload by default), median of 10."""
     import oracle.verify_oracle as O
 
     sl = x[:rows].float()
