@@ -3620,8 +3620,10 @@ static int verify_prepare(const dsv_verify_args& a, bool drafts, const char* wha
              "%s: the sparse joint target needs the verify step, the flashinfer backend, no min-p, no greedy "
              "rows and 1 <= max_top_k <= %d (<= vocab)", what, SJ_CAP);
   if (drafts) {
-    if (!a.top_ps || !a.candidates || !a.q_ids || !a.q_values || !a.uniforms || !a.uniform_final || !a.prefix_lens ||
-        !a.accept || !a.commit || !a.bonus || !a.output || !a.new_seq)
+    // (a block of one row verifies no draft: its q and per-step coins are empty arrays)
+    const bool steps = a.T >= 2;
+    if (!a.top_ps || !a.candidates || (steps && (!a.q_ids || !a.q_values || !a.uniforms)) || !a.uniform_final ||
+        !a.prefix_lens || !a.accept || !a.commit || !a.bonus || !a.output || !a.new_seq)
       DSV_FAIL(DSV_ERR_INVALID, "%s: required pointer is null", what);
     if (a.K < 1 || a.K > QMAX) DSV_FAIL(DSV_ERR_INVALID, "%s: q width K=%d outside [1, %d]", what, a.K, QMAX);
   }

@@ -117,10 +117,10 @@ typedef struct dsv_verify_args {
   const float* repetition;       /* [bs]: x<0 ? x*r : x/r on history tokens */
   /* draft proposal */
   const int64_t* candidates;     /* [bs, T]: anchor then T-1 drafts */
-  const void* q_ids;             /* [bs, T-1, K] int32 or int64 */
+  const void* q_ids;             /* [bs, T-1, K] int32 or int64 (may be NULL when T == 1) */
   int32_t q_ids_i64, K;
-  const float* q_values;         /* [bs, T-1, K] */
-  const float* uniforms;         /* [bs, T-1] */
+  const float* q_values;         /* [bs, T-1, K] (may be NULL when T == 1) */
+  const float* uniforms;         /* [bs, T-1] (may be NULL when T == 1) */
   const float* uniform_final;    /* [bs] */
   const int32_t* prefix_lens;    /* [bs] */
   const int32_t* page_table;     /* [bs, page_cols] (page size 1) or NULL */
