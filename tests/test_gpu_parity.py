@@ -512,6 +512,14 @@ def test_verify_ragged_round_full(device):
     _full(W.ragged_round(), device, "ragged 32x(4..16)x262144 bf16")
 
 
+def test_verify_rejection_and_ragged_flashinfer(device):
+    """The rejection (top-k 20, top-p 0.95; 20 q lanes, so not the sparse joint route) and ragged
+    (top-p 0.9 over the whole vocabulary) workloads under the flashinfer backend: every request."""
+    _full(W.rejection_round(sigma_draft=0.5), device, "rejection 32x17x151936 fp32 sigma=0.5 flashinfer",
+          backend="flashinfer")
+    _full(W.ragged_round(), device, "ragged 32x(4..16)x262144 bf16 flashinfer", backend="flashinfer")
+
+
 def test_topk_rows_full(device):
     """The top-k workload ([1088, 151936] bf16, planted peaks, ~1% duplicates): all rows for
     k in {1, 20, 64}, ids and values bit-exact in (value desc, id asc) order."""
