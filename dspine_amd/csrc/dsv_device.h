@@ -326,6 +326,11 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t rs, uint32_t 
   const auto t = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (int)soff, 2);
   return make_uint4(t[0], t[1], t[2], t[3]);
 }
+// The same load with the default cache policy (the lines stay in the caches for a later reader).
+__device__ __forceinline__ uint4 buf_load16_cached(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  const auto t = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (int)soff, 0);
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff, (int)soff, 0);
 }

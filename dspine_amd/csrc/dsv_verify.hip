@@ -151,6 +151,7 @@ __device__ __noinline__ int count_key_chunk(const uint32_t* cbits, const char* r
 // Bonus draw machinery (used by the row merge and k_final; see the bonus section below)
 // ---------------------------------------------------------------------------------------
 constexpr int FCT = 512;      // threads of k_final
+constexpr int KF_ROLES = 4;   // k_final workgroups a request: the request's own and three helpers
 constexpr int DNW_MAX = FCT / WAVE;
 constexpr int64_t BONUS_LATER = -2;  // rbonus: the row is drawn in k_final
 // rbonus <= BONUS_PLAN: the row's draw is planned; the request's final scans chunk
@@ -2870,8 +2871,40 @@ __global__ __launch_bounds__(FCT) void k_final(KParams P) {
   __shared__ uint4 s_hv[FCT / WAVE * WHITV];  // history-hit slots of the draw
   __shared__ uint32_t s_hm[FCT / WAVE * WHITV];
   const dsv_verify_args& a = P.a;
-  const int b = blockIdx.x;
+  // KF_ROLES workgroups a request: role 0 decides it; the others are helpers (below).  A
+  // request's workgroups are bs apart, so for bs a multiple of 8 they share an XCD (and its L2).
+  const int b = (int)(blockIdx.x % (unsigned)a.bs);
+  const int role = (int)(blockIdx.x / (unsigned)a.bs);
   const uint32_t dfl = P.only_deferred ? P.deferred[b] : 1u;
+  if (role != 0) {
+    // A helper: when the row merge planned the request's draw (the accepted row and its chunk
+    // ride in the deferred flag), a share of that chunk is read with the default cache policy,
+    // so that the lines are in the caches when role 0 streams the chunk: one workgroup's reads
+    // of 40 KB take several rounds of its own outstanding misses.
+    if constexpr (ALIGNED) {
+      if (dfl >= 2u) {
+        constexpr int n = Elems<DT>::n, CHE = Elems<DT>::chunk;
+        const int acc = (int)(dfl & (DEFER_ACC - 1)) - 2;
+        const int cpl = (int)(dfl >> 24) - 1;
+        const int64_t r = request_row0(a, b) + acc;
+        if (cpl >= 0 && cpl < P.C && acc >= 0 && r >= 0 && r < a.rows) {
+          const int64_t lo = (int64_t)cpl * CHE, hi = lo + CHE < a.vocab ? lo + CHE : a.vocab;
+          const uint32_t bytes = (uint32_t)((hi - lo) * (16 / n));
+          const auto rsr = buf_rsrc(row_ptr(a, r) + lo * (16 / n), bytes);
+          const uint32_t nvec = (bytes + 15u) / 16u;
+          const uint32_t part = (nvec + (KF_ROLES - 2)) / (KF_ROLES - 1);
+          const uint32_t v0 = (uint32_t)(role - 1) * part, v1 = v0 + part < nvec ? v0 + part : nvec;
+          uint32_t x = 0u;
+          for (uint32_t v = v0 + threadIdx.x; v < v1; v += FCT) {
+            const uint4 t = buf_load16_cached(rsr, v * 16u, 0u);
+            x ^= t.x ^ t.y ^ t.z ^ t.w;
+          }
+          asm volatile("" ::"v"(x));
+        }
+      }
+    }
+    return;
+  }
   if (dfl == 0u) {
     // the row merge wrote the request's outputs -- if the request has rows (its deferred flag
     // is set by the chunk pass of its own rows; one without is decided here)
@@ -3748,7 +3781,7 @@ extern "C" int dsv_verify(const dsv_verify_args* args, dsv_stream_t stream_) {
     const size_t lds = !P.final_nuc ? 0 : a.logits_dtype == DSV_BF16 ? (size_t)HIST_WORDS * 4 : sizeof(F32NucLds);
     auto go = [&](const void* fn, auto kernel) {
       if (lds) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      hipLaunchKernelGGL(kernel, dim3(a.bs), dim3(FCT), lds, stream, P);
+      hipLaunchKernelGGL(kernel, dim3((unsigned)a.bs * KF_ROLES), dim3(FCT), lds, stream, P);
     };
     if (a.logits_dtype == DSV_BF16) {
       if (P.aligned)
